@@ -1,0 +1,45 @@
+"""Build step for the gfx950 HIP library (libainfer_moe.so, in-tree).
+
+hipcc cross-compiles for gfx950 without a GPU present.  All HIP code is
+compiled with packed-fp32 instruction selection disabled.
+"""
+import os
+import subprocess
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+CSRC = PKG / "csrc"
+LIB = PKG / "libainfer_moe.so"
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+SOURCES = ["moe_api.hip", "moe_route.hip", "moe_expert.hip"]
+FLAGS = [
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-fno-gpu-rdc", "-Wall", "-Wno-unused-function",
+]
+
+
+def build_library(verbose: bool = False) -> Path:
+    """Compile every HIP source into ainfer_amd/libainfer_moe.so."""
+    objs = []
+    for src in SOURCES:
+        obj = CSRC / (src + ".o")
+        cmd = [HIPCC, *[f for f in FLAGS if f != "-shared"], "-c", str(CSRC / src), "-o", str(obj)]
+        _run(cmd, verbose)
+        objs.append(str(obj))
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(LIB), *objs], verbose)
+    return LIB
+
+
+def _run(cmd, verbose):
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"build failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    return r
+
+
+if __name__ == "__main__":
+    print(build_library(verbose=True))

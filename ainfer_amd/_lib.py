@@ -1,0 +1,91 @@
+"""ctypes binding of include/ainfer_moe.h (libainfer_moe.so, built in-tree).
+
+Loading fails loudly: there is no CPU fallback behind this module.
+"""
+import ctypes as C
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libainfer_moe.so"
+
+OK = 0
+ERR_SHAPE, ERR_NULL, ERR_WORKSPACE, ERR_TOKENS, ERR_HIP, ERR_ARG = -1, -2, -3, -4, -5, -6
+SCALE_BF16, SCALE_FP16 = 0, 1
+NORM_PLAIN, NORM_ONE_PLUS = 0, 1
+FILL_BYTES, FILL_BF16_NORMAL, FILL_FP16_ABSNORMAL, FILL_BF16_ABSNORMAL = 0, 1, 2, 3
+MAX_TOKENS = 65536
+
+# every symbol include/ainfer_moe.h declares
+EXPORTS = (
+    "ainfer_moe_strerror", "ainfer_moe_validate", "ainfer_moe_workspace_bytes",
+    "ainfer_moe_forward", "ainfer_moe_block_forward", "ainfer_moe_route",
+    "ainfer_moe_dispatch", "ainfer_moe_rmsnorm", "ainfer_moe_fill",
+    "ainfer_moe_profile_enable", "ainfer_moe_profile_read",
+)
+N_STAGES = 7
+STAGES = ("rmsnorm", "router", "topk", "dispatch", "gate_up", "down", "combine")
+
+
+class Shape(C.Structure):
+    _fields_ = [("hidden", C.c_int32), ("n_experts", C.c_int32), ("top_k", C.c_int32),
+                ("inter", C.c_int32), ("shared_inter", C.c_int32), ("group", C.c_int32),
+                ("scale_dtype", C.c_int32), ("reserved", C.c_int32)]
+
+
+class Weights(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in (
+        "router_w", "router_bias", "shared_gate_w", "w_gate", "s_gate", "w_up", "s_up",
+        "w_down", "s_down", "ws_gate", "ss_gate", "ws_up", "ss_up", "ws_down", "ss_down")]
+
+
+class MoeError(RuntimeError):
+    pass
+
+
+_lib = None
+
+
+def lib():
+    """The loaded library; raises if it was not built."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise MoeError(f"{LIB_PATH} is missing: run __graft_entry__.build() first "
+                           "(there is no fallback path)")
+        L = C.CDLL(str(LIB_PATH))
+        P, I32, SZ, F = C.c_void_p, C.c_int32, C.c_size_t, C.c_float
+        sp, wp = C.POINTER(Shape), C.POINTER(Weights)
+        L.ainfer_moe_strerror.restype = C.c_char_p
+        L.ainfer_moe_strerror.argtypes = [C.c_int]
+        L.ainfer_moe_validate.argtypes = [sp]
+        L.ainfer_moe_workspace_bytes.restype = SZ
+        L.ainfer_moe_workspace_bytes.argtypes = [sp, I32]
+        L.ainfer_moe_forward.argtypes = [sp, wp, P, P, I32, P, SZ, P]
+        L.ainfer_moe_block_forward.argtypes = [sp, wp, P, I32, F, P, P, I32, P, SZ, P]
+        L.ainfer_moe_route.argtypes = [sp, wp, P, I32, P, P, P, P, P, SZ, P]
+        L.ainfer_moe_dispatch.argtypes = [sp, P, I32, P, P, P, P, P, SZ, P]
+        L.ainfer_moe_rmsnorm.argtypes = [P, P, I32, F, P, I32, I32, P]
+        L.ainfer_moe_fill.argtypes = [I32, C.c_uint64, F, SZ, P, P]
+        L.ainfer_moe_profile_enable.argtypes = [I32]
+        L.ainfer_moe_profile_read.argtypes = [C.POINTER(C.c_float), I32, C.POINTER(I32)]
+        for name in EXPORTS:
+            getattr(L, name).restype = getattr(L, name).restype or C.c_int
+        _lib = L
+    return _lib
+
+
+def check(rc):
+    if rc != OK:
+        raise MoeError(f"ainfer_moe status {rc}: {lib().ainfer_moe_strerror(rc).decode()}")
+    return rc
+
+
+def profile_enable(on: bool):
+    check(lib().ainfer_moe_profile_enable(1 if on else 0))
+
+
+def profile_read():
+    """Mean device microseconds per stage since profile_enable(True)."""
+    arr = (C.c_float * N_STAGES)()
+    n = C.c_int32(0)
+    check(lib().ainfer_moe_profile_read(arr, N_STAGES, C.byref(n)))
+    return dict(zip(STAGES, list(arr))), n.value

@@ -1,0 +1,375 @@
+// moe_api.hip - the C ABI of include/ainfer_moe.h: validation, workspace
+// layout and the stage sequence router -> top-k -> dispatch -> gate/up ->
+// down -> combine.  Host code; every device buffer comes from the caller.
+#include <string.h>
+
+#include "moe_common.h"
+#include "moe_internal.h"
+
+namespace {
+
+// ---- profiling: one event per stage boundary, per call ---------------------
+constexpr int NSTAGE = AINFER_MOE_N_STAGES;
+constexpr int PROF_SLOTS = 64;
+struct Prof {
+  bool on = false;
+  bool created = false;
+  hipEvent_t ev[PROF_SLOTS][NSTAGE + 1];
+  bool used[PROF_SLOTS][NSTAGE + 1];
+  int slot = 0, calls = 0;
+  double sum_us[NSTAGE];
+  int cnt[NSTAGE];
+} g_prof;
+
+void prof_flush_slot(int s) {
+  // stage i spans the last recorded event before it to its own end event
+  int prev = -1;
+  for (int i = 0; i <= NSTAGE; ++i) {
+    if (!g_prof.used[s][i]) continue;
+    if (prev >= 0) {
+      hipEventSynchronize(g_prof.ev[s][i]);
+      float ms = 0.f;
+      if (hipEventElapsedTime(&ms, g_prof.ev[s][prev], g_prof.ev[s][i]) == hipSuccess) {
+        g_prof.sum_us[i - 1] += ms * 1000.0;
+        g_prof.cnt[i - 1] += 1;
+      }
+    }
+    prev = i;
+    g_prof.used[s][i] = false;
+  }
+}
+
+struct ProfCall {
+  int s = -1;
+  hipStream_t st;
+  explicit ProfCall(hipStream_t stream) : st(stream) {
+    if (!g_prof.on) return;
+    s = g_prof.slot;
+    g_prof.slot = (g_prof.slot + 1) % PROF_SLOTS;
+    prof_flush_slot(s);  // reuse: collect the slot's previous call first
+    g_prof.calls++;
+  }
+  // mark the end of stage `stage` (index = stage + 1); the call's first
+  // mark is the start event
+  void start() {
+    if (s >= 0) rec(0);
+  }
+  void end(int stage) {
+    if (s >= 0) rec(stage + 1);
+  }
+  void rec(int i) {
+    hipEventRecord(g_prof.ev[s][i], st);
+    g_prof.used[s][i] = true;
+  }
+};
+
+struct Layout {
+  size_t logits, sg_logit, idx, w, sg, xperm, chunk_counts, rank, counts, offsets, perm, inv,
+      tiles, n_tiles, act, act_s, o, h, total;
+};
+
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+int max_tiles_bound(const ainfer_moe_shape &s, int T, int mt) {
+  long tk = (long)T * s.top_k;
+  long routed = tk / mt + (tk < s.n_experts ? tk : s.n_experts);
+  long sh = s.shared_inter > 0 ? (T + mt - 1) / mt : 0;
+  return (int)(routed + sh);
+}
+
+Layout layout_of(const ainfer_moe_shape &s, int Tm) {
+  Layout L;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    size_t o = off;
+    off += align256(bytes);
+    return o;
+  };
+  const size_t T = (size_t)(Tm > 0 ? Tm : 1), E = s.n_experts, k = s.top_k, H = s.hidden;
+  const size_t nchunks = (T + 63) / 64;
+  L.logits = take(T * E * 4);
+  L.sg_logit = take(T * 4);
+  L.idx = take(T * k * 4);
+  L.w = take(T * k * 4);
+  L.sg = take(T * 4);
+  L.xperm = take(T * H * 2);
+  L.chunk_counts = take(nchunks * E * 4);
+  L.rank = take(T * k * 4);
+  L.counts = take(E * 4);
+  L.offsets = take((E + 1) * 4);
+  L.perm = take(T * k * 4);
+  L.inv = take(T * k * 4);
+  L.tiles = take((size_t)max_tiles_bound(s, (int)T, SMALL_MT) * 8);
+  L.n_tiles = take(4);
+  L.act = take(T * k * s.inter * 2);
+  L.act_s = take(T * (size_t)(s.shared_inter > 0 ? s.shared_inter : 1) * 2);
+  L.o = take(T * (k + 1) * H * 4);
+  L.h = take(T * H * 2);
+  L.total = off;
+  return L;
+}
+
+template <typename P>
+P *at(void *ws, size_t off) {
+  return (P *)((char *)ws + off);
+}
+
+int check_ws(const ainfer_moe_shape *s, int T, void *ws, size_t ws_bytes) {
+  if (!ws) return AINFER_ERR_NULL;
+  if (((uintptr_t)ws) & 255) return AINFER_ERR_WORKSPACE;
+  if (ws_bytes < layout_of(*s, T).total) return AINFER_ERR_WORKSPACE;
+  return AINFER_OK;
+}
+
+int check_weights(const ainfer_moe_shape *s, const ainfer_moe_weights *w) {
+  if (!w || !w->router_w || !w->w_gate || !w->s_gate || !w->w_up || !w->s_up || !w->w_down ||
+      !w->s_down)
+    return AINFER_ERR_NULL;
+  if (s->shared_inter > 0 && (!w->ws_gate || !w->ss_gate || !w->ws_up || !w->ss_up ||
+                              !w->ws_down || !w->ss_down))
+    return AINFER_ERR_NULL;
+  return AINFER_OK;
+}
+
+#define HIP_TRY(expr)                              \
+  do {                                             \
+    if ((expr) != hipSuccess) return AINFER_ERR_HIP; \
+  } while (0)
+
+// Router + top-k (+ MFMA-order copy of x when xperm != NULL).
+int do_route(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const void *x, int T,
+             int32_t *idx, float *tw, float *sg, float *logits, float *sg_logit, void *xperm,
+             hipStream_t st) {
+  HIP_TRY(launch_router(x, w->router_w, w->router_bias, w->shared_gate_w, logits, sg_logit,
+                        T, s->hidden, s->n_experts, st));
+  HIP_TRY(launch_topk(logits, sg_logit, w->shared_gate_w != nullptr, x, idx, tw, sg, xperm, T,
+                      s->n_experts, s->top_k, s->hidden, st));
+  return AINFER_OK;
+}
+
+int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const void *x,
+               const void *resid, void *y, int T, void *ws, hipStream_t st,
+               ProfCall *pc) {
+  const Layout L = layout_of(*s, T);
+  const int E = s->n_experts, k = s->top_k, H = s->hidden;
+  const int has_shared = s->shared_inter > 0;
+  HIP_TRY(launch_router(x, w->router_w, w->router_bias, w->shared_gate_w,
+                        at<float>(ws, L.logits), at<float>(ws, L.sg_logit), T, H, E, st));
+  pc->end(1);
+  HIP_TRY(launch_topk(at<float>(ws, L.logits), at<float>(ws, L.sg_logit),
+                      w->shared_gate_w != nullptr, x, at<int32_t>(ws, L.idx), at<float>(ws, L.w),
+                      at<float>(ws, L.sg), at<uint16_t>(ws, L.xperm), T, E, k, H, st));
+  pc->end(2);
+  HIP_TRY(launch_dispatch(at<int32_t>(ws, L.idx), T, k, E, SMALL_MT, has_shared,
+                          at<int32_t>(ws, L.chunk_counts), at<int32_t>(ws, L.rank),
+                          at<int32_t>(ws, L.counts), at<int32_t>(ws, L.offsets),
+                          at<int32_t>(ws, L.perm), at<int32_t>(ws, L.inv), at<int2>(ws, L.tiles),
+                          at<int32_t>(ws, L.n_tiles), st));
+  pc->end(3);
+  ExpertArgs a;
+  memset(&a, 0, sizeof a);
+  a.perm = at<int32_t>(ws, L.perm);
+  a.offsets = at<int32_t>(ws, L.offsets);
+  a.tiles = at<int2>(ws, L.tiles);
+  a.n_tiles = at<int32_t>(ws, L.n_tiles);
+  a.T = T;
+  a.k = k;
+  a.E = E;
+  a.H = H;
+  a.I = s->inter;
+  a.Is = s->shared_inter;
+  const int max_tiles = max_tiles_bound(*s, T, SMALL_MT);
+  // gate/up + SiLU-mul
+  a.w0 = w->w_gate;
+  a.w1 = w->w_up;
+  a.s0 = (const uint16_t *)w->s_gate;
+  a.s1 = (const uint16_t *)w->s_up;
+  a.ws0 = w->ws_gate;
+  a.ws1 = w->ws_up;
+  a.ss0 = (const uint16_t *)w->ss_gate;
+  a.ss1 = (const uint16_t *)w->ss_up;
+  a.a_routed = at<uint16_t>(ws, L.xperm);
+  a.a_shared = at<uint16_t>(ws, L.xperm);
+  a.act = at<uint16_t>(ws, L.act);
+  a.act_s = at<uint16_t>(ws, L.act_s);
+  HIP_TRY(launch_expert_small(0, s->scale_dtype, a, max_tiles, st));
+  pc->end(4);
+  // down
+  a.w0 = w->w_down;
+  a.s0 = (const uint16_t *)w->s_down;
+  a.ws0 = w->ws_down;
+  a.ss0 = (const uint16_t *)w->ss_down;
+  a.w1 = nullptr;
+  a.s1 = nullptr;
+  a.ws1 = nullptr;
+  a.ss1 = nullptr;
+  a.a_routed = at<uint16_t>(ws, L.act);
+  a.a_shared = at<uint16_t>(ws, L.act_s);
+  a.o = at<float>(ws, L.o);
+  HIP_TRY(launch_expert_small(1, s->scale_dtype, a, max_tiles, st));
+  pc->end(5);
+  HIP_TRY(launch_combine(at<float>(ws, L.o), at<int32_t>(ws, L.inv), at<float>(ws, L.w),
+                         at<float>(ws, L.sg), has_shared, resid, y, T, k, H, st));
+  pc->end(6);
+  return AINFER_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *ainfer_moe_strerror(int status) {
+  switch (status) {
+  case AINFER_OK: return "ok";
+  case AINFER_ERR_SHAPE: return "unsupported shape";
+  case AINFER_ERR_NULL: return "required pointer is NULL";
+  case AINFER_ERR_WORKSPACE: return "workspace too small or not 256-byte aligned";
+  case AINFER_ERR_TOKENS: return "token count out of range";
+  case AINFER_ERR_HIP: return "HIP runtime error";
+  case AINFER_ERR_ARG: return "argument out of range";
+  default: return "unknown status";
+  }
+}
+
+int ainfer_moe_validate(const ainfer_moe_shape *s) {
+  if (!s) return AINFER_ERR_NULL;
+  if (s->group != 128 || s->reserved != 0) return AINFER_ERR_SHAPE;
+  if (s->hidden < 128 || s->hidden % 128 || s->hidden > 8192) return AINFER_ERR_SHAPE;
+  if (s->inter < 128 || s->inter % 128 || s->inter > 8192) return AINFER_ERR_SHAPE;
+  if (s->shared_inter < 0 || s->shared_inter % 128 || s->shared_inter > 8192)
+    return AINFER_ERR_SHAPE;
+  if (s->n_experts < 1 || s->n_experts > 1024) return AINFER_ERR_SHAPE;
+  if (s->top_k < 1 || s->top_k > 32 || s->top_k > s->n_experts) return AINFER_ERR_SHAPE;
+  if (s->scale_dtype != AINFER_SCALE_FP16 && s->scale_dtype != AINFER_SCALE_BF16)
+    return AINFER_ERR_SHAPE;
+  return AINFER_OK;
+}
+
+size_t ainfer_moe_workspace_bytes(const ainfer_moe_shape *s, int32_t max_tokens) {
+  if (ainfer_moe_validate(s) != AINFER_OK) return 0;
+  if (max_tokens < 0 || max_tokens > AINFER_MOE_MAX_TOKENS) return 0;
+  return layout_of(*s, max_tokens).total;
+}
+
+int ainfer_moe_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const void *x,
+                       void *y, int32_t T, void *ws, size_t ws_bytes, void *stream) {
+  int rc = ainfer_moe_validate(s);
+  if (rc) return rc;
+  if (T < 0 || T > AINFER_MOE_MAX_TOKENS) return AINFER_ERR_TOKENS;
+  if ((rc = check_weights(s, w))) return rc;
+  if (T == 0) return AINFER_OK;
+  if (!x || !y) return AINFER_ERR_NULL;
+  if ((rc = check_ws(s, T, ws, ws_bytes))) return rc;
+  ProfCall pc((hipStream_t)stream);
+  pc.start();
+  return do_forward(s, w, x, nullptr, y, T, ws, (hipStream_t)stream, &pc);
+}
+
+int ainfer_moe_block_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w,
+                             const void *norm_w, int32_t norm_mode, float eps,
+                             const void *resid_in, void *resid_out, int32_t T, void *ws,
+                             size_t ws_bytes, void *stream) {
+  int rc = ainfer_moe_validate(s);
+  if (rc) return rc;
+  if (T < 0 || T > AINFER_MOE_MAX_TOKENS) return AINFER_ERR_TOKENS;
+  if ((rc = check_weights(s, w))) return rc;
+  if (norm_mode != AINFER_NORM_PLAIN && norm_mode != AINFER_NORM_ONE_PLUS) return AINFER_ERR_ARG;
+  if (!(eps >= 0.0f)) return AINFER_ERR_ARG;
+  if (T == 0) return AINFER_OK;
+  if (!resid_in || !resid_out) return AINFER_ERR_NULL;
+  if ((rc = check_ws(s, T, ws, ws_bytes))) return rc;
+  const Layout L = layout_of(*s, T);
+  hipStream_t st = (hipStream_t)stream;
+  void *h = at<void>(ws, L.h);
+  ProfCall pc(st);
+  pc.start();
+  HIP_TRY(launch_rmsnorm(resid_in, norm_w, norm_mode, eps, h, T, s->hidden, st));
+  pc.end(0);
+  return do_forward(s, w, h, resid_in, resid_out, T, ws, st, &pc);
+}
+
+int ainfer_moe_route(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const void *x,
+                     int32_t T, int32_t *topk_idx, float *topk_w, float *shared_gate,
+                     float *logits, void *ws, size_t ws_bytes, void *stream) {
+  int rc = ainfer_moe_validate(s);
+  if (rc) return rc;
+  if (T < 0 || T > AINFER_MOE_MAX_TOKENS) return AINFER_ERR_TOKENS;
+  if (!w || !w->router_w) return AINFER_ERR_NULL;
+  if (T == 0) return AINFER_OK;
+  if (!x || !topk_idx || !topk_w || !shared_gate) return AINFER_ERR_NULL;
+  if ((rc = check_ws(s, T, ws, ws_bytes))) return rc;
+  const Layout L = layout_of(*s, T);
+  float *lg = logits ? logits : at<float>(ws, L.logits);
+  return do_route(s, w, x, T, topk_idx, topk_w, shared_gate, lg, at<float>(ws, L.sg_logit),
+                  nullptr, (hipStream_t)stream);
+}
+
+int ainfer_moe_dispatch(const ainfer_moe_shape *s, const int32_t *topk_idx, int32_t T,
+                        int32_t *counts, int32_t *offsets, int32_t *perm, int32_t *inv_perm,
+                        void *ws, size_t ws_bytes, void *stream) {
+  int rc = ainfer_moe_validate(s);
+  if (rc) return rc;
+  if (T < 0 || T > AINFER_MOE_MAX_TOKENS) return AINFER_ERR_TOKENS;
+  if (!counts || !offsets) return AINFER_ERR_NULL;
+  if (T > 0 && (!topk_idx || !perm)) return AINFER_ERR_NULL;
+  if ((rc = check_ws(s, T, ws, ws_bytes))) return rc;
+  const Layout L = layout_of(*s, T);
+  HIP_TRY(launch_dispatch(topk_idx, T, s->top_k, s->n_experts, SMALL_MT, s->shared_inter > 0,
+                          at<int32_t>(ws, L.chunk_counts), at<int32_t>(ws, L.rank), counts,
+                          offsets, perm, inv_perm, at<int2>(ws, L.tiles),
+                          at<int32_t>(ws, L.n_tiles), (hipStream_t)stream));
+  return AINFER_OK;
+}
+
+int ainfer_moe_rmsnorm(const void *x, const void *w, int32_t norm_mode, float eps, void *y,
+                       int32_t T, int32_t H, void *stream) {
+  if (T < 0 || T > AINFER_MOE_MAX_TOKENS) return AINFER_ERR_TOKENS;
+  if (H <= 0 || H % 8) return AINFER_ERR_SHAPE;
+  if (norm_mode != AINFER_NORM_PLAIN && norm_mode != AINFER_NORM_ONE_PLUS) return AINFER_ERR_ARG;
+  if (T == 0) return AINFER_OK;
+  if (!x || !y) return AINFER_ERR_NULL;
+  HIP_TRY(launch_rmsnorm(x, w, norm_mode, eps, y, T, H, (hipStream_t)stream));
+  return AINFER_OK;
+}
+
+int ainfer_moe_profile_enable(int32_t enable) {
+  if (enable && !g_prof.created) {
+    for (int i = 0; i < PROF_SLOTS; ++i)
+      for (int j = 0; j <= NSTAGE; ++j) {
+        if (hipEventCreate(&g_prof.ev[i][j]) != hipSuccess) return AINFER_ERR_HIP;
+        g_prof.used[i][j] = false;
+      }
+    g_prof.created = true;
+  }
+  if (enable) {
+    for (int i = 0; i < NSTAGE; ++i) g_prof.sum_us[i] = 0.0, g_prof.cnt[i] = 0;
+    g_prof.calls = 0;
+    g_prof.slot = 0;
+    if (g_prof.created)
+      for (int i = 0; i < PROF_SLOTS; ++i)
+        for (int j = 0; j <= NSTAGE; ++j) g_prof.used[i][j] = false;
+  }
+  g_prof.on = enable != 0;
+  return AINFER_OK;
+}
+
+int ainfer_moe_profile_read(float *stage_us, int32_t n_stages, int32_t *n_calls) {
+  if (!stage_us && n_stages > 0) return AINFER_ERR_NULL;
+  if (g_prof.created)
+    for (int i = 0; i < PROF_SLOTS; ++i) prof_flush_slot(i);
+  for (int i = 0; i < n_stages && i < NSTAGE; ++i)
+    stage_us[i] = g_prof.cnt[i] ? (float)(g_prof.sum_us[i] / g_prof.cnt[i]) : 0.0f;
+  if (n_calls) *n_calls = g_prof.calls;
+  return AINFER_OK;
+}
+
+int ainfer_moe_fill(int32_t kind, uint64_t seed, float std_, size_t n, void *out,
+                    void *stream) {
+  if (kind < AINFER_FILL_BYTES || kind > AINFER_FILL_BF16_ABSNORMAL) return AINFER_ERR_ARG;
+  if (n == 0) return AINFER_OK;
+  if (!out) return AINFER_ERR_NULL;
+  HIP_TRY(launch_fill(kind, seed, std_, n, out, (hipStream_t)stream));
+  return AINFER_OK;
+}
+
+}  // extern "C"

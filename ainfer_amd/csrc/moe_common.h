@@ -1,0 +1,54 @@
+// moe_common.h - device helpers shared by the gfx950 MoE kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/ainfer_moe.h"
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+
+#define WAVE 64
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float((uint32_t)b << 16);
+}
+// round to nearest even, NaN kept quiet
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+__device__ __forceinline__ float fp16_to_f32(uint16_t h) {
+  return (float)__builtin_bit_cast(_Float16, h);
+}
+template <int SD>
+__device__ __forceinline__ float scale_to_f32(uint16_t s) {
+  if constexpr (SD == AINFER_SCALE_FP16)
+    return fp16_to_f32(s);
+  else
+    return bf16_to_f32(s);
+}
+
+__device__ __forceinline__ f32x4 mfma_bf16_16x16x32(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c,
+                                                 0, 0, 0);
+}
+
+// Four packed int4 -> bf16 pairs for one MFMA k-slice.
+// d is a dword of 8 nibbles (k offsets 0..7, low nibble first) already
+// xor'ed with 0x88888888 so each nibble holds q + 8.  Slice j (0..3) takes
+// nibbles j and j+4 into the low/high bf16 halves as 128 + (q + 8): the
+// bf16 pattern 0x43NN with N the nibble is exactly 128 + N.
+__device__ __forceinline__ uint32_t nib_pair_bf16(uint32_t d, int j) {
+  return ((d >> (4 * j)) & 0x000F000Fu) | 0x43004300u;
+}
+
+// Index inside a 32-element block of the MFMA-order ("slice-major")
+// layout: position p = 8*j + e holds natural k = 4*e + j.
+__host__ __device__ __forceinline__ int perm32_pos(int k) {
+  return (k & ~31) | (((k & 3) << 3) | ((k & 31) >> 2));
+}

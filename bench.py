@@ -1,0 +1,251 @@
+#!/usr/bin/env python3
+"""Benchmark of the INT4 MoE layer on one MI355X.
+
+Headline (the JSON line's `value`): config c1 decode, batch 1 -- layer
+microseconds per token (H2048, 512 experts, top-10, I512, + shared expert,
+INT4 g128 fp16 scales).  `details` adds c1 at 4 and 16 tokens and the c2
+prefill (4096 tokens, Zipf(1.1) routing) in tokens/s and % of bf16 MFMA peak.
+
+Inputs are resident in HBM before the timed region.  Decode steps cycle over
+NL distinct layer copies and NX distinct token batches so the weights each
+step reads are not left in the 256 MB MALL by the previous step.  Per-kernel
+device times come from HIP events the library records on the launch stream
+(ainfer_moe_profile_*) in a second pass over the same steps; the headline
+timed region runs without them.
+
+The CPU baseline is the C oracle (oracle/libmoe_oracle.so, `port`) on the
+box's host cores, on a bounded sample of the same decode workload.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, GB/s
+MFMA_BF16_PEAK_TFS = 2500.0  # MI355X dense bf16 MFMA, TFLOP/s
+METRIC = "MoE layer decode us/token + % HBM peak; prefill tokens/s + % MFMA peak"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def unique_experts(layer, x, ws):
+    import torch
+    idx, _, _, _ = layer.route(x, ws)
+    return int(torch.unique(idx).numel())
+
+
+def gateup_bytes(cfg, U):
+    """INT4 nibbles + fp16 scales of gate and up for U routed experts and the
+    shared expert, plus the bf16 tokens read."""
+    per = lambda I: 2 * (cfg.hidden * I // 2 + cfg.hidden * I // 128 * 2)
+    return U * per(cfg.inter) + (per(cfg.shared_inter) if cfg.shared_inter else 0)
+
+
+def run_decode(layers, cfg, T, steps, warmup, NX, stream):
+    import torch
+    from ainfer_amd import _lib as L
+    from ainfer_amd.moe import make_input
+    NL = len(layers)
+    xs = [make_input(cfg, T, tag=1000 + 7 * T + i) for i in range(NX)]
+    ws = layers[0].workspace(T)
+    y = torch.empty(T, cfg.hidden, dtype=torch.bfloat16, device="cuda")
+    for s in range(warmup):
+        layers[s % NL].forward(xs[s % NX], y, ws, stream)
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for s in range(steps):
+        layers[s % NL].forward(xs[s % NX], y, ws, stream)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / steps
+    # profiled pass: per-kernel device times on the launch stream
+    L.profile_enable(True)
+    for s in range(steps):
+        layers[s % NL].forward(xs[s % NX], y, ws, stream)
+    torch.cuda.synchronize()
+    stages, ncalls = L.profile_read()
+    L.profile_enable(False)
+    # routing statistics of the pairs the loop visited
+    pairs = sorted({(s % NL, s % NX) for s in range(steps)})
+    U = sum(unique_experts(layers[l], xs[i], ws) for l, i in pairs) / len(pairs)
+    torch.cuda.synchronize()
+    return ms, stages, U
+
+
+def run_prefill(layer, cfg, T, steps, warmup, stream):
+    import torch
+    from ainfer_amd import _lib as L
+    from ainfer_amd.moe import make_input
+    x = make_input(cfg, T, tag=4242)
+    ws = layer.workspace(T)
+    y = torch.empty(T, cfg.hidden, dtype=torch.bfloat16, device="cuda")
+    for _ in range(warmup):
+        layer.forward(x, y, ws, stream)
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(steps):
+        layer.forward(x, y, ws, stream)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / steps
+    L.profile_enable(True)
+    for _ in range(steps):
+        layer.forward(x, y, ws, stream)
+    torch.cuda.synchronize()
+    stages, _ = L.profile_read()
+    L.profile_enable(False)
+    U = unique_experts(layer, x, ws)
+    return ms, stages, U
+
+
+def cpu_baseline(layer, cfg, T, budget_s):
+    """The C oracle on host cores, bounded to about budget_s seconds."""
+    import numpy as np
+    import torch
+    from oracle import oracle as O
+    from ainfer_amd.moe import make_input
+
+    def host(t):
+        if t is None:
+            return None
+        if t.dtype in (torch.bfloat16, torch.float16):
+            return t.view(torch.int16).cpu().numpy().view(np.uint16)
+        return t.cpu().numpy()
+
+    hl = O.HostLayer(cfg.shape_tuple(), {n: host(t) for n, t in layer.t.items()})
+    threads = max(1, min(os.cpu_count() or 1, 16))
+    xs = [host(make_input(cfg, T, tag=9000 + i)) for i in range(8)]
+    hl.forward(xs[0], T, threads)  # warm
+    times = []
+    t_end = time.perf_counter() + budget_s
+    i = 0
+    while (time.perf_counter() < t_end or len(times) < 3) and len(times) < 2000:
+        t = time.perf_counter()
+        hl.forward(xs[i % len(xs)], T, threads)
+        times.append(time.perf_counter() - t)
+        i += 1
+    times.sort()
+    med = times[len(times) // 2]
+    return {"value": med * 1e6 / T, "unit": "us/token", "cores": threads, "kind": "port",
+            "sample": f"c1 decode T={T}: {len(times)} layer calls of the C oracle "
+                      f"(median), {threads} threads, {len(xs)} distinct inputs"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--layers", type=int, default=8, help="distinct c1 layer copies cycled")
+    ap.add_argument("--prefill-steps", type=int, default=10)
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the expert-parallel sharding plan is described in DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from ainfer_amd.moe import MoeLayer
+    from ainfer_amd.synthetic import CONFIGS, algorithmic_bytes, algorithmic_flops
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    stream = torch.cuda.current_stream()
+    c1 = CONFIGS["c1"]
+    log(f"[bench] allocating {args.layers} c1 layers "
+        f"({args.layers * c1.layer_weight_bytes() / 1e9:.1f} GB)")
+    layers = [MoeLayer(c1, layer=i) for i in range(args.layers)]
+    torch.cuda.synchronize()
+
+    decode = {}
+    for T in (1, 4, 16):
+        log(f"[bench] c1 decode T={T}")
+        ms, st, U = run_decode(layers, c1, T, args.steps, args.warmup, 64, stream)
+        nbytes = algorithmic_bytes(c1, T, round(U))
+        gu_us = st["gate_up"]
+        gu_gbs = gateup_bytes(c1, U) / (gu_us * 1e-6) / 1e9 if gu_us > 0 else 0.0
+        decode[T] = {
+            "us_per_step": ms * 1e3, "us_per_token": ms * 1e3 / T,
+            "unique_experts": U, "alg_bytes": nbytes,
+            "layer_hbm_gbs": nbytes / (ms * 1e-3) / 1e9,
+            "layer_hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "stage_us": {k: round(v, 3) for k, v in st.items()},
+            "gate_up_gbs": gu_gbs,
+        }
+        log(f"[bench]   {json.dumps(decode[T])}")
+
+    prefill = None
+    if not args.no_prefill:
+        del layers
+        torch.cuda.empty_cache()
+        c2 = CONFIGS["c2"]
+        T = 4096
+        log("[bench] c2 prefill T=4096")
+        layer2 = MoeLayer(c2)
+        ms, st, U = run_prefill(layer2, c2, T, args.prefill_steps, 2, stream)
+        fl = algorithmic_flops(c2, T)
+        gu_flops = 2 * T * (c2.top_k + 1) * 2 * c2.hidden * c2.inter
+        prefill = {
+            "tokens_per_s": T / (ms * 1e-3), "ms_per_step": ms, "unique_experts": U,
+            "alg_flops": fl, "layer_tflops": fl / (ms * 1e-3) / 1e12,
+            "layer_mfma_frac": fl / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFS,
+            "stage_us": {k: round(v, 3) for k, v in st.items()},
+            "gate_up_tflops": gu_flops / (st["gate_up"] * 1e-6) / 1e12 if st["gate_up"] else 0,
+        }
+        log(f"[bench]   {json.dumps(prefill)}")
+        layers = [MoeLayer(c1, layer=0)]
+
+    cpu = None
+    if not args.no_cpu:
+        log("[bench] cpu baseline")
+        cpu = cpu_baseline(layers[0], c1, 1, args.cpu_seconds)
+        log(f"[bench]   {json.dumps(cpu)}")
+
+    d1 = decode[1]
+    out = {
+        "metric": METRIC,
+        "value": round(d1["us_per_token"], 3),
+        "unit": "us/token",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": d1["us_per_step"] / 1e3,
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded counter-based generator; random-init INT4 weights)",
+        "config": {"workload": "c1 decode T=1: H2048 E512 top-10 I512 + 1 shared expert "
+                               "(sigmoid gate), INT4 g128 fp16 scales",
+                   "layer_copies": args.layers, "global_batch": 1,
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(d1["gate_up_gbs"], 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(d1["gate_up_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "k_expert_small<fp16, gate/up> (dominant decode kernel)"},
+        "cpu_baseline": cpu,
+        "details": {
+            "layer_hbm_frac_T1": round(d1["layer_hbm_frac"], 4),
+            "decode": {str(T): {k: (round(v, 4) if isinstance(v, float) else v)
+                                for k, v in d.items()} for T, d in decode.items()},
+            "prefill_c2_T4096": prefill,
+        },
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,192 @@
+/*
+ * ainfer_moe.h - C ABI of the MI355X (gfx950) INT4 mixture-of-experts layer.
+ *
+ * Plain C: POD structs, raw device pointers, sizes, an opaque stream handle
+ * (a hipStream_t passed as void*, NULL = the default stream) and int status
+ * codes.  No C++ or torch types cross this boundary.
+ *
+ * Conventions carried over from the reference runtime's operator surface
+ * (tools/decode/decode_l0.cpp):
+ *   - the caller owns every buffer, including the workspace; nothing is
+ *     allocated inside a forward call (decode_l0.cpp:220-295 allocates all
+ *     arenas and scratch once at init);
+ *   - kernels receive raw device pointers into caller-owned weight arenas
+ *     (decode_l0.cpp:494-504, the gemvE lambda);
+ *   - all work is stream-ordered; a call returns after enqueueing
+ *     (decode_l0.cpp:484-493 appends launch + barrier to a list);
+ *   - errors are reported, never fatal: the reference CHECK()s and exits
+ *     (decode_l0.cpp:26-34); this layer returns a negative status instead,
+ *     with the text available from ainfer_moe_strerror().
+ *
+ * Weight format (per tensor, expert-contiguous):
+ *   packed  [rows][K/2] uint8, two signed 4-bit values per byte, low nibble =
+ *           even k, two's complement in [-8, 7]
+ *           (tools/binfer.py:76-102, tools/gemv/gemv.cpp:46-71);
+ *   scales  [rows][K/128] fp16 (or bf16, selected by scale_dtype), one per
+ *           group of 128 consecutive k (docs/binfer_spec.md:79-91).
+ *   dequantised weight w[n][k] = q[n][k] * scale[n][k/128].
+ * Routed expert e: gate/up are [I][H] (rows = I, K = H), down is [H][I]
+ * (rows = H, K = I); expert e's tensor starts at e * rows * K/2 bytes and
+ * its scales at e * rows * K/128 elements.
+ *
+ * Layer semantics (one token t, x_t in bf16):
+ *   logit_e   = dot(x_t, router_w[e]) (+ router_bias[e])     fp32
+ *   top-k     = the k largest logits, equal logits ordered lower index first
+ *               (the tie rule of tools/sample/sampler.h:97-98)
+ *   w_j       = exp(logit_j - logit_max) / sum_{selected} exp(...)
+ *               (= softmax over all E, keep top-k, renormalise)
+ *   g_s       = sigmoid(dot(x_t, shared_gate_w))   (1 when no gate vector)
+ *   expert_e(x) = W_down (silu(W_gate x) * (W_up x))
+ *   y_t       = sum_j w_j * expert_{e_j}(x_t) + g_s * shared(x_t)
+ * Router dot products use one fixed fp32 summation order (the "lane-strided
+ * chunk order": 64 lanes, lane l sums 8-element chunks l, l+64, ...
+ * sequentially with fma, then an xor butterfly over 32,16,8,4,2,1), so
+ * logits, and therefore top-k indices, are bit-identical to the CPU oracle.
+ * The dispatch permutation orders (token, slot) pairs by expert ascending,
+ * then token ascending.
+ */
+#ifndef AINFER_MOE_H
+#define AINFER_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+enum {
+  AINFER_OK = 0,
+  AINFER_ERR_SHAPE = -1,      /* shape fails validation                     */
+  AINFER_ERR_NULL = -2,       /* a required pointer is NULL                 */
+  AINFER_ERR_WORKSPACE = -3,  /* workspace too small or misaligned          */
+  AINFER_ERR_TOKENS = -4,     /* T < 0 or above the supported maximum       */
+  AINFER_ERR_HIP = -5,        /* a HIP runtime call failed                  */
+  AINFER_ERR_ARG = -6         /* another argument is out of range           */
+};
+
+enum { AINFER_SCALE_BF16 = 0, AINFER_SCALE_FP16 = 1 };
+
+/* RMSNorm weight forms: reference RMSNormW uses y = x*inv*(1+w)
+ * (tools/cmdlist/kernels.cpp:73-116); the operator fixture
+ * (reference/operators_t14.npz rmsnorm_*) uses y = x*inv*w. */
+enum { AINFER_NORM_PLAIN = 0, AINFER_NORM_ONE_PLUS = 1 };
+
+/* Largest token count one call accepts (prefill chunk). */
+#define AINFER_MOE_MAX_TOKENS 65536
+
+typedef struct ainfer_moe_shape {
+  int32_t hidden;       /* H, multiple of 128                               */
+  int32_t n_experts;    /* E, 1..1024                                       */
+  int32_t top_k;        /* k, 1..min(E, 32)                                 */
+  int32_t inter;        /* I of each routed expert, multiple of 128         */
+  int32_t shared_inter; /* I of the shared expert, multiple of 128; 0 = none */
+  int32_t group;        /* quantisation group along K; must be 128          */
+  int32_t scale_dtype;  /* AINFER_SCALE_FP16 or AINFER_SCALE_BF16           */
+  int32_t reserved;     /* must be 0                                        */
+} ainfer_moe_shape;
+
+typedef struct ainfer_moe_weights {
+  const void *router_w;      /* [E][H] bf16                                 */
+  const float *router_bias;  /* [E] fp32 added to the logits, or NULL       */
+  const void *shared_gate_w; /* [H] bf16 sigmoid gate of the shared expert,
+                                or NULL (gate = 1)                          */
+  const uint8_t *w_gate;     /* [E][I][H/2]                                 */
+  const void *s_gate;        /* [E][I][H/128]                               */
+  const uint8_t *w_up;       /* [E][I][H/2]                                 */
+  const void *s_up;          /* [E][I][H/128]                               */
+  const uint8_t *w_down;     /* [E][H][I/2]                                 */
+  const void *s_down;        /* [E][H][I/128]                               */
+  const uint8_t *ws_gate;    /* shared expert [Is][H/2] (unused if Is == 0)  */
+  const void *ss_gate;       /* [Is][H/128]                                 */
+  const uint8_t *ws_up;      /* [Is][H/2]                                   */
+  const void *ss_up;         /* [Is][H/128]                                 */
+  const uint8_t *ws_down;    /* [H][Is/2]                                   */
+  const void *ss_down;       /* [H][Is/128]                                 */
+} ainfer_moe_weights;
+
+/* Text for a status code. */
+const char *ainfer_moe_strerror(int status);
+
+/* AINFER_OK when the shape is supported, AINFER_ERR_SHAPE otherwise. */
+int ainfer_moe_validate(const ainfer_moe_shape *shape);
+
+/* Bytes of device workspace one call with up to max_tokens tokens needs
+ * (0 on an invalid shape).  The workspace must be 256-byte aligned. */
+size_t ainfer_moe_workspace_bytes(const ainfer_moe_shape *shape,
+                                  int32_t max_tokens);
+
+/* The whole layer: y[T][H] (bf16) = MoE(x[T][H] bf16).
+ * Replaces the reference MLP sub-sequence decode_l0.cpp:663-674
+ * (xq -> gemvE gate -> gemvE up -> SiluMul -> xq -> gemvE down -> res) with
+ * router -> dispatch -> grouped INT4 expert SwiGLU -> combine + shared. */
+int ainfer_moe_forward(const ainfer_moe_shape *shape,
+                       const ainfer_moe_weights *weights, const void *x,
+                       void *y, int32_t T, void *workspace,
+                       size_t workspace_bytes, void *stream);
+
+/* One decoder-block MLP half with residual, as in decode_l0.cpp:663-674:
+ *   h = RMSNorm(resid_in) (eps, norm_w in norm_mode, NULL = unit weight),
+ *   resid_out = bf16(resid_in + MoE(h)).   resid_out may alias resid_in. */
+int ainfer_moe_block_forward(const ainfer_moe_shape *shape,
+                             const ainfer_moe_weights *weights,
+                             const void *norm_w, int32_t norm_mode, float eps,
+                             const void *resid_in, void *resid_out, int32_t T,
+                             void *workspace, size_t workspace_bytes,
+                             void *stream);
+
+/* ---- stage-level entries (the pieces forward composes) ----------------- */
+
+/* Router: topk_idx[T][k] int32, topk_w[T][k] fp32 (renormalised, slot 0 =
+ * largest logit), shared_gate[T] fp32 (sigmoid, or 1), and optionally
+ * logits[T][E] fp32 (NULL to skip).  Workspace as for forward. */
+int ainfer_moe_route(const ainfer_moe_shape *shape,
+                     const ainfer_moe_weights *weights, const void *x,
+                     int32_t T, int32_t *topk_idx, float *topk_w,
+                     float *shared_gate, float *logits, void *workspace,
+                     size_t workspace_bytes, void *stream);
+
+/* Dispatch: counts[E], offsets[E+1] (exclusive scan of counts),
+ * perm[T*k] (position p holds t*k + j, expert-contiguous, token ascending
+ * within an expert) and inv_perm[T*k] (inverse of perm). */
+int ainfer_moe_dispatch(const ainfer_moe_shape *shape,
+                        const int32_t *topk_idx, int32_t T, int32_t *counts,
+                        int32_t *offsets, int32_t *perm, int32_t *inv_perm,
+                        void *workspace, size_t workspace_bytes, void *stream);
+
+/* RMSNorm over rows: y[T][H] bf16 = x * 1/sqrt(mean(x^2) + eps) * w
+ * (norm_mode PLAIN) or * (1 + w) (ONE_PLUS); w bf16 [H] or NULL (unit).
+ * Sum of squares in fp64, as RMSNormW (kernels.cpp:73-116). */
+int ainfer_moe_rmsnorm(const void *x, const void *w, int32_t norm_mode,
+                       float eps, void *y, int32_t T, int32_t H, void *stream);
+
+/* ---- synthetic data (counter-based, bit-identical to the CPU oracle) --- */
+enum {
+  AINFER_FILL_BYTES = 0,      /* uniform random bytes (packed int4 weights)  */
+  AINFER_FILL_BF16_NORMAL = 1,/* bf16 of std * n,  n ~ standardised sum of
+                                 8 uniform bytes (Irwin-Hall approximation of
+                                 N(0,1))                                     */
+  AINFER_FILL_FP16_ABSNORMAL = 2, /* fp16 of |std * n|                       */
+  AINFER_FILL_BF16_ABSNORMAL = 3  /* bf16 of |std * n|                       */
+};
+/* Fill n elements (bytes for FILL_BYTES, 2-byte values otherwise) of out.
+ * Element i is a function of (seed, i) only. */
+int ainfer_moe_fill(int32_t kind, uint64_t seed, float std_, size_t n,
+                    void *out, void *stream);
+
+/* ---- per-stage timing (the AINFER_PROFILE instrumentation of
+ * tools/decode/decode_l0.cpp:705,714-725,870-884, with device events) -----
+ * While enabled, forward/block_forward record a HIP event on the caller's
+ * stream before and after every kernel.  ainfer_moe_profile_read()
+ * waits for them and returns, per stage, the mean device time in
+ * microseconds over the calls since enable, and the call count.  Stages:
+ * 0 rmsnorm, 1 router, 2 top-k, 3 dispatch, 4 gate/up, 5 down, 6 combine. */
+#define AINFER_MOE_N_STAGES 7
+int ainfer_moe_profile_enable(int32_t enable);
+int ainfer_moe_profile_read(float *stage_us, int32_t n_stages, int32_t *n_calls);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* AINFER_MOE_H */

@@ -1,0 +1,250 @@
+"""Pins the CPU oracle (oracle/moe_oracle.c) before anything is compared
+against it: reference fixtures, hand-derived goldens, closed forms,
+invariants and brute force.  CPU only."""
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+GOLD = Path(__file__).resolve().parent / "golden"
+
+
+# ---------------------------------------------------------------- bits -----
+def test_bf16_roundtrip_matches_binfer_formula(oracle):
+    # tools/binfer.py:68-73 formula, computed in numpy independently
+    rng = np.random.default_rng(0)
+    f = rng.standard_normal(4096).astype(np.float32) * 10
+    u = f.view(np.uint32).astype(np.uint64)
+    want = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    got = np.array([oracle.lib().mo_f32_to_bf16(float(v)) for v in f[:512]], np.uint16)
+    assert np.array_equal(got, want[:512])
+    assert np.array_equal(oracle.f32_to_bf16(f), want)
+
+
+def test_fp16_conversion_matches_ieee(oracle):
+    rng = np.random.default_rng(1)
+    vals = np.concatenate([
+        rng.standard_normal(2000).astype(np.float32) * 0.02,
+        (rng.standard_normal(500) * 1e-6).astype(np.float32),       # subnormal range
+        (rng.standard_normal(200) * 1e-8).astype(np.float32),
+        np.array([65504, 65519.99, 65520, 1e9, 0.0, -0.0, 2 ** -25, 2 ** -24, 3 * 2 ** -26],
+                 np.float32)])
+    want = vals.astype(np.float16).view(np.uint16)
+    L = oracle.lib()
+    got = np.array([L.mo_f32_to_fp16(float(v)) for v in vals], np.uint16)
+    assert np.array_equal(got, want)
+    back = np.array([L.mo_fp16_to_f32(int(h)) for h in want], np.float32)
+    assert np.array_equal(back, want.view(np.float16).astype(np.float32))
+
+
+# ---------------------------------------------------------------- fill -----
+def test_splitmix_known_answer(oracle):
+    # splitmix64 seeded with 0: first outputs are the published test values
+    L = oracle.lib()
+    assert L.mo_rnd(0, 0) == 0xE220A8397B1DCDAF
+    assert L.mo_rnd(0, 1) == 0x6E789E6AA1B965F4
+    from ainfer_amd.synthetic import splitmix
+    for s in (0, 1, 12345, 2 ** 63 + 7):
+        for i in (0, 1, 99, 10 ** 9):
+            assert splitmix(s, i) == L.mo_rnd(s, i)
+
+
+def test_fill_bytes_and_normal_moments(oracle):
+    b = oracle.fill(oracle.FILL_BYTES, 7, 0.0, 1 << 20)
+    r0 = oracle.lib().mo_rnd(7, 0)
+    assert list(b[:8]) == [(r0 >> (8 * i)) & 0xFF for i in range(8)]
+    nib = np.concatenate([b & 0xF, b >> 4]).astype(np.int64)
+    assert abs(nib.mean() - 7.5) < 0.02          # uniform nibbles: int4 uniform in [-8, 7]
+    x = oracle.bf16_to_f32(oracle.fill(oracle.FILL_BF16_NORMAL, 3, 1.0, 1 << 20))
+    assert abs(x.mean()) < 5e-3 and abs(x.std() - 1.0) < 5e-3
+    assert np.abs(x).max() < 4.9                  # Irwin-Hall(8) support is +-4.88
+    s = oracle.fill(oracle.FILL_FP16_ABSNORMAL, 4, 0.02, 1 << 18).view(np.float16).astype(np.float64)
+    assert (s >= 0).all() and abs(s.mean() - 0.02 * math.sqrt(2 / math.pi)) < 2e-4
+
+
+# ---------------------------------------------------------------- int4 -----
+def test_dequant_hand_golden(oracle):
+    # one row, K = 128: byte i packs k = 2i (low nibble) and k = 2i+1 (high)
+    packed = np.zeros(64, np.uint8)
+    packed[0] = 0x8F      # k0 = 0xF -> -1, k1 = 0x8 -> -8
+    packed[1] = 0x70      # k2 = 0, k3 = 7
+    packed[2] = 0x19      # k4 = 9 -> -7, k5 = 1
+    scale = np.array([0x3C00], np.uint16)   # fp16 1.0
+    out = oracle.dequant(packed, scale, oracle.SCALE_FP16, 1, 128)[0]
+    assert list(out[:6]) == [-1, -8, 0, 7, -7, 1] and not out[6:].any()
+    scale2 = np.array([0x4000], np.uint16)  # bf16 2.0
+    out2 = oracle.dequant(packed, scale2, oracle.SCALE_BF16, 1, 128)[0]
+    assert list(out2[:6]) == [-2, -16, 0, 14, -14, 2]
+
+
+def test_quantize_hand_golden_and_roundtrip(oracle):
+    w = np.zeros((2, 128), np.float32)
+    w[0, 0] = 7.0                 # amax 7 -> scale 1
+    w[0, 1] = -7.0
+    w[0, 2] = 2.5                 # rint half-even -> 2
+    w[0, 3] = 3.5                 # -> 4
+    w[0, 4] = -0.5                # -> -0
+    # row 1: all zero -> scale 1, q = 0
+    packed, scales = oracle.quantize(w)
+    assert scales[0] == 0x3F80 and scales[1] == 0x3F80          # bf16 1.0
+    deq = oracle.dequant(packed, scales, oracle.SCALE_BF16, 2, 128)
+    assert list(deq[0, :5]) == [7, -7, 2, 4, 0] and not deq[1].any()
+    rng = np.random.default_rng(2)
+    w = rng.standard_normal((8, 256)).astype(np.float32)
+    packed, scales = oracle.quantize(w)
+    deq = oracle.dequant(packed, scales, oracle.SCALE_BF16, 8, 256)
+    # half a step per element, plus |q| <= 8 times the bf16 rounding of the scale
+    step = oracle.bf16_to_f32(scales).repeat(128).reshape(8, 256)
+    assert (np.abs(deq - w) <= (0.5 + 8 * 2.0 ** -8) * step).all()
+    packed2, _ = oracle.quantize(deq)
+    assert np.array_equal(packed2, packed)  # dequantised values requantise to themselves
+
+
+# ---------------------------------------------------------------- pointwise -
+def test_silu_mul_matches_reference_fixture(oracle):
+    d = np.load(GOLD / "operators_t14_subset.npz", allow_pickle=False)
+    got = oracle.silu_mul(d["g"], d["u"])
+    np.testing.assert_allclose(got, d["silu_gate_out"], rtol=1e-12, atol=1e-14)
+
+
+def test_rmsnorm_matches_reference_fixture_plain_form(oracle):
+    d = np.load(GOLD / "operators_t14_subset.npz", allow_pickle=False)
+    x, w, want = d["rmsnorm_in"], d["rmsnorm_w"], d["rmsnorm_out"]
+    got = oracle.rmsnorm_f32(x, w, oracle.NORM_PLAIN)
+    np.testing.assert_allclose(got, want, rtol=2e-6, atol=2e-6)
+    wrong = oracle.rmsnorm_f32(x, w, oracle.NORM_ONE_PLUS)
+    assert np.abs(wrong - want).max() > 0.1     # the (1+w) form is not the fixture's
+
+
+# ---------------------------------------------------------------- router ---
+def test_router_dot_exact_cases(oracle):
+    one = np.full(2048, 0x3F80, np.uint16)     # bf16 1.0
+    assert oracle.router_dot(one, one) == 2048.0
+    x = np.zeros(1024, np.uint16)
+    x[5] = 0x4000                               # 2.0
+    w = np.zeros(1024, np.uint16)
+    w[5] = 0xC040                               # -3.0
+    assert oracle.router_dot(x, w) == -6.0
+
+
+def test_router_dot_within_fp32_bound(oracle):
+    rng = np.random.default_rng(3)
+    for H in (128, 1024, 2048, 4096):
+        x = oracle.f32_to_bf16(rng.standard_normal(H).astype(np.float32))
+        w = oracle.f32_to_bf16((rng.standard_normal(H) * 0.02).astype(np.float32))
+        xf, wf = oracle.bf16_to_f32(x).astype(np.float64), oracle.bf16_to_f32(w).astype(np.float64)
+        exact = float(np.dot(xf, wf))
+        bound = (H + 64) * 2.0 ** -24 * float(np.abs(xf * wf).sum())
+        assert abs(oracle.router_dot(x, w) - exact) <= bound
+
+
+def _brute_topk(lg, k):
+    # value descending, index ascending (tools/sample/sampler.h:97-98)
+    order = sorted(range(len(lg)), key=lambda e: (-lg[e], e))
+    return order[:k]
+
+
+def test_topk_brute_force_with_ties(oracle):
+    rng = np.random.default_rng(4)
+    for E, k in ((8, 2), (64, 8), (512, 10), (1000, 32)):
+        lg = (rng.integers(-4, 4, size=(16, E)) * 0.25).astype(np.float32)  # heavy ties
+        idx, w = oracle.topk(lg, k)
+        for t in range(16):
+            assert list(idx[t]) == _brute_topk(list(lg[t]), k)
+            p = np.exp(lg[t, idx[t]].astype(np.float64) - lg[t, idx[t][0]])
+            np.testing.assert_allclose(w[t], p / p.sum(), rtol=1e-6)
+        np.testing.assert_allclose(w.sum(1), 1.0, rtol=1e-6)
+
+
+def test_topk_reference_sampler_fixtures(oracle):
+    # tools/sample/sample.cpp:128-160 argmax fixtures, restated: spike, all
+    # equal -> first index, double max -> smaller index
+    V = 4096
+    cases = []
+    v = np.full(V, -1.0, np.float32); v[0] = 5.0; cases.append((v, 0))
+    v = np.full(V, -2.0, np.float32); v[V - 1] = 7.0; cases.append((v, V - 1))
+    v = np.full(V, 0.25, np.float32); cases.append((v, 0))
+    v = np.full(V, -3.0, np.float32); v[999] = 4.0; v[1999] = 4.0; cases.append((v, 999))
+    for v, want in cases:
+        idx, _ = oracle.topk(v[None, :], 1)
+        assert idx[0, 0] == want
+    v = np.full(V, 0.25, np.float32)
+    idx, w = oracle.topk(v[None, :], 10)
+    assert list(idx[0]) == list(range(10)) and np.allclose(w, 0.1)
+
+
+def test_topk_against_reference_sampler_build(oracle):
+    if oracle.ref_sampler() is None:
+        pytest.skip("oracle/_ref not built (needs /root/reference at build time)")
+    rng = np.random.default_rng(5)
+    for trial in range(50):
+        E, k = (512, 10) if trial % 2 else (64, 8)
+        lg = (rng.standard_normal(E) * (0.25 if trial % 3 else 1.0)).astype(np.float32)
+        if trial % 5 == 0:
+            lg = np.round(lg * 4) / 4                     # ties
+        idx, w = oracle.topk(lg[None, :], k)
+        probs = oracle.ref_topk_probs(lg, k)
+        support = np.nonzero(probs)[0]
+        assert sorted(support.tolist()) == sorted(idx[0].tolist())
+        np.testing.assert_allclose(probs[idx[0]], w[0], rtol=2e-6)
+
+
+# ---------------------------------------------------------------- dispatch -
+def test_dispatch_invariants_and_brute_force(oracle):
+    rng = np.random.default_rng(6)
+    for T, E, k in ((1, 8, 2), (5, 8, 3), (130, 64, 8), (1000, 512, 10)):
+        idx = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32)
+        counts, offsets, perm, inv = oracle.dispatch(idx, E)
+        assert counts.sum() == T * k and offsets[0] == 0 and offsets[-1] == T * k
+        assert np.array_equal(np.diff(offsets), counts)
+        assert np.array_equal(np.sort(perm), np.arange(T * k))
+        assert np.array_equal(inv[perm], np.arange(T * k))
+        # brute force: stable sort of (expert, token) keys
+        flat = idx.reshape(-1)
+        want = sorted(range(T * k), key=lambda i: (flat[i], i // k))
+        assert list(perm) == want
+
+
+# ---------------------------------------------------------------- layer ----
+def _tiny_layer(oracle, E=8, k=2, H=256, I=128, Is=128, gate=True, zipf=0.0):
+    from ainfer_amd.synthetic import MoeConfig
+    cfg = MoeConfig("tiny", H, E, k, I, Is, (3,), zipf=zipf, shared_gate=gate)
+    return cfg, oracle.HostLayer.synthetic(cfg)
+
+
+@pytest.mark.parametrize("Is,gate", [(128, True), (256, False), (0, False)])
+def test_forward_matches_dense_fp64(oracle, Is, gate):
+    cfg, hl = _tiny_layer(oracle, Is=Is, gate=gate)
+    T = 5
+    x = oracle.fill(oracle.FILL_BF16_NORMAL, 99, 1.0, T * cfg.hidden).reshape(T, cfg.hidden)
+    idx, w, sg, lg = hl.route(x, T)
+    if not gate:
+        assert (sg == 1.0).all()
+    y = hl.forward(x, T)
+    dense = hl.forward_dense(x, T, idx, w, sg)
+    np.testing.assert_allclose(y, dense, rtol=1e-5, atol=1e-5 * np.abs(dense).max())
+
+
+def test_router_logits_bias_added(oracle):
+    cfg, hl = _tiny_layer(oracle, E=16, k=4, zipf=1.1)
+    T = 4
+    x = oracle.fill(oracle.FILL_BF16_NORMAL, 5, 1.0, T * cfg.hidden).reshape(T, cfg.hidden)
+    _, _, _, lg = hl.route(x, T)
+    H = cfg.hidden
+    rw = hl.a["router_w"].reshape(cfg.n_experts, H)
+    for t in range(T):
+        for e in range(cfg.n_experts):
+            want = np.float32(oracle.router_dot(x[t], rw[e])) + hl.a["router_bias"][e]
+            assert lg[t, e] == np.float32(want)
+
+
+def test_block_forward_is_norm_then_moe_plus_residual(oracle):
+    cfg, hl = _tiny_layer(oracle)
+    T, H = 3, cfg.hidden
+    r = oracle.fill(oracle.FILL_BF16_NORMAL, 11, 3.0, T * H).reshape(T, H)
+    out = hl.block_forward(r, T)
+    h = oracle.rmsnorm_bf16(r, None, oracle.NORM_PLAIN)
+    y = hl.forward(h, T)
+    want = oracle.f32_to_bf16(oracle.bf16_to_f32(r) + y)
+    assert np.array_equal(out, want)
