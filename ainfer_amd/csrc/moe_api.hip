@@ -65,7 +65,7 @@ struct ProfCall {
 
 struct Layout {
   size_t logits, sg_logit, idx, w, sg, xperm, chunk_counts, rank, counts, offsets, perm, inv,
-      tiles, n_tiles, act, act_s, o, h, total;
+      ptok, tiles, n_tiles, cnt, ticket, act, act_s, o, h, total;
 };
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -99,8 +99,11 @@ Layout layout_of(const ainfer_moe_shape &s, int Tm) {
   L.offsets = take((E + 1) * 4);
   L.perm = take(T * k * 4);
   L.inv = take(T * k * 4);
-  L.tiles = take((size_t)max_tiles_bound(s, (int)T, SMALL_MT) * 8);
+  L.ptok = take(T * k * 4);
+  L.tiles = take((size_t)max_tiles_bound(s, (int)T, SMALL_MT) * 16);
   L.n_tiles = take(4);
+  L.cnt = take(T * (H / 16) * 4);
+  L.ticket = take(4);
   L.act = take(T * k * s.inter * 2);
   L.act_s = take(T * (size_t)(s.shared_inter > 0 ? s.shared_inter : 1) * 2);
   L.o = take(T * (k + 1) * H * 4);
@@ -136,15 +139,19 @@ int check_weights(const ainfer_moe_shape *s, const ainfer_moe_weights *w) {
     if ((expr) != hipSuccess) return AINFER_ERR_HIP; \
   } while (0)
 
-// Router + top-k (+ MFMA-order copy of x when xperm != NULL).
-int do_route(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const void *x, int T,
-             int32_t *idx, float *tw, float *sg, float *logits, float *sg_logit, void *xperm,
-             hipStream_t st) {
-  HIP_TRY(launch_router(x, w->router_w, w->router_bias, w->shared_gate_w, logits, sg_logit,
-                        T, s->hidden, s->n_experts, st));
-  HIP_TRY(launch_topk(logits, sg_logit, w->shared_gate_w != nullptr, x, idx, tw, sg, xperm, T,
-                      s->n_experts, s->top_k, s->hidden, st));
-  return AINFER_OK;
+DispatchOut dispatch_out(const ainfer_moe_shape *s, const Layout &L, void *ws, int T) {
+  DispatchOut d;
+  d.counts = at<int32_t>(ws, L.counts);
+  d.offsets = at<int32_t>(ws, L.offsets);
+  d.perm = at<int32_t>(ws, L.perm);
+  d.inv = at<int32_t>(ws, L.inv);
+  d.ptok = at<int32_t>(ws, L.ptok);
+  d.tiles = at<int4>(ws, L.tiles);
+  d.n_tiles = at<int32_t>(ws, L.n_tiles);
+  d.cnt = at<int32_t>(ws, L.cnt);
+  d.n_cnt = T * (s->hidden / 16);
+  d.ticket = at<int32_t>(ws, L.ticket);
+  return d;
 }
 
 int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const void *x,
@@ -153,25 +160,33 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
   const Layout L = layout_of(*s, T);
   const int E = s->n_experts, k = s->top_k, H = s->hidden;
   const int has_shared = s->shared_inter > 0;
+  const bool fused = T <= FUSED_DISPATCH_MAX_T;
+  DispatchOut d = dispatch_out(s, L, ws, T);
   HIP_TRY(launch_router(x, w->router_w, w->router_bias, w->shared_gate_w,
-                        at<float>(ws, L.logits), at<float>(ws, L.sg_logit), T, H, E, st));
+                        at<float>(ws, L.logits), at<float>(ws, L.sg_logit),
+                        fused ? d.ticket : nullptr, T, H, E, st));
   pc->end(1);
   HIP_TRY(launch_topk(at<float>(ws, L.logits), at<float>(ws, L.sg_logit),
                       w->shared_gate_w != nullptr, x, at<int32_t>(ws, L.idx), at<float>(ws, L.w),
-                      at<float>(ws, L.sg), at<uint16_t>(ws, L.xperm), T, E, k, H, st));
+                      at<float>(ws, L.sg), at<uint16_t>(ws, L.xperm), T, E, k, H, has_shared,
+                      fused ? &d : nullptr, st));
   pc->end(2);
-  HIP_TRY(launch_dispatch(at<int32_t>(ws, L.idx), T, k, E, SMALL_MT, has_shared,
-                          at<int32_t>(ws, L.chunk_counts), at<int32_t>(ws, L.rank),
-                          at<int32_t>(ws, L.counts), at<int32_t>(ws, L.offsets),
-                          at<int32_t>(ws, L.perm), at<int32_t>(ws, L.inv), at<int2>(ws, L.tiles),
-                          at<int32_t>(ws, L.n_tiles), st));
+  if (!fused)
+    HIP_TRY(launch_dispatch(at<int32_t>(ws, L.idx), T, k, E, SMALL_MT, has_shared,
+                            at<int32_t>(ws, L.chunk_counts), at<int32_t>(ws, L.rank), d, st));
   pc->end(3);
   ExpertArgs a;
   memset(&a, 0, sizeof a);
-  a.perm = at<int32_t>(ws, L.perm);
-  a.offsets = at<int32_t>(ws, L.offsets);
-  a.tiles = at<int2>(ws, L.tiles);
-  a.n_tiles = at<int32_t>(ws, L.n_tiles);
+  a.ptok = d.ptok;
+  a.tiles = d.tiles;
+  a.n_tiles = d.n_tiles;
+  a.cnt = d.cnt;
+  a.inv = d.inv;
+  a.topk_w = at<float>(ws, L.w);
+  a.sg = at<float>(ws, L.sg);
+  a.resid = (const uint16_t *)resid;
+  a.y = (uint16_t *)y;
+  a.has_shared = has_shared;
   a.T = T;
   a.k = k;
   a.E = E;
@@ -192,9 +207,9 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
   a.a_shared = at<uint16_t>(ws, L.xperm);
   a.act = at<uint16_t>(ws, L.act);
   a.act_s = at<uint16_t>(ws, L.act_s);
-  HIP_TRY(launch_expert_small(0, s->scale_dtype, a, max_tiles, st));
+  HIP_TRY(launch_expert_stream(0, s->scale_dtype, a, max_tiles, st));
   pc->end(4);
-  // down
+  // down + combine
   a.w0 = w->w_down;
   a.s0 = (const uint16_t *)w->s_down;
   a.ws0 = w->ws_down;
@@ -206,11 +221,8 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
   a.a_routed = at<uint16_t>(ws, L.act);
   a.a_shared = at<uint16_t>(ws, L.act_s);
   a.o = at<float>(ws, L.o);
-  HIP_TRY(launch_expert_small(1, s->scale_dtype, a, max_tiles, st));
+  HIP_TRY(launch_expert_stream(1, s->scale_dtype, a, max_tiles, st));
   pc->end(5);
-  HIP_TRY(launch_combine(at<float>(ws, L.o), at<int32_t>(ws, L.inv), at<float>(ws, L.w),
-                         at<float>(ws, L.sg), has_shared, resid, y, T, k, H, st));
-  pc->end(6);
   return AINFER_OK;
 }
 
@@ -299,9 +311,14 @@ int ainfer_moe_route(const ainfer_moe_shape *s, const ainfer_moe_weights *w, con
   if (!x || !topk_idx || !topk_w || !shared_gate) return AINFER_ERR_NULL;
   if ((rc = check_ws(s, T, ws, ws_bytes))) return rc;
   const Layout L = layout_of(*s, T);
+  hipStream_t st = (hipStream_t)stream;
   float *lg = logits ? logits : at<float>(ws, L.logits);
-  return do_route(s, w, x, T, topk_idx, topk_w, shared_gate, lg, at<float>(ws, L.sg_logit),
-                  nullptr, (hipStream_t)stream);
+  HIP_TRY(launch_router(x, w->router_w, w->router_bias, w->shared_gate_w, lg,
+                        at<float>(ws, L.sg_logit), nullptr, T, s->hidden, s->n_experts, st));
+  HIP_TRY(launch_topk(lg, at<float>(ws, L.sg_logit), w->shared_gate_w != nullptr, x, topk_idx,
+                      topk_w, shared_gate, nullptr, T, s->n_experts, s->top_k, s->hidden,
+                      s->shared_inter > 0, nullptr, st));
+  return AINFER_OK;
 }
 
 int ainfer_moe_dispatch(const ainfer_moe_shape *s, const int32_t *topk_idx, int32_t T,
@@ -314,10 +331,15 @@ int ainfer_moe_dispatch(const ainfer_moe_shape *s, const int32_t *topk_idx, int3
   if (T > 0 && (!topk_idx || !perm)) return AINFER_ERR_NULL;
   if ((rc = check_ws(s, T, ws, ws_bytes))) return rc;
   const Layout L = layout_of(*s, T);
+  DispatchOut d;
+  memset(&d, 0, sizeof d);
+  d.counts = counts;
+  d.offsets = offsets;
+  d.perm = perm;
+  d.inv = inv_perm;
   HIP_TRY(launch_dispatch(topk_idx, T, s->top_k, s->n_experts, SMALL_MT, s->shared_inter > 0,
-                          at<int32_t>(ws, L.chunk_counts), at<int32_t>(ws, L.rank), counts,
-                          offsets, perm, inv_perm, at<int2>(ws, L.tiles),
-                          at<int32_t>(ws, L.n_tiles), (hipStream_t)stream));
+                          at<int32_t>(ws, L.chunk_counts), at<int32_t>(ws, L.rank), d,
+                          (hipStream_t)stream));
   return AINFER_OK;
 }
 

@@ -52,3 +52,29 @@ __device__ __forceinline__ uint32_t nib_pair_bf16(uint32_t d, int j) {
 __host__ __device__ __forceinline__ int perm32_pos(int k) {
   return (k & ~31) | (((k & 3) << 3) | ((k & 31) >> 2));
 }
+
+// ---- wave64 reductions on the DPP path (no LDS round trip) ---------------
+// Inclusive reduction up to lane 63 (quad_perm xor1/xor2, row half-mirror,
+// row mirror, row_bcast15, row_bcast31), then a readlane broadcast.
+template <typename Op>
+__device__ __forceinline__ uint32_t wave_reduce_u32(uint32_t v, Op op) {
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0xB1, 0xF, 0xF, false));
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x4E, 0xF, 0xF, false));
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x141, 0xF, 0xF, false));
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x140, 0xF, 0xF, false));
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x142, 0xA, 0xF, false));
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x143, 0xC, 0xF, false));
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  return wave_reduce_u32(v, [](uint32_t a, uint32_t b) { return a > b ? a : b; });
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+  return wave_reduce_u32(v, [](uint32_t a, uint32_t b) { return a < b ? a : b; });
+}
+// fp32 -> uint32 whose unsigned order is the float order (-0 < +0 aside)
+__device__ __forceinline__ uint32_t ordered_key(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) == 0u) u = 0u;  // -0 ties with +0, as in float compares
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}

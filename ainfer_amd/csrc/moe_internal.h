@@ -17,33 +17,57 @@ struct ExpertArgs {
   uint16_t *act;              // MODE 0 out: [Tk][I] bf16, MFMA order
   uint16_t *act_s;            // MODE 0 out: [T][Is]
   float *o;                   // MODE 1 out: [Tk + T][H] fp32
-  const int32_t *perm;        // dispatch permutation
-  const int32_t *offsets;     // [E+1]
-  const int2 *tiles;          // (expert, first row) list
+  const int32_t *ptok;        // token of each dispatch position
+  const int4 *tiles;          // (expert, first position, rows, first row)
   const int32_t *n_tiles;
+  // MODE 1 combine
+  int32_t *cnt;               // [T][n_slabs] arrival counters (zeroed by dispatch)
+  const int32_t *inv;         // [T*k] dispatch position of (t, j)
+  const float *topk_w;        // [T][k]
+  const float *sg;            // [T] shared gate
+  const uint16_t *resid;      // [T][H] bf16 residual or NULL
+  uint16_t *y;                // [T][H] bf16 out
+  int has_shared;
   int T, k, E, H, I, Is;
+  int WK, WR, n_slabs;        // set by the launcher
+};
+
+// Outputs of the dispatch stage.  tiles: (expert, first position, rows,
+// first row within the expert); shared-expert tiles carry expert id E and a
+// token base.  ptok[pos] = token of dispatch position pos.  cnt[n_cnt] are
+// the combine arrival counters, zeroed by the dispatch.  ticket is the
+// last-block counter of the fused top-k + dispatch launch.
+struct DispatchOut {
+  int32_t *counts, *offsets, *perm, *inv, *ptok;
+  int4 *tiles;
+  int32_t *n_tiles;
+  int32_t *cnt;
+  int n_cnt;
+  int32_t *ticket;
 };
 
 hipError_t launch_fill(int kind, uint64_t seed, float std_, size_t n, void *out,
                        hipStream_t s);
 hipError_t launch_rmsnorm(const void *x, const void *w, int mode, float eps, void *y,
                           int T, int H, hipStream_t s);
+// ticket (may be NULL) is zeroed for the fused top-k + dispatch launch
 hipError_t launch_router(const void *x, const void *rw, const float *bias, const void *gw,
-                         float *logits, float *sg_logit, int T, int H, int E,
+                         float *logits, float *sg_logit, int32_t *ticket, int T, int H, int E,
                          hipStream_t s);
+// fused != NULL (T <= 64 only): the last block also runs the dispatch.
 hipError_t launch_topk(const float *logits, const float *sg_logit, int has_gate,
                        const void *x, int32_t *idx, float *w, float *sg, void *xperm, int T,
-                       int E, int k, int H, hipStream_t s);
+                       int E, int k, int H, int has_shared, const DispatchOut *fused,
+                       hipStream_t s);
 hipError_t launch_dispatch(const int32_t *idx, int T, int k, int E, int mt, int has_shared,
-                           int32_t *chunk_counts, int32_t *rank, int32_t *counts,
-                           int32_t *offsets, int32_t *perm, int32_t *inv, int2 *tiles,
-                           int32_t *n_tiles, hipStream_t s);
-hipError_t launch_combine(const float *o, const int32_t *inv, const float *w, const float *sg,
-                          int has_shared, const void *resid, void *y, int T, int k, int H,
-                          hipStream_t s);
-// mode 0: gate/up + SiLU-mul; mode 1: down.  max_tiles bounds the tile list.
-hipError_t launch_expert_small(int mode, int scale_dtype, const ExpertArgs &a, int max_tiles,
-                               hipStream_t s);
+                           int32_t *chunk_counts, int32_t *rank, const DispatchOut &ds,
+                           hipStream_t s);
+// mode 0: gate/up + SiLU-mul; mode 1: down + combine.  max_tiles bounds
+// the tile list.
+hipError_t launch_expert_stream(int mode, int scale_dtype, ExpertArgs a, int max_tiles,
+                                hipStream_t s);
 
 // tile height of the small-M expert kernels
 constexpr int SMALL_MT = 16;
+// largest T routed by the fused top-k + dispatch launch
+constexpr int FUSED_DISPATCH_MAX_T = 64;
