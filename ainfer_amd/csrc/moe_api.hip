@@ -180,13 +180,6 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
   a.ptok = d.ptok;
   a.tiles = d.tiles;
   a.n_tiles = d.n_tiles;
-  a.cnt = d.cnt;
-  a.inv = d.inv;
-  a.topk_w = at<float>(ws, L.w);
-  a.sg = at<float>(ws, L.sg);
-  a.resid = (const uint16_t *)resid;
-  a.y = (uint16_t *)y;
-  a.has_shared = has_shared;
   a.T = T;
   a.k = k;
   a.E = E;
@@ -194,6 +187,7 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
   a.I = s->inter;
   a.Is = s->shared_inter;
   const int max_tiles = max_tiles_bound(*s, T, SMALL_MT);
+  const int kbw = 4;  // measured best at T = 1, 4, 16 (k-groups per wave)
   // gate/up + SiLU-mul
   a.w0 = w->w_gate;
   a.w1 = w->w_up;
@@ -207,7 +201,7 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
   a.a_shared = at<uint16_t>(ws, L.xperm);
   a.act = at<uint16_t>(ws, L.act);
   a.act_s = at<uint16_t>(ws, L.act_s);
-  HIP_TRY(launch_expert_stream(0, s->scale_dtype, a, max_tiles, st));
+  HIP_TRY(launch_expert_stream(0, s->scale_dtype, a, max_tiles, kbw, st));
   pc->end(4);
   // down + combine
   a.w0 = w->w_down;
@@ -221,8 +215,11 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
   a.a_routed = at<uint16_t>(ws, L.act);
   a.a_shared = at<uint16_t>(ws, L.act_s);
   a.o = at<float>(ws, L.o);
-  HIP_TRY(launch_expert_stream(1, s->scale_dtype, a, max_tiles, st));
+  HIP_TRY(launch_expert_stream(1, s->scale_dtype, a, max_tiles, kbw, st));
   pc->end(5);
+  HIP_TRY(launch_combine(at<float>(ws, L.o), d.inv, at<float>(ws, L.w), at<float>(ws, L.sg),
+                         has_shared, resid, y, T, k, H, st));
+  pc->end(6);
   return AINFER_OK;
 }
 
@@ -254,6 +251,10 @@ int ainfer_moe_validate(const ainfer_moe_shape *s) {
   if (s->top_k < 1 || s->top_k > 32 || s->top_k > s->n_experts) return AINFER_ERR_SHAPE;
   if (s->scale_dtype != AINFER_SCALE_FP16 && s->scale_dtype != AINFER_SCALE_BF16)
     return AINFER_ERR_SHAPE;
+  int kbw, wk, wr;
+  for (int mode = 0; mode < 2; ++mode)
+    if (!expert_geometry(mode, s->hidden, s->inter, s->shared_inter, 1, &kbw, &wk, &wr))
+      return AINFER_ERR_SHAPE;
   return AINFER_OK;
 }
 

@@ -78,3 +78,13 @@ __device__ __forceinline__ uint32_t ordered_key(float f) {
   if ((u & 0x7FFFFFFFu) == 0u) u = 0u;  // -0 ties with +0, as in float compares
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
+
+// ---- buffer loads: lanes whose offset is past num_records read 0 ---------
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+__device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+constexpr uint32_t BUF_OOB = 0x80000000u;

@@ -20,14 +20,6 @@ struct ExpertArgs {
   const int32_t *ptok;        // token of each dispatch position
   const int4 *tiles;          // (expert, first position, rows, first row)
   const int32_t *n_tiles;
-  // MODE 1 combine
-  int32_t *cnt;               // [T][n_slabs] arrival counters (zeroed by dispatch)
-  const int32_t *inv;         // [T*k] dispatch position of (t, j)
-  const float *topk_w;        // [T][k]
-  const float *sg;            // [T] shared gate
-  const uint16_t *resid;      // [T][H] bf16 residual or NULL
-  uint16_t *y;                // [T][H] bf16 out
-  int has_shared;
   int T, k, E, H, I, Is;
   int WK, WR, n_slabs;        // set by the launcher
 };
@@ -62,10 +54,17 @@ hipError_t launch_topk(const float *logits, const float *sg_logit, int has_gate,
 hipError_t launch_dispatch(const int32_t *idx, int T, int k, int E, int mt, int has_shared,
                            int32_t *chunk_counts, int32_t *rank, const DispatchOut &ds,
                            hipStream_t s);
-// mode 0: gate/up + SiLU-mul; mode 1: down + combine.  max_tiles bounds
+hipError_t launch_combine(const float *o, const int32_t *inv, const float *w, const float *sg,
+                          int has_shared, const void *resid, void *y, int T, int k, int H,
+                          hipStream_t s);
+// false when the shape has no wave geometry (more than 8 waves along K)
+bool expert_geometry(int mode, int H, int I, int Is, int pref_kbw, int *KBW, int *WK,
+                     int *WR);
+// mode 0: gate/up + SiLU-mul; mode 1: down.  max_tiles bounds
 // the tile list.
+// pref_kbw: preferred 128-wide k-groups per wave (1, 2 or 4).
 hipError_t launch_expert_stream(int mode, int scale_dtype, ExpertArgs a, int max_tiles,
-                                hipStream_t s);
+                                int pref_kbw, hipStream_t s);
 
 // tile height of the small-M expert kernels
 constexpr int SMALL_MT = 16;

@@ -510,3 +510,63 @@ hipError_t launch_dispatch(const int32_t *idx, int T, int k, int E, int mt, int 
   return hipGetLastError();
 }
 
+
+// ---------------------------------------------------------------------------
+// Combine: y[t] = sum_j w[t][j] * o[inv[t*k+j]] + g_s[t] * o[T*k + t]
+// (+ residual), in slot order with fp32 fma, bf16 out.  One thread per 4
+// columns.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_combine(const float *__restrict__ o,
+                                                 const int32_t *__restrict__ inv,
+                                                 const float *__restrict__ w,
+                                                 const float *__restrict__ sg, int has_shared,
+                                                 const uint16_t *__restrict__ resid,
+                                                 uint16_t *__restrict__ y, int T, int k, int H) {
+  const int per_tok = H >> 2;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= T * per_tok) return;
+  const int t = i / per_tok, h0 = (i % per_tok) * 4;
+  int pos[32];
+  float wj[32];
+#pragma unroll
+  for (int j = 0; j < 32; ++j)
+    if (j < k) {
+      pos[j] = inv[(size_t)t * k + j];
+      wj[j] = w[(size_t)t * k + j];
+    }
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < 32; ++j)
+    if (j < k) {
+      const f32x4 v = *(const f32x4 *)(o + (size_t)pos[j] * H + h0);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc[q] = __builtin_fmaf(wj[j], v[q], acc[q]);
+    }
+  if (has_shared) {
+    const float g = sg[t];
+    const f32x4 v = *(const f32x4 *)(o + ((size_t)T * k + t) * H + h0);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) acc[q] = __builtin_fmaf(g, v[q], acc[q]);
+  }
+  if (resid) {
+    const uint2 r = *(const uint2 *)(resid + (size_t)t * H + h0);
+    acc[0] += __uint_as_float(r.x << 16);
+    acc[1] += __uint_as_float(r.x & 0xFFFF0000u);
+    acc[2] += __uint_as_float(r.y << 16);
+    acc[3] += __uint_as_float(r.y & 0xFFFF0000u);
+  }
+  uint2 out;
+  out.x = (uint32_t)f32_to_bf16(acc[0]) | ((uint32_t)f32_to_bf16(acc[1]) << 16);
+  out.y = (uint32_t)f32_to_bf16(acc[2]) | ((uint32_t)f32_to_bf16(acc[3]) << 16);
+  *(uint2 *)(y + (size_t)t * H + h0) = out;
+}
+
+hipError_t launch_combine(const float *o, const int32_t *inv, const float *w, const float *sg,
+                          int has_shared, const void *resid, void *y, int T, int k, int H,
+                          hipStream_t s) {
+  if (T == 0) return hipSuccess;
+  const int n = T * (H / 4);
+  k_combine<<<(n + 255) / 256, 256, 0, s>>>(o, inv, w, sg, has_shared, (const uint16_t *)resid,
+                                            (uint16_t *)y, T, k, H);
+  return hipGetLastError();
+}

@@ -182,7 +182,7 @@ int ainfer_moe_fill(int32_t kind, uint64_t seed, float std_, size_t n,
  * waits for them and returns, per stage, the mean device time in
  * microseconds over the calls since enable, and the call count.  Stages:
  * 0 rmsnorm, 1 router, 2 top-k (+ dispatch when T <= 64), 3 dispatch,
- * 4 gate/up, 5 down (+ combine), 6 reserved. */
+ * 4 gate/up, 5 down, 6 combine. */
 #define AINFER_MOE_N_STAGES 7
 int ainfer_moe_profile_enable(int32_t enable);
 int ainfer_moe_profile_read(float *stage_us, int32_t n_stages, int32_t *n_calls);
