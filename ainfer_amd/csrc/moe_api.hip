@@ -65,7 +65,7 @@ struct ProfCall {
 
 struct Layout {
   size_t logits, sg_logit, idx, w, sg, xperm, chunk_counts, rank, counts, offsets, perm, inv,
-      ptok, tiles, n_tiles, cnt, ticket, act, act_s, o, h, total;
+      ptok, tiles, n_tiles, cnt, ticket, act, act_s, o, h, wnorm, total;
 };
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -108,6 +108,7 @@ Layout layout_of(const ainfer_moe_shape &s, int Tm) {
   L.act_s = take(T * (size_t)(s.shared_inter > 0 ? s.shared_inter : 1) * 2);
   L.o = take(T * (k + 1) * H * 4);
   L.h = take(T * H * 2);
+  L.wnorm = take(E * 4);
   L.total = off;
   return L;
 }
@@ -162,14 +163,11 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
   const int has_shared = s->shared_inter > 0;
   const bool fused = T <= FUSED_DISPATCH_MAX_T;
   DispatchOut d = dispatch_out(s, L, ws, T);
-  HIP_TRY(launch_router(x, w->router_w, w->router_bias, w->shared_gate_w,
-                        at<float>(ws, L.logits), at<float>(ws, L.sg_logit),
-                        fused ? d.ticket : nullptr, T, H, E, st));
-  pc->end(1);
-  HIP_TRY(launch_topk(at<float>(ws, L.logits), at<float>(ws, L.sg_logit),
-                      w->shared_gate_w != nullptr, x, at<int32_t>(ws, L.idx), at<float>(ws, L.w),
-                      at<float>(ws, L.sg), at<uint16_t>(ws, L.xperm), T, E, k, H, has_shared,
-                      fused ? &d : nullptr, st));
+  HIP_TRY(launch_router_fast(x, w->router_w, w->router_bias, w->shared_gate_w,
+                             at<float>(ws, L.logits), at<float>(ws, L.wnorm),
+                             at<int32_t>(ws, L.idx), at<float>(ws, L.w), at<float>(ws, L.sg),
+                             at<uint16_t>(ws, L.xperm), T, H, E, k, has_shared,
+                             fused ? &d : nullptr, st));
   pc->end(2);
   if (!fused)
     HIP_TRY(launch_dispatch(at<int32_t>(ws, L.idx), T, k, E, SMALL_MT, has_shared,
@@ -251,6 +249,7 @@ int ainfer_moe_validate(const ainfer_moe_shape *s) {
   if (s->top_k < 1 || s->top_k > 32 || s->top_k > s->n_experts) return AINFER_ERR_SHAPE;
   if (s->scale_dtype != AINFER_SCALE_FP16 && s->scale_dtype != AINFER_SCALE_BF16)
     return AINFER_ERR_SHAPE;
+  if (!router_supported(s->hidden, s->n_experts)) return AINFER_ERR_SHAPE;
   int kbw, wk, wr;
   for (int mode = 0; mode < 2; ++mode)
     if (!expert_geometry(mode, s->hidden, s->inter, s->shared_inter, 1, &kbw, &wk, &wr))
@@ -313,12 +312,14 @@ int ainfer_moe_route(const ainfer_moe_shape *s, const ainfer_moe_weights *w, con
   if ((rc = check_ws(s, T, ws, ws_bytes))) return rc;
   const Layout L = layout_of(*s, T);
   hipStream_t st = (hipStream_t)stream;
-  float *lg = logits ? logits : at<float>(ws, L.logits);
-  HIP_TRY(launch_router(x, w->router_w, w->router_bias, w->shared_gate_w, lg,
-                        at<float>(ws, L.sg_logit), nullptr, T, s->hidden, s->n_experts, st));
-  HIP_TRY(launch_topk(lg, at<float>(ws, L.sg_logit), w->shared_gate_w != nullptr, x, topk_idx,
-                      topk_w, shared_gate, nullptr, T, s->n_experts, s->top_k, s->hidden,
-                      s->shared_inter > 0, nullptr, st));
+  HIP_TRY(launch_router_fast(x, w->router_w, w->router_bias, w->shared_gate_w,
+                             at<float>(ws, L.logits), at<float>(ws, L.wnorm), topk_idx, topk_w,
+                             shared_gate, nullptr, T, s->hidden, s->n_experts, s->top_k,
+                             s->shared_inter > 0, nullptr, st));
+  // the full canonical logits, on request (lane-strided chunk order, VALU)
+  if (logits)
+    HIP_TRY(launch_router(x, w->router_w, w->router_bias, w->shared_gate_w, logits,
+                          at<float>(ws, L.sg_logit), nullptr, T, s->hidden, s->n_experts, st));
   return AINFER_OK;
 }
 

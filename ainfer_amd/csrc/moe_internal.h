@@ -46,11 +46,15 @@ hipError_t launch_rmsnorm(const void *x, const void *w, int mode, float eps, voi
 hipError_t launch_router(const void *x, const void *rw, const float *bias, const void *gw,
                          float *logits, float *sg_logit, int32_t *ticket, int T, int H, int E,
                          hipStream_t s);
-// fused != NULL (T <= 64 only): the last block also runs the dispatch.
-hipError_t launch_topk(const float *logits, const float *sg_logit, int has_gate,
-                       const void *x, int32_t *idx, float *w, float *sg, void *xperm, int T,
-                       int E, int k, int H, int has_shared, const DispatchOut *fused,
-                       hipStream_t s);
+// Router: approximate MFMA logits -> exact candidate refine -> top-k,
+// weights, shared gate, MFMA-order copy of x.  fused != NULL (T <= 64 only):
+// the last block also runs the dispatch.  approx [T][E] and wnorm [E] are
+// scratch.
+bool router_supported(int H, int E);
+hipError_t launch_router_fast(const void *x, const void *rw, const float *bias, const void *gw,
+                              float *approx, float *wnorm, int32_t *idx, float *w, float *sg,
+                              void *xperm, int T, int H, int E, int k, int has_shared,
+                              const DispatchOut *fused, hipStream_t s);
 hipError_t launch_dispatch(const int32_t *idx, int T, int k, int E, int mt, int has_shared,
                            int32_t *chunk_counts, int32_t *rank, const DispatchOut &ds,
                            hipStream_t s);

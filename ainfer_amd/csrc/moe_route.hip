@@ -201,177 +201,6 @@ __global__ __launch_bounds__(256) void k_router_logits(const uint16_t *__restric
   }
 }
 
-// ---------------------------------------------------------------------------
-// Top-k + weights + shared gate + the MFMA-order copy of x.  One wave per
-// token.  Lane l holds logits l, l+64, ...; each of the k rounds takes the
-// lane-local best (strict >, ascending index), then a wave max of the
-// order-preserving key and a wave min of the index among lanes holding that
-// key (value descending, index ascending: the CPU oracle's rule).
-//
-// With `ds` set (T <= 64), the last block to finish also runs the dispatch:
-// per-expert 64-bit token masks in LDS (order-free atomic OR), counts, an
-// exclusive scan, the tile list, perm / inv / ptok, and it zeroes the
-// combine arrival counters.
-// ---------------------------------------------------------------------------
-constexpr int TOPK_MAXV = 16;  // E <= 1024
-
-__device__ void dispatch_small_block(const int32_t *__restrict__ idx, int T, int k, int E,
-                                     int has_shared, const DispatchOut &ds);
-
-__global__ __launch_bounds__(256) void k_topk(const float *__restrict__ logits,
-                                              const float *__restrict__ sg_logit,
-                                              int has_gate, const uint16_t *__restrict__ x,
-                                              int32_t *__restrict__ topk_idx,
-                                              float *__restrict__ topk_w,
-                                              float *__restrict__ sgate,
-                                              uint16_t *__restrict__ xperm, int T, int E,
-                                              int k, int H, int has_shared, DispatchOut ds,
-                                              int fused) {
-  const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  if (t < T) {
-    const float *lr = logits + (size_t)t * E;
-    uint32_t key[TOPK_MAXV];
-#pragma unroll
-    for (int i = 0; i < TOPK_MAXV; ++i) {
-      int e = lane + 64 * i;
-      key[i] = e < E ? ordered_key(lr[e]) : 0u;  // 0: below every finite key
-    }
-    uint32_t taken = 0;
-    int seli = 0;
-    for (int j = 0; j < k; ++j) {
-      uint32_t bk = 0;
-      int bi = 0x7FFFFFFF;
-#pragma unroll
-      for (int i = 0; i < TOPK_MAXV; ++i) {
-        const int e = lane + 64 * i;
-        if (e < E && !(taken & (1u << i)) && (bi == 0x7FFFFFFF || key[i] > bk)) {
-          bk = key[i];
-          bi = e;
-        }
-      }
-      const uint32_t wk = wave_max_u32(bk);
-      const int wi = (int)wave_min_u32(bk == wk ? (uint32_t)bi : 0xFFFFFFFFu);
-      if ((wi & 63) == lane) taken |= 1u << (wi >> 6);
-      if (lane == j) seli = wi;
-    }
-    // weights: exp(l_j - l_0) / sum_j, sum in slot order
-    const float lmax = lr[__builtin_amdgcn_readfirstlane(seli)];
-    const float p = lane < k ? expf(lr[seli] - lmax) : 0.0f;
-    float sum = 0.0f;
-    for (int j = 0; j < k; ++j) sum += __shfl(p, j, 64);
-    if (lane < k) {
-      topk_idx[(size_t)t * k + lane] = seli;
-      topk_w[(size_t)t * k + lane] = p / sum;
-    }
-    if (lane == 0) sgate[t] = has_gate ? 1.0f / (1.0f + expf(-sg_logit[t])) : 1.0f;
-    // MFMA-order copy: 32-element blocks, position 8*j+e <- k = 4*e+j
-    if (xperm) {
-      const uint16_t *xr = x + (size_t)t * H;
-      uint16_t *xo = xperm + (size_t)t * H;
-      for (int b = lane; b < (H >> 5); b += 64) {
-        const u32x4 *src = (const u32x4 *)(xr + b * 32);
-        u32x4 s0 = src[0], s1 = src[1], s2 = src[2], s3 = src[3];
-        uint32_t in[16] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3],
-                           s2[0], s2[1], s2[2], s2[3], s3[0], s3[1], s3[2], s3[3]};
-        uint32_t out[16];
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-          for (int e2 = 0; e2 < 4; ++e2) {
-            // positions 8j+2e2 and 8j+2e2+1 hold k = 8*e2+j and 8*e2+4+j
-            int ka = 8 * e2 + j, kb = ka + 4;
-            uint32_t lo = (in[ka >> 1] >> (16 * (ka & 1))) & 0xFFFFu;
-            uint32_t hi = (in[kb >> 1] >> (16 * (kb & 1))) & 0xFFFFu;
-            out[4 * j + e2] = lo | (hi << 16);
-          }
-        u32x4 *dst = (u32x4 *)(xo + b * 32);
-        dst[0] = u32x4{out[0], out[1], out[2], out[3]};
-        dst[1] = u32x4{out[4], out[5], out[6], out[7]};
-        dst[2] = u32x4{out[8], out[9], out[10], out[11]};
-        dst[3] = u32x4{out[12], out[13], out[14], out[15]};
-      }
-    }
-  }
-  if (!fused) return;
-  // ---- last block runs the dispatch -------------------------------------
-  __shared__ int is_last;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    __threadfence();
-    const int ticket = atomicAdd(ds.ticket, 1);
-    is_last = ticket == (int)gridDim.x - 1;
-  }
-  __syncthreads();
-  if (!is_last) return;
-  __threadfence();
-  if (threadIdx.x == 0) atomicExch(ds.ticket, 0);
-  dispatch_small_block(topk_idx, T, k, E, has_shared, ds);
-}
-
-// 256 threads, T <= 64.
-__device__ void dispatch_small_block(const int32_t *__restrict__ idx, int T, int k, int E,
-                                     int has_shared, const DispatchOut &ds) {
-  __shared__ unsigned long long mask[1024];
-  __shared__ int scan_c[256], scan_t[256];
-  __shared__ int off_lds[1024];
-  const int tid = threadIdx.x;
-  for (int e = tid; e < E; e += 256) mask[e] = 0ull;
-  __syncthreads();
-  for (int i = tid; i < T * k; i += 256)
-    atomicOr(&mask[__builtin_nontemporal_load(idx + i)], 1ull << (i / k));
-  __syncthreads();
-  // per-thread contiguous expert range [e0, e0 + per)
-  const int per = (E + 255) / 256;
-  const int e0 = tid * per;
-  int c_loc = 0, t_loc = 0;
-  for (int e = e0; e < e0 + per && e < E; ++e) {
-    const int c = __popcll(mask[e]);
-    c_loc += c;
-    t_loc += (c + SMALL_MT - 1) / SMALL_MT;
-  }
-  scan_c[tid] = c_loc;
-  scan_t[tid] = t_loc;
-  __syncthreads();
-  for (int off = 1; off < 256; off <<= 1) {
-    const int a = tid >= off ? scan_c[tid - off] : 0;
-    const int b = tid >= off ? scan_t[tid - off] : 0;
-    __syncthreads();
-    scan_c[tid] += a;
-    scan_t[tid] += b;
-    __syncthreads();
-  }
-  int off_e = scan_c[tid] - c_loc, tile = scan_t[tid] - t_loc;
-  for (int e = e0; e < e0 + per && e < E; ++e) {
-    const int c = __popcll(mask[e]);
-    ds.counts[e] = c;
-    ds.offsets[e] = off_e;
-    off_lds[e] = off_e;
-    for (int m0 = 0; m0 < c; m0 += SMALL_MT)
-      ds.tiles[tile++] = make_int4(e, off_e + m0, min(SMALL_MT, c - m0), m0);
-    off_e += c;
-  }
-  const int routed_tiles = scan_t[255];
-  if (tid == 0) ds.offsets[E] = scan_c[255];
-  const int nsh = has_shared ? (T + SMALL_MT - 1) / SMALL_MT : 0;
-  if (tid < nsh)
-    ds.tiles[routed_tiles + tid] =
-        make_int4(E, tid * SMALL_MT, min(SMALL_MT, T - tid * SMALL_MT), tid * SMALL_MT);
-  if (tid == 0) *ds.n_tiles = routed_tiles + nsh;
-  __syncthreads();
-  // placement: rank of token t among the tokens of expert e
-  for (int i = tid; i < T * k; i += 256) {
-    const int t = i / k;
-    const int e = __builtin_nontemporal_load(idx + i);
-    const unsigned long long below = t == 0 ? 0ull : ((~0ull) >> (64 - t));
-    const int pos = off_lds[e] + __popcll(mask[e] & below);
-    ds.perm[pos] = i;
-    ds.inv[i] = pos;
-    ds.ptok[pos] = t;
-  }
-  for (int i = tid; i < ds.n_cnt; i += 256) ds.cnt[i] = 0;
-}
-
 hipError_t launch_router(const void *x, const void *rw, const float *bias, const void *gw,
                          float *logits, float *sg_logit, int32_t *ticket, int T, int H, int E,
                          hipStream_t s) {
@@ -380,20 +209,6 @@ hipError_t launch_router(const void *x, const void *rw, const float *bias, const
   k_router_logits<<<(rows + 3) / 4, 256, 0, s>>>((const uint16_t *)x, (const uint16_t *)rw,
                                                  bias, (const uint16_t *)gw, logits,
                                                  sg_logit, ticket, T, H, E);
-  return hipGetLastError();
-}
-
-hipError_t launch_topk(const float *logits, const float *sg_logit, int has_gate,
-                       const void *x, int32_t *idx, float *w, float *sg, void *xperm, int T,
-                       int E, int k, int H, int has_shared, const DispatchOut *fused,
-                       hipStream_t s) {
-  if (T == 0) return hipSuccess;
-  DispatchOut ds;
-  memset(&ds, 0, sizeof ds);
-  if (fused) ds = *fused;
-  k_topk<<<(T + 3) / 4, 256, 0, s>>>(logits, sg_logit, has_gate, (const uint16_t *)x, idx, w,
-                                     sg, (uint16_t *)xperm, T, E, k, H, has_shared, ds,
-                                     fused ? 1 : 0);
   return hipGetLastError();
 }
 

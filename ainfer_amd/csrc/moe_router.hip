@@ -1,0 +1,392 @@
+// moe_router.hip - router for gfx950: MFMA logits, exact candidate refine,
+// top-k, renormalised weights, sigmoid shared gate.
+//
+// The top-k must equal, bit for bit, the top-k of the fp32 logits computed in
+// the lane-strided chunk order (include/ainfer_moe.h).  Computing that order
+// for all E experts is a latency-bound VALU job, so the router runs in two
+// kernels:
+//
+//  k_router_mfma: approximate logits on bf16 MFMA (products exact, fp32
+//    accumulation in the hardware's order) plus the 2-norm of every router
+//    weight row.
+//  k_select: one wave per token.  With L_k the k-th largest approximate
+//    logit and d >= |approx - exact| + |canonical - exact| for every expert,
+//    any expert whose canonical logit can reach the canonical top-k has
+//    approx >= L_k - 2d (the top-k experts by approx all have canonical >=
+//    L_k - d).  Those candidates are recomputed in the canonical order and
+//    the top-k is taken among them: the result equals the top-k over all E
+//    canonical logits.  d is a rigorous fp32 summation bound: for n products
+//    accumulated with one rounding each (to nearest or toward zero),
+//    |error| <= n * 2^-23 * sum|x_i w_i| <= n * 2^-23 * ||x|| * ||w_e||
+//    (Cauchy-Schwarz), taken for both paths, plus margins for the bias
+//    addition and for denormal flushing.  When many logits tie, every expert
+//    becomes a candidate and the same code recomputes all of them.
+//
+// The dispatch for T <= 64 runs in k_select's last block (dispatch_small_block,
+// moe_dispatch.h).
+#include <string.h>
+
+#include "moe_common.h"
+#include "moe_dispatch.h"
+#include "moe_internal.h"
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// Approximate logits.  Block = NW waves over one (16-expert, 16*MS-token)
+// tile; wave w takes k-slice [w*H/NW, (w+1)*H/NW) in 32-wide MFMA steps.
+// Lane l: expert row l%16, k offset 8*(l/16) inside each step (A and B use
+// the same k mapping, so both operands load 16 contiguous bytes).
+// ---------------------------------------------------------------------------
+template <int MS>
+__global__ __launch_bounds__(1024) void k_router_mfma(const uint16_t *__restrict__ x,
+                                                      const uint16_t *__restrict__ rw,
+                                                      const float *__restrict__ bias,
+                                                      float *__restrict__ approx,
+                                                      float *__restrict__ wnorm,
+                                                      int32_t *__restrict__ ticket, int T, int H,
+                                                      int E, int NW) {
+  extern __shared__ float red[];  // [NW][MS*256] partial logits, then [NW][16] norms
+  // the last-block counter of the following k_select launch starts at 0
+  if (ticket && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *ticket = 0;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int n = lane & 15, q = lane >> 4;
+  const int e0 = blockIdx.x * 16, t0 = blockIdx.y * 16 * MS;
+  const int e = min(e0 + n, E - 1);
+  const int steps = H / (32 * NW);  // 32-wide k-steps of this wave
+  const int kbase = wave * steps * 32;
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint32_t)T * (uint32_t)H * 2u);
+  f32x4 acc[MS];
+#pragma unroll
+  for (int ms = 0; ms < MS; ++ms) acc[ms] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float ss = 0.0f;
+  const uint16_t *wrow = rw + (size_t)e * H + kbase + 8 * q;
+  uint32_t xoff[MS];
+#pragma unroll
+  for (int ms = 0; ms < MS; ++ms) {
+    const int t = t0 + 16 * ms + n;
+    xoff[ms] = t < T ? ((uint32_t)t * (uint32_t)H + (uint32_t)(kbase + 8 * q)) * 2u : BUF_OOB;
+  }
+  for (int s0 = 0; s0 < steps; s0 += 4) {
+    u32x4 wv[4], xv[MS][4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int ss_ = min(s0 + s, steps - 1);
+      wv[s] = *(const u32x4 *)(wrow + 32 * ss_);
+#pragma unroll
+      for (int ms = 0; ms < MS; ++ms)
+        xv[ms][s] = buf_load16(xr, xoff[ms] == BUF_OOB ? BUF_OOB : xoff[ms] + 64u * ss_);
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      if (s0 + s < steps) {
+#pragma unroll
+        for (int ms = 0; ms < MS; ++ms) acc[ms] = mfma_bf16_16x16x32(xv[ms][s], wv[s], acc[ms]);
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const float lo = __uint_as_float(wv[s][d] << 16), hi = __uint_as_float(wv[s][d] & 0xFFFF0000u);
+          ss = __builtin_fmaf(lo, lo, ss);
+          ss = __builtin_fmaf(hi, hi, ss);
+        }
+      }
+    }
+  }
+  // partial logits: lane (q, n) holds tokens 4q+r of each m-subtile, expert n
+#pragma unroll
+  for (int ms = 0; ms < MS; ++ms)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[wave * (MS * 256) + ms * 256 + (4 * q + r) * 16 + n] = acc[ms][r];
+  ss += __shfl_xor(ss, 16, 64);
+  ss += __shfl_xor(ss, 32, 64);
+  float *nred = red + NW * MS * 256;
+  if (q == 0) nred[wave * 16 + n] = ss;
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < MS * 256; idx += blockDim.x) {
+    const int ms = idx >> 8, cell = idx & 255;
+    const int t = t0 + 16 * ms + (cell >> 4), ee = e0 + (cell & 15);
+    if (t >= T || ee >= E) continue;
+    float v = 0.0f;
+    for (int w = 0; w < NW; ++w) v += red[w * (MS * 256) + idx];
+    approx[(size_t)t * E + ee] = bias ? v + bias[ee] : v;
+  }
+  if (blockIdx.y == 0 && threadIdx.x < 16 && e0 + (int)threadIdx.x < E) {
+    float v = 0.0f;
+    for (int w = 0; w < NW; ++w) v += nred[w * 16 + threadIdx.x];
+    wnorm[e0 + threadIdx.x] = sqrtf(v);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// canonical dot: x in registers (lane l holds chunks l, l+64, ...), one
+// router row w; sequential fma in chunk order, then the xor butterfly.
+// ---------------------------------------------------------------------------
+template <int CH>
+__device__ __forceinline__ float canon_dot(const u32x4 (&xc)[CH], const uint16_t *w, int lane,
+                                           int nch) {
+  u32x4 wv[CH];
+#pragma unroll
+  for (int j = 0; j < CH; ++j) {
+    const int c = min(lane + 64 * j, nch - 1);
+    wv[j] = *(const u32x4 *)(w + (size_t)c * 8);
+  }
+  float acc = 0.0f;
+#pragma unroll
+  for (int j = 0; j < CH; ++j) {
+    if (lane + 64 * j < nch) {
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        acc = __builtin_fmaf(__uint_as_float(xc[j][d] << 16), __uint_as_float(wv[j][d] << 16), acc);
+        acc = __builtin_fmaf(__uint_as_float(xc[j][d] & 0xFFFF0000u),
+                             __uint_as_float(wv[j][d] & 0xFFFF0000u), acc);
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) acc = acc + __shfl_xor(acc, m, 64);
+  return acc;
+}
+
+__device__ __forceinline__ float key_to_float(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+
+constexpr int SEL_WAVES = 4;
+
+template <int NV, int CH>
+__global__ __launch_bounds__(256) void k_select(const float *__restrict__ approx,
+                                                const float *__restrict__ wnorm,
+                                                const uint16_t *__restrict__ x,
+                                                const uint16_t *__restrict__ rw,
+                                                const float *__restrict__ bias,
+                                                const uint16_t *__restrict__ gw,
+                                                int32_t *__restrict__ topk_idx,
+                                                float *__restrict__ topk_w,
+                                                float *__restrict__ sgate,
+                                                uint16_t *__restrict__ xperm, int T, int E,
+                                                int k, int H, int has_shared, DispatchOut ds,
+                                                int fused) {
+  __shared__ int cl[SEL_WAVES][1024];
+  __shared__ float cv[SEL_WAVES][1024];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int t = blockIdx.x * SEL_WAVES + wave;
+  if (t < T) {
+    const float *ar = approx + (size_t)t * E;
+    // ---- k-th largest approximate logit -------------------------------
+    uint32_t key[NV];
+    float wn = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int e = lane + 64 * i;
+      key[i] = e < E ? ordered_key(ar[e]) : 0u;
+      if (e < E) wn = fmaxf(wn, wnorm[e]);
+    }
+    uint32_t taken = 0, kth = 0;
+    for (int j = 0; j < k; ++j) {
+      uint32_t bk = 0;
+      int bi = 0x7FFFFFFF;
+#pragma unroll
+      for (int i = 0; i < NV; ++i)
+        if (!(taken & (1u << i)) && (bi == 0x7FFFFFFF || key[i] > bk)) {
+          bk = key[i];
+          bi = i;
+        }
+      const uint32_t wk = wave_max_u32(bk);
+      const int wl = (int)wave_min_u32(bk == wk ? (uint32_t)lane : 64u);
+      if (lane == wl) taken |= 1u << bi;
+      kth = wk;
+    }
+    // ---- x row in registers (canonical chunk layout) and its norm ------
+    const int nch = H >> 3;
+    const uint16_t *xrow = x + (size_t)t * H;
+    u32x4 xc[CH];
+    float xs = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      const int c = min(lane + 64 * j, nch - 1);
+      xc[j] = *(const u32x4 *)(xrow + (size_t)c * 8);
+      if (lane + 64 * j < nch) {
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const float lo = __uint_as_float(xc[j][d] << 16), hi = __uint_as_float(xc[j][d] & 0xFFFF0000u);
+          xs = __builtin_fmaf(lo, lo, xs);
+          xs = __builtin_fmaf(hi, hi, xs);
+        }
+      }
+    }
+    for (int m = 32; m >= 1; m >>= 1) xs += __shfl_xor(xs, m, 64);
+    for (int m = 32; m >= 1; m >>= 1) wn = fmaxf(wn, __shfl_xor(wn, m, 64));
+    // ---- candidate threshold --------------------------------------------
+    const float lk = key_to_float(kth);
+    const float nrm = sqrtf(xs) * wn * 1.0625f;
+    const float d = 2.0f * (float)(H + 64) * 0x1p-23f * nrm;  // |approx - canonical|
+    const float thr = lk - 2.0f * d - 0x1p-21f * (fabsf(lk) + 2.0f * d) - 1e-30f * (float)H;
+    // ---- candidate list, expert-ascending -------------------------------
+    int nc = 0;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int e = lane + 64 * i;
+      const bool c = e < E && key_to_float(key[i]) >= thr;
+      const uint64_t b = __ballot(c);
+      if (c) cl[wave][nc + __popcll(b & ((1ull << lane) - 1ull))] = e;
+      nc += __popcll(b);
+    }
+    __builtin_amdgcn_wave_barrier();
+    // ---- canonical logits of the candidates ------------------------------
+    for (int c = 0; c < nc; ++c) {
+      const int e = cl[wave][c];
+      float v = canon_dot<CH>(xc, rw + (size_t)e * H, lane, nch);
+      if (bias) v = v + bias[e];
+      if (lane == 0) cv[wave][c] = v;
+    }
+    __builtin_amdgcn_wave_barrier();
+    // ---- top-k among candidates (value desc, expert asc) ----------------
+    uint32_t tmask = 0;  // taken bits per lane slot (nc <= 1024: 16 slots)
+    int seli = 0;
+    float selv = 0.0f;
+    for (int j = 0; j < k; ++j) {
+      uint32_t bk = 0;
+      int bs = 0x7FFFFFFF;
+      for (int i = 0; i < 16 && lane + 64 * i < nc; ++i) {
+        const uint32_t kk = ordered_key(cv[wave][lane + 64 * i]);
+        if (!(tmask & (1u << i)) && (bs == 0x7FFFFFFF || kk > bk)) {
+          bk = kk;
+          bs = lane + 64 * i;
+        }
+      }
+      const uint32_t wk = wave_max_u32(bk);
+      const int ws = (int)wave_min_u32(bk == wk && bs != 0x7FFFFFFF ? (uint32_t)bs : 0xFFFFFFFFu);
+      if ((ws & 63) == lane) tmask |= 1u << (ws >> 6);
+      if (lane == j) {
+        seli = cl[wave][ws];
+        selv = cv[wave][ws];
+      }
+    }
+    const float vmax = __shfl(selv, 0, 64);
+    const float p = lane < k ? expf(selv - vmax) : 0.0f;
+    float sum = 0.0f;
+    for (int j = 0; j < k; ++j) sum += __shfl(p, j, 64);
+    if (lane < k) {
+      topk_idx[(size_t)t * k + lane] = seli;
+      topk_w[(size_t)t * k + lane] = p / sum;
+    }
+    // ---- shared gate ----------------------------------------------------
+    float g = 1.0f;
+    if (gw) g = 1.0f / (1.0f + expf(-canon_dot<CH>(xc, gw, lane, nch)));
+    if (lane == 0) sgate[t] = g;
+    // ---- MFMA-order copy of x: position 8*j+e <- k = 4*e+j --------------
+    if (xperm) {
+      uint16_t *xo = xperm + (size_t)t * H;
+      for (int b = lane; b < (H >> 5); b += 64) {
+        const u32x4 *src = (const u32x4 *)(xrow + b * 32);
+        const u32x4 s0 = src[0], s1 = src[1], s2 = src[2], s3 = src[3];
+        const uint32_t in[16] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3],
+                                 s2[0], s2[1], s2[2], s2[3], s3[0], s3[1], s3[2], s3[3]};
+        uint32_t out[16];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int e2 = 0; e2 < 4; ++e2) {
+            const int ka = 8 * e2 + j, kb = ka + 4;
+            const uint32_t lo = (in[ka >> 1] >> (16 * (ka & 1))) & 0xFFFFu;
+            const uint32_t hi = (in[kb >> 1] >> (16 * (kb & 1))) & 0xFFFFu;
+            out[4 * j + e2] = lo | (hi << 16);
+          }
+        u32x4 *dst = (u32x4 *)(xo + b * 32);
+        dst[0] = u32x4{out[0], out[1], out[2], out[3]};
+        dst[1] = u32x4{out[4], out[5], out[6], out[7]};
+        dst[2] = u32x4{out[8], out[9], out[10], out[11]};
+        dst[3] = u32x4{out[12], out[13], out[14], out[15]};
+      }
+    }
+  }
+  if (!fused) return;
+  // ---- the last block runs the dispatch ---------------------------------
+  __shared__ int is_last;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __threadfence();
+    is_last = atomicAdd(ds.ticket, 1) == (int)gridDim.x - 1;
+  }
+  __syncthreads();
+  if (!is_last) return;
+  __threadfence();
+  if (threadIdx.x == 0) atomicExch(ds.ticket, 0);
+  dispatch_small_block(topk_idx, T, k, E, has_shared, ds);
+}
+
+template <int NV>
+hipError_t launch_select_nv(int ch, unsigned grid, const float *approx, const float *wnorm,
+                            const void *x, const void *rw, const float *bias, const void *gw,
+                            int32_t *idx, float *w, float *sg, void *xperm, int T, int E,
+                            int k, int H, int has_shared, const DispatchOut &ds, int fused,
+                            hipStream_t s) {
+#define SEL_ARGS                                                                            \
+  approx, wnorm, (const uint16_t *)x, (const uint16_t *)rw, bias, (const uint16_t *)gw, idx, \
+      w, sg, (uint16_t *)xperm, T, E, k, H, has_shared, ds, fused
+  switch (ch) {
+  case 1: k_select<NV, 1><<<grid, 256, 0, s>>>(SEL_ARGS); break;
+  case 2: k_select<NV, 2><<<grid, 256, 0, s>>>(SEL_ARGS); break;
+  case 4: k_select<NV, 4><<<grid, 256, 0, s>>>(SEL_ARGS); break;
+  default: k_select<NV, 8><<<grid, 256, 0, s>>>(SEL_ARGS); break;
+  }
+#undef SEL_ARGS
+  return hipGetLastError();
+}
+
+}  // namespace
+
+bool router_supported(int H, int E) { return H % 128 == 0 && H <= 4096 && E <= 1024; }
+
+hipError_t launch_router_fast(const void *x, const void *rw, const float *bias, const void *gw,
+                              float *approx, float *wnorm, int32_t *idx, float *w, float *sg,
+                              void *xperm, int T, int H, int E, int k, int has_shared,
+                              const DispatchOut *fused, hipStream_t s) {
+  if (T == 0) return hipSuccess;
+  // ---- approximate logits + row norms ------------------------------------
+  const int MS = T <= 16 ? 1 : (T <= 32 ? 2 : 4);
+  const int mt = 16 * MS;
+  // decode: one token tile, K split over up to 16 waves; prefill: 4 waves
+  int NW = T <= 64 ? H / 128 : 4;
+  if (NW > 16) NW = 16;
+  while (NW > 1 && (H % (32 * NW))) --NW;
+  const dim3 grid((E + 15) / 16, (T + mt - 1) / mt);
+  const size_t lds = sizeof(float) * ((size_t)NW * MS * 256 + NW * 16);
+  if (MS == 1)
+    k_router_mfma<1><<<grid, NW * 64, lds, s>>>((const uint16_t *)x, (const uint16_t *)rw, bias,
+                                                approx, wnorm, fused ? fused->ticket : nullptr,
+                                                T, H, E, NW);
+  else if (MS == 2)
+    k_router_mfma<2><<<grid, NW * 64, lds, s>>>((const uint16_t *)x, (const uint16_t *)rw, bias,
+                                                approx, wnorm, fused ? fused->ticket : nullptr,
+                                                T, H, E, NW);
+  else
+    k_router_mfma<4><<<grid, NW * 64, lds, s>>>((const uint16_t *)x, (const uint16_t *)rw, bias,
+                                                approx, wnorm, fused ? fused->ticket : nullptr,
+                                                T, H, E, NW);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  // ---- refine + select ------------------------------------------------------
+  const int ch = (H / 8 + 63) / 64;  // chunks per lane
+  const int chp = ch <= 1 ? 1 : (ch <= 2 ? 2 : (ch <= 4 ? 4 : 8));
+  const int nv = (E + 63) / 64;
+  DispatchOut ds;
+  memset(&ds, 0, sizeof ds);
+  if (fused) ds = *fused;
+  const unsigned sgrid = (T + SEL_WAVES - 1) / SEL_WAVES;
+  const int fz = fused ? 1 : 0;
+  if (nv <= 1)
+    return launch_select_nv<1>(chp, sgrid, approx, wnorm, x, rw, bias, gw, idx, w, sg, xperm, T,
+                               E, k, H, has_shared, ds, fz, s);
+  if (nv <= 2)
+    return launch_select_nv<2>(chp, sgrid, approx, wnorm, x, rw, bias, gw, idx, w, sg, xperm, T,
+                               E, k, H, has_shared, ds, fz, s);
+  if (nv <= 4)
+    return launch_select_nv<4>(chp, sgrid, approx, wnorm, x, rw, bias, gw, idx, w, sg, xperm, T,
+                               E, k, H, has_shared, ds, fz, s);
+  if (nv <= 8)
+    return launch_select_nv<8>(chp, sgrid, approx, wnorm, x, rw, bias, gw, idx, w, sg, xperm, T,
+                               E, k, H, has_shared, ds, fz, s);
+  return launch_select_nv<16>(chp, sgrid, approx, wnorm, x, rw, bias, gw, idx, w, sg, xperm, T,
+                              E, k, H, has_shared, ds, fz, s);
+}

@@ -73,6 +73,11 @@ class MoeLayer:
         self.t = t
         self.weights = L.Weights(*[_ptr(t.get(n)) for n, _ in L.Weights._fields_])
 
+    def set_tensor(self, name: str, t):
+        """Replace one device tensor (same layout) and refresh the C struct."""
+        self.t[name] = t
+        self.weights = L.Weights(*[_ptr(self.t.get(n)) for n, _ in L.Weights._fields_])
+
     def workspace(self, max_tokens: int) -> torch.Tensor:
         n = L.lib().ainfer_moe_workspace_bytes(C.byref(self.shape), max_tokens)
         if n == 0:

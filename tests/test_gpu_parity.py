@@ -101,6 +101,50 @@ def test_route_and_dispatch_bit_exact(torch, oracle, name, T):
     assert np.array_equal(to_np(inv), iv)
 
 
+def _route_check(torch, oracle, layer, x, what):
+    T = x.shape[0]
+    ws = layer.workspace(T)
+    idx, w, sg, lg = layer.route(x, ws, want_logits=True)
+    torch.cuda.synchronize()
+    hl = host_copy(oracle, layer)
+    r_idx, r_w, r_sg, r_lg = hl.route(to_np(x), T)
+    assert np.array_equal(to_np(lg).view(np.uint32), r_lg.view(np.uint32)), what
+    assert np.array_equal(to_np(idx), r_idx), what
+    np.testing.assert_allclose(to_np(w), r_w, rtol=2e-6, atol=1e-7)
+    return r_idx
+
+
+def test_router_ties_and_degenerate_inputs(torch, oracle):
+    """Inputs built to defeat the candidate refine: exact ties (duplicated
+    router rows), all logits equal (every expert a candidate), coarse values
+    with many near and exact ties, and large-magnitude activations."""
+    from ainfer_amd.moe import make_input
+    layer = get_layer(torch, "c1")
+    E, H = layer.cfg.n_experts, layer.cfg.hidden
+    rw0 = layer.t["router_w"].clone()
+    for T in (1, 16, 64, 300):
+        x = make_input(layer.cfg, T, tag=77 + T)
+        # duplicated rows: experts 2i and 2i+1 always tie
+        rw = rw0.view(E, H).clone()
+        rw[1::2] = rw[0::2]
+        layer.set_tensor("router_w", rw.reshape(-1).contiguous())
+        idx = _route_check(torch, oracle, layer, x, f"dup rows T={T}")
+        assert (idx[:, ::2] % 2 == 0).all()  # lower index of each tied pair first
+        # all logits equal: top-k is experts 0..k-1
+        layer.set_tensor("router_w", torch.zeros_like(rw0))
+        idx = _route_check(torch, oracle, layer, x, f"zeros T={T}")
+        assert (idx == np.arange(layer.cfg.top_k)).all()
+        # coarse values: many exact and near ties
+        q = torch.randint(-1, 2, rw0.shape, device="cuda").to(torch.bfloat16) * 0.015625
+        xq = torch.randint(-2, 3, x.shape, device="cuda").to(torch.bfloat16)
+        layer.set_tensor("router_w", q.contiguous())
+        _route_check(torch, oracle, layer, xq, f"coarse T={T}")
+        # large activations
+        layer.set_tensor("router_w", rw0)
+        _route_check(torch, oracle, layer, (x.float() * 4096).to(torch.bfloat16), f"big T={T}")
+    layer.set_tensor("router_w", rw0)
+
+
 FWD_CASES = [("c0", 1), ("c1", 1), ("c1", 4), ("c1", 16), ("c3", 64)]
 
 
