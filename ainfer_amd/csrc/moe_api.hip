@@ -163,11 +163,18 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
   const int has_shared = s->shared_inter > 0;
   const bool fused = T <= FUSED_DISPATCH_MAX_T;
   DispatchOut d = dispatch_out(s, L, ws, T);
-  HIP_TRY(launch_router_fast(x, w->router_w, w->router_bias, w->shared_gate_w,
-                             at<float>(ws, L.logits), at<float>(ws, L.wnorm),
-                             at<int32_t>(ws, L.idx), at<float>(ws, L.w), at<float>(ws, L.sg),
-                             at<uint16_t>(ws, L.xperm), T, H, E, k, has_shared,
-                             fused ? &d : nullptr, st));
+  if (T <= EXACT_ROUTER_MAX_T)
+    HIP_TRY(launch_router_exact(x, w->router_w, w->router_bias, w->shared_gate_w,
+                                at<float>(ws, L.logits), at<float>(ws, L.sg_logit),
+                                at<int32_t>(ws, L.idx), at<float>(ws, L.w), at<float>(ws, L.sg),
+                                at<uint16_t>(ws, L.xperm), T, H, E, k, has_shared,
+                                fused ? &d : nullptr, st));
+  else
+    HIP_TRY(launch_router_fast(x, w->router_w, w->router_bias, w->shared_gate_w,
+                               at<float>(ws, L.logits), at<float>(ws, L.wnorm),
+                               at<int32_t>(ws, L.idx), at<float>(ws, L.w), at<float>(ws, L.sg),
+                               at<uint16_t>(ws, L.xperm), T, H, E, k, has_shared,
+                               fused ? &d : nullptr, st));
   pc->end(2);
   if (!fused)
     HIP_TRY(launch_dispatch(at<int32_t>(ws, L.idx), T, k, E, SMALL_MT, has_shared,
@@ -312,6 +319,14 @@ int ainfer_moe_route(const ainfer_moe_shape *s, const ainfer_moe_weights *w, con
   if ((rc = check_ws(s, T, ws, ws_bytes))) return rc;
   const Layout L = layout_of(*s, T);
   hipStream_t st = (hipStream_t)stream;
+  if (T <= EXACT_ROUTER_MAX_T) {
+    HIP_TRY(launch_router_exact(x, w->router_w, w->router_bias, w->shared_gate_w,
+                                logits ? logits : at<float>(ws, L.logits),
+                                at<float>(ws, L.sg_logit), topk_idx, topk_w, shared_gate, nullptr,
+                                T, s->hidden, s->n_experts, s->top_k, s->shared_inter > 0,
+                                nullptr, st));
+    return AINFER_OK;
+  }
   HIP_TRY(launch_router_fast(x, w->router_w, w->router_bias, w->shared_gate_w,
                              at<float>(ws, L.logits), at<float>(ws, L.wnorm), topk_idx, topk_w,
                              shared_gate, nullptr, T, s->hidden, s->n_experts, s->top_k,

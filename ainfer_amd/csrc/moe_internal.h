@@ -55,6 +55,14 @@ hipError_t launch_router_fast(const void *x, const void *rw, const float *bias, 
                               float *approx, float *wnorm, int32_t *idx, float *w, float *sg,
                               void *xperm, int T, int H, int E, int k, int has_shared,
                               const DispatchOut *fused, hipStream_t s);
+// Small T: canonical logits of all experts on VALU (k_router_logits), then the
+// same selection without the refine.  logits [T][E], sg_logit [T] out.
+hipError_t launch_router_exact(const void *x, const void *rw, const float *bias, const void *gw,
+                               float *logits, float *sg_logit, int32_t *idx, float *w, float *sg,
+                               void *xperm, int T, int H, int E, int k, int has_shared,
+                               const DispatchOut *fused, hipStream_t s);
+// below this many tokens the router computes every logit in the canonical order
+constexpr int EXACT_ROUTER_MAX_T = 16;
 hipError_t launch_dispatch(const int32_t *idx, int T, int k, int E, int mt, int has_shared,
                            int32_t *chunk_counts, int32_t *rank, const DispatchOut &ds,
                            hipStream_t s);

@@ -147,14 +147,52 @@ __device__ __forceinline__ float canon_dot(const u32x4 (&xc)[CH], const uint16_t
   return acc;
 }
 
+// NB canonical dots at once (loads of all rows issued before any math);
+// rows past nrows repeat the last row and their results are ignored.
+template <int CH, int NB>
+__device__ __forceinline__ void canon_dot_batch(const u32x4 (&xc)[CH], const uint16_t *const (&w)[NB],
+                                                int lane, int nch, float (&out)[NB]) {
+  u32x4 wv[NB][CH];
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      const int c = min(lane + 64 * j, nch - 1);
+      wv[b][j] = *(const u32x4 *)(w[b] + (size_t)c * 8);
+    }
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      if (lane + 64 * j < nch) {
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          acc = __builtin_fmaf(__uint_as_float(xc[j][d] << 16), __uint_as_float(wv[b][j][d] << 16), acc);
+          acc = __builtin_fmaf(__uint_as_float(xc[j][d] & 0xFFFF0000u),
+                               __uint_as_float(wv[b][j][d] & 0xFFFF0000u), acc);
+        }
+      }
+    }
+    out[b] = acc;
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1)
+#pragma unroll
+    for (int b = 0; b < NB; ++b) out[b] = out[b] + __shfl_xor(out[b], m, 64);
+}
+
 __device__ __forceinline__ float key_to_float(uint32_t k) {
   return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
 }
 
 constexpr int SEL_WAVES = 4;
 
-template <int NV, int CH>
+// EXACT: `approx` already holds the canonical logits (k_router_logits) and
+// `sgl` the canonical shared-gate logits; the refine is skipped.
+template <int NV, int CH, bool EXACT>
 __global__ __launch_bounds__(256) void k_select(const float *__restrict__ approx,
+                                                const float *__restrict__ sgl,
                                                 const float *__restrict__ wnorm,
                                                 const uint16_t *__restrict__ x,
                                                 const uint16_t *__restrict__ rw,
@@ -179,7 +217,7 @@ __global__ __launch_bounds__(256) void k_select(const float *__restrict__ approx
     for (int i = 0; i < NV; ++i) {
       const int e = lane + 64 * i;
       key[i] = e < E ? ordered_key(ar[e]) : 0u;
-      if (e < E) wn = fmaxf(wn, wnorm[e]);
+      if (!EXACT && e < E) wn = fmaxf(wn, wnorm[e]);
     }
     uint32_t taken = 0, kth = 0;
     for (int j = 0; j < k; ++j) {
@@ -219,8 +257,9 @@ __global__ __launch_bounds__(256) void k_select(const float *__restrict__ approx
     // ---- candidate threshold --------------------------------------------
     const float lk = key_to_float(kth);
     const float nrm = sqrtf(xs) * wn * 1.0625f;
-    const float d = 2.0f * (float)(H + 64) * 0x1p-23f * nrm;  // |approx - canonical|
-    const float thr = lk - 2.0f * d - 0x1p-21f * (fabsf(lk) + 2.0f * d) - 1e-30f * (float)H;
+    const float d = EXACT ? 0.0f : 2.0f * (float)(H + 64) * 0x1p-23f * nrm;  // |approx - canonical|
+    const float thr = EXACT ? lk
+                            : lk - 2.0f * d - 0x1p-21f * (fabsf(lk) + 2.0f * d) - 1e-30f * (float)H;
     // ---- candidate list, expert-ascending -------------------------------
     int nc = 0;
 #pragma unroll
@@ -233,11 +272,23 @@ __global__ __launch_bounds__(256) void k_select(const float *__restrict__ approx
     }
     __builtin_amdgcn_wave_barrier();
     // ---- canonical logits of the candidates ------------------------------
-    for (int c = 0; c < nc; ++c) {
-      const int e = cl[wave][c];
-      float v = canon_dot<CH>(xc, rw + (size_t)e * H, lane, nch);
-      if (bias) v = v + bias[e];
-      if (lane == 0) cv[wave][c] = v;
+    if (EXACT) {
+      for (int c = lane; c < nc; c += 64) cv[wave][c] = ar[cl[wave][c]];
+    } else {
+      for (int c0 = 0; c0 < nc; c0 += 4) {
+        const uint16_t *rows[4];
+        int ee[4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          ee[b] = cl[wave][min(c0 + b, nc - 1)];
+          rows[b] = rw + (size_t)ee[b] * H;
+        }
+        float v[4];
+        canon_dot_batch<CH, 4>(xc, rows, lane, nch, v);
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+          if (lane == 0 && c0 + b < nc) cv[wave][c0 + b] = bias ? v[b] + bias[ee[b]] : v[b];
+      }
     }
     __builtin_amdgcn_wave_barrier();
     // ---- top-k among candidates (value desc, expert asc) ----------------
@@ -272,7 +323,7 @@ __global__ __launch_bounds__(256) void k_select(const float *__restrict__ approx
     }
     // ---- shared gate ----------------------------------------------------
     float g = 1.0f;
-    if (gw) g = 1.0f / (1.0f + expf(-canon_dot<CH>(xc, gw, lane, nch)));
+    if (gw) g = 1.0f / (1.0f + expf(-(EXACT ? sgl[t] : canon_dot<CH>(xc, gw, lane, nch))));
     if (lane == 0) sgate[t] = g;
     // ---- MFMA-order copy of x: position 8*j+e <- k = 4*e+j --------------
     if (xperm) {
@@ -315,20 +366,21 @@ __global__ __launch_bounds__(256) void k_select(const float *__restrict__ approx
   dispatch_small_block(topk_idx, T, k, E, has_shared, ds);
 }
 
-template <int NV>
-hipError_t launch_select_nv(int ch, unsigned grid, const float *approx, const float *wnorm,
+template <int NV, bool EXACT>
+hipError_t launch_select_nv(int ch, unsigned grid, const float *approx, const float *sgl,
+                            const float *wnorm,
                             const void *x, const void *rw, const float *bias, const void *gw,
                             int32_t *idx, float *w, float *sg, void *xperm, int T, int E,
                             int k, int H, int has_shared, const DispatchOut &ds, int fused,
                             hipStream_t s) {
 #define SEL_ARGS                                                                            \
-  approx, wnorm, (const uint16_t *)x, (const uint16_t *)rw, bias, (const uint16_t *)gw, idx, \
+  approx, sgl, wnorm, (const uint16_t *)x, (const uint16_t *)rw, bias, (const uint16_t *)gw, idx, \
       w, sg, (uint16_t *)xperm, T, E, k, H, has_shared, ds, fused
   switch (ch) {
-  case 1: k_select<NV, 1><<<grid, 256, 0, s>>>(SEL_ARGS); break;
-  case 2: k_select<NV, 2><<<grid, 256, 0, s>>>(SEL_ARGS); break;
-  case 4: k_select<NV, 4><<<grid, 256, 0, s>>>(SEL_ARGS); break;
-  default: k_select<NV, 8><<<grid, 256, 0, s>>>(SEL_ARGS); break;
+  case 1: k_select<NV, 1, EXACT><<<grid, 256, 0, s>>>(SEL_ARGS); break;
+  case 2: k_select<NV, 2, EXACT><<<grid, 256, 0, s>>>(SEL_ARGS); break;
+  case 4: k_select<NV, 4, EXACT><<<grid, 256, 0, s>>>(SEL_ARGS); break;
+  default: k_select<NV, 8, EXACT><<<grid, 256, 0, s>>>(SEL_ARGS); break;
   }
 #undef SEL_ARGS
   return hipGetLastError();
@@ -337,6 +389,30 @@ hipError_t launch_select_nv(int ch, unsigned grid, const float *approx, const fl
 }  // namespace
 
 bool router_supported(int H, int E) { return H % 128 == 0 && H <= 4096 && E <= 1024; }
+
+template <bool EXACT>
+hipError_t launch_select(const float *approx, const float *sgl, const float *wnorm,
+                         const void *x, const void *rw, const float *bias, const void *gw,
+                         int32_t *idx, float *w, float *sg, void *xperm, int T, int H, int E,
+                         int k, int has_shared, const DispatchOut *fused, hipStream_t s) {
+  const int ch = (H / 8 + 63) / 64;  // chunks per lane
+  const int chp = ch <= 1 ? 1 : (ch <= 2 ? 2 : (ch <= 4 ? 4 : 8));
+  const int nv = (E + 63) / 64;
+  DispatchOut ds;
+  memset(&ds, 0, sizeof ds);
+  if (fused) ds = *fused;
+  const unsigned g = (T + SEL_WAVES - 1) / SEL_WAVES;
+  const int fz = fused ? 1 : 0;
+#define SEL_CALL(NVV)                                                                        \
+  launch_select_nv<NVV, EXACT>(chp, g, approx, sgl, wnorm, x, rw, bias, gw, idx, w, sg, xperm, \
+                               T, E, k, H, has_shared, ds, fz, s)
+  if (nv <= 1) return SEL_CALL(1);
+  if (nv <= 2) return SEL_CALL(2);
+  if (nv <= 4) return SEL_CALL(4);
+  if (nv <= 8) return SEL_CALL(8);
+  return SEL_CALL(16);
+#undef SEL_CALL
+}
 
 hipError_t launch_router_fast(const void *x, const void *rw, const float *bias, const void *gw,
                               float *approx, float *wnorm, int32_t *idx, float *w, float *sg,
@@ -367,26 +443,18 @@ hipError_t launch_router_fast(const void *x, const void *rw, const float *bias, 
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
   // ---- refine + select ------------------------------------------------------
-  const int ch = (H / 8 + 63) / 64;  // chunks per lane
-  const int chp = ch <= 1 ? 1 : (ch <= 2 ? 2 : (ch <= 4 ? 4 : 8));
-  const int nv = (E + 63) / 64;
-  DispatchOut ds;
-  memset(&ds, 0, sizeof ds);
-  if (fused) ds = *fused;
-  const unsigned sgrid = (T + SEL_WAVES - 1) / SEL_WAVES;
-  const int fz = fused ? 1 : 0;
-  if (nv <= 1)
-    return launch_select_nv<1>(chp, sgrid, approx, wnorm, x, rw, bias, gw, idx, w, sg, xperm, T,
-                               E, k, H, has_shared, ds, fz, s);
-  if (nv <= 2)
-    return launch_select_nv<2>(chp, sgrid, approx, wnorm, x, rw, bias, gw, idx, w, sg, xperm, T,
-                               E, k, H, has_shared, ds, fz, s);
-  if (nv <= 4)
-    return launch_select_nv<4>(chp, sgrid, approx, wnorm, x, rw, bias, gw, idx, w, sg, xperm, T,
-                               E, k, H, has_shared, ds, fz, s);
-  if (nv <= 8)
-    return launch_select_nv<8>(chp, sgrid, approx, wnorm, x, rw, bias, gw, idx, w, sg, xperm, T,
-                               E, k, H, has_shared, ds, fz, s);
-  return launch_select_nv<16>(chp, sgrid, approx, wnorm, x, rw, bias, gw, idx, w, sg, xperm, T,
-                              E, k, H, has_shared, ds, fz, s);
+  return launch_select<false>(approx, nullptr, wnorm, x, rw, bias, gw, idx, w, sg, xperm, T, H,
+                              E, k, has_shared, fused, s);
+}
+
+hipError_t launch_router_exact(const void *x, const void *rw, const float *bias, const void *gw,
+                               float *logits, float *sg_logit, int32_t *idx, float *w, float *sg,
+                               void *xperm, int T, int H, int E, int k, int has_shared,
+                               const DispatchOut *fused, hipStream_t s) {
+  if (T == 0) return hipSuccess;
+  hipError_t err = launch_router(x, rw, bias, gw, logits, sg_logit,
+                                 fused ? fused->ticket : nullptr, T, H, E, s);
+  if (err != hipSuccess) return err;
+  return launch_select<true>(logits, sg_logit, nullptr, x, rw, bias, gw, idx, w, sg, xperm, T, H,
+                             E, k, has_shared, fused, s);
 }
