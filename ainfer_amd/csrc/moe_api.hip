@@ -65,7 +65,7 @@ struct ProfCall {
 
 struct Layout {
   size_t logits, sg_logit, idx, w, sg, xperm, chunk_counts, rank, counts, offsets, perm, inv,
-      ptok, tiles, n_tiles, cnt, ticket, act, act_s, o, h, wnorm, total;
+      ptok, tiles, n_tiles, cnt, ticket, act, act_s, o, h, wnorm, xsum, asum, asum_s, total;
 };
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -100,15 +100,18 @@ Layout layout_of(const ainfer_moe_shape &s, int Tm) {
   L.perm = take(T * k * 4);
   L.inv = take(T * k * 4);
   L.ptok = take(T * k * 4);
-  L.tiles = take((size_t)max_tiles_bound(s, (int)T, SMALL_MT) * 16);
+  L.tiles = take((size_t)max_tiles_bound(s, (int)T, SMALL_MT) * 16);  // >= the GEMM_MT bound
   L.n_tiles = take(4);
   L.cnt = take(T * (H / 16) * 4);
   L.ticket = take(4);
   L.act = take(T * k * s.inter * 2);
   L.act_s = take(T * (size_t)(s.shared_inter > 0 ? s.shared_inter : 1) * 2);
-  L.o = take(T * (k + 1) * H * 4);
+  L.o = take(T * (k + 1) * H * 2);
   L.h = take(T * H * 2);
   L.wnorm = take(E * 4);
+  L.xsum = take(T * (H / 128) * 4);
+  L.asum = take(T * k * (s.inter / 64) * 4);
+  L.asum_s = take(T * (size_t)(s.shared_inter > 0 ? s.shared_inter / 64 : 1) * 4);
   L.total = off;
   return L;
 }
@@ -162,6 +165,8 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
   const int E = s->n_experts, k = s->top_k, H = s->hidden;
   const int has_shared = s->shared_inter > 0;
   const bool fused = T <= FUSED_DISPATCH_MAX_T;
+  const bool gemm = T >= GEMM_MIN_T;
+  const int mt = gemm ? GEMM_MT : SMALL_MT;
   DispatchOut d = dispatch_out(s, L, ws, T);
   if (T <= EXACT_ROUTER_MAX_T)
     HIP_TRY(launch_router_exact(x, w->router_w, w->router_bias, w->shared_gate_w,
@@ -173,13 +178,60 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
     HIP_TRY(launch_router_fast(x, w->router_w, w->router_bias, w->shared_gate_w,
                                at<float>(ws, L.logits), at<float>(ws, L.wnorm),
                                at<int32_t>(ws, L.idx), at<float>(ws, L.w), at<float>(ws, L.sg),
-                               at<uint16_t>(ws, L.xperm), T, H, E, k, has_shared,
-                               fused ? &d : nullptr, st));
+                               at<uint16_t>(ws, L.xperm), gemm ? at<float>(ws, L.xsum) : nullptr,
+                               T, H, E, k, has_shared, fused ? &d : nullptr, st));
   pc->end(2);
   if (!fused)
-    HIP_TRY(launch_dispatch(at<int32_t>(ws, L.idx), T, k, E, SMALL_MT, has_shared,
+    HIP_TRY(launch_dispatch(at<int32_t>(ws, L.idx), T, k, E, mt, has_shared,
                             at<int32_t>(ws, L.chunk_counts), at<int32_t>(ws, L.rank), d, st));
   pc->end(3);
+  if (gemm) {
+    GemmArgs g;
+    memset(&g, 0, sizeof g);
+    g.ptok = d.ptok;
+    g.tiles = d.tiles;
+    g.n_tiles = d.n_tiles;
+    g.T = T;
+    g.k = k;
+    g.E = E;
+    g.H = H;
+    g.I = s->inter;
+    g.Is = s->shared_inter;
+    g.xsum = at<float>(ws, L.xsum);
+    g.asum = at<float>(ws, L.asum);
+    g.asum_s = at<float>(ws, L.asum_s);
+    const int gtiles = max_tiles_bound(*s, T, GEMM_MT);
+    g.w0 = w->w_gate;
+    g.w1 = w->w_up;
+    g.s0 = (const uint16_t *)w->s_gate;
+    g.s1 = (const uint16_t *)w->s_up;
+    g.ws0 = w->ws_gate;
+    g.ws1 = w->ws_up;
+    g.ss0 = (const uint16_t *)w->ss_gate;
+    g.ss1 = (const uint16_t *)w->ss_up;
+    g.a_routed = at<uint16_t>(ws, L.xperm);
+    g.act = at<uint16_t>(ws, L.act);
+    g.act_s = at<uint16_t>(ws, L.act_s);
+    HIP_TRY(launch_expert_gemm(0, s->scale_dtype, g, gtiles, st));
+    pc->end(4);
+    g.w0 = w->w_down;
+    g.s0 = (const uint16_t *)w->s_down;
+    g.ws0 = w->ws_down;
+    g.ss0 = (const uint16_t *)w->ss_down;
+    g.w1 = nullptr;
+    g.s1 = nullptr;
+    g.ws1 = nullptr;
+    g.ss1 = nullptr;
+    g.a_routed = at<uint16_t>(ws, L.act);
+    g.a_shared = at<uint16_t>(ws, L.act_s);
+    g.o = at<uint16_t>(ws, L.o);
+    HIP_TRY(launch_expert_gemm(1, s->scale_dtype, g, gtiles, st));
+    pc->end(5);
+    HIP_TRY(launch_combine(at<uint16_t>(ws, L.o), d.inv, at<float>(ws, L.w), at<float>(ws, L.sg),
+                           has_shared, resid, y, T, k, H, st));
+    pc->end(6);
+    return AINFER_OK;
+  }
   ExpertArgs a;
   memset(&a, 0, sizeof a);
   a.ptok = d.ptok;
@@ -219,10 +271,10 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
   a.ss1 = nullptr;
   a.a_routed = at<uint16_t>(ws, L.act);
   a.a_shared = at<uint16_t>(ws, L.act_s);
-  a.o = at<float>(ws, L.o);
+  a.o = at<uint16_t>(ws, L.o);
   HIP_TRY(launch_expert_stream(1, s->scale_dtype, a, max_tiles, kbw, st));
   pc->end(5);
-  HIP_TRY(launch_combine(at<float>(ws, L.o), d.inv, at<float>(ws, L.w), at<float>(ws, L.sg),
+  HIP_TRY(launch_combine(at<uint16_t>(ws, L.o), d.inv, at<float>(ws, L.w), at<float>(ws, L.sg),
                          has_shared, resid, y, T, k, H, st));
   pc->end(6);
   return AINFER_OK;
@@ -329,8 +381,8 @@ int ainfer_moe_route(const ainfer_moe_shape *s, const ainfer_moe_weights *w, con
   }
   HIP_TRY(launch_router_fast(x, w->router_w, w->router_bias, w->shared_gate_w,
                              at<float>(ws, L.logits), at<float>(ws, L.wnorm), topk_idx, topk_w,
-                             shared_gate, nullptr, T, s->hidden, s->n_experts, s->top_k,
-                             s->shared_inter > 0, nullptr, st));
+                             shared_gate, nullptr, nullptr, T, s->hidden, s->n_experts,
+                             s->top_k, s->shared_inter > 0, nullptr, st));
   // the full canonical logits, on request (lane-strided chunk order, VALU)
   if (logits)
     HIP_TRY(launch_router(x, w->router_w, w->router_bias, w->shared_gate_w, logits,

@@ -88,3 +88,15 @@ __device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t o
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
 constexpr uint32_t BUF_OOB = 0x80000000u;
+
+// ---- XCD-aware block order -------------------------------------------------
+// Workgroups are dispatched round-robin over the 8 XCDs (block b -> XCD b%8),
+// each with its own L2.  This bijection hands each XCD a contiguous range of
+// logical block ids, so neighbouring work items (which share operands) run
+// on the same L2.
+constexpr int N_XCD = 8;
+__device__ __forceinline__ int xcd_remap(int b, int G) {
+  const int q = G / N_XCD, r = G % N_XCD;
+  const int xcd = b % N_XCD, idx = b / N_XCD;
+  return xcd < r ? xcd * (q + 1) + idx : r * (q + 1) + (xcd - r) * q + idx;
+}

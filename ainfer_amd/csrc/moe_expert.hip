@@ -28,7 +28,7 @@
 //
 // MODE 0: gate and up together, epilogue silu(g)*u -> act (bf16, MFMA
 //         order).
-// MODE 1: down, epilogue o (fp32) per dispatch position; the combine kernel
+// MODE 1: down, epilogue o (bf16) per dispatch position; the combine kernel
 //         sums a token's k + 1 rows in slot order.
 #include "moe_common.h"
 #include "moe_internal.h"
@@ -172,7 +172,7 @@ __global__ __launch_bounds__(1024) void k_expert(ExpertArgs a) {
       dst[(size_t)(pos0 + tm) * N + perm32_pos(row)] = f32_to_bf16(silu_mul(g, u));
     } else {
       const size_t orow = shared ? (size_t)a.T * a.k + pos0 + tm : (size_t)(pos0 + tm);
-      a.o[orow * a.H + row] = g;
+      a.o[orow * a.H + row] = f32_to_bf16(g);
     }
   }
 }

@@ -1,0 +1,335 @@
+// moe_gemm.hip - grouped INT4 expert GEMM for prefill (bf16 MFMA).
+//
+// Same arithmetic as the decode kernel (moe_expert.hip): weights become bf16
+// 136 + q with one AND-OR per pair, every 128-wide group accumulates from
+// -136 * sum_{k in g} a[m][k] and the group's scale is applied with one fp32
+// fma per output, so the result is sum_g s_g * sum_{k in g} q * a.
+// Restates the reference's INT4 GEMM (ChunkGemm, tools/cmdlist/kernels.cpp:
+// 691-785; gemmMT4, tools/prefill/prefill.cpp:46-129) for bf16 MFMA.
+//
+// Block tile: 128 tokens (one expert tile of the dispatch) x 128 weight rows
+// (MODE 0: 64 gate rows + the matching 64 up rows; MODE 1: 128 down rows),
+// K in 128-wide groups.  4 waves as 2 (tokens) x 2 (rows); a wave owns
+// 64 x 64 = 4 x 4 tiles of v_mfma_f32_16x16x32_bf16.
+//
+// Data movement: a 3-stage LDS ring per block.  Each stage holds one group
+// of the token rows (128 x 256 B, already in MFMA order) and of the raw INT4
+// weight rows (128 x 64 B).  Both arrive by global->LDS DMA
+// (global_load_lds_dwordx4: lane i of a wave lands at M0 + 16 i), two groups
+// ahead of the math, with no staging registers.  The DMA is issued from
+// inline asm and its completion tracked with explicit vmcnt waits, so the
+// compiler's conservative waits do not serialise the ring.  Rows are XOR-
+// swizzled in 16-byte chunks (A: chunk c of row r at c ^ (r & 15)) so that
+// the 16 lanes reading 16 rows at one column
+// hit distinct bank groups (B: chunk q at q ^ bswz(r)).  Scales and the group sums sum_{k in g} a
+// (for x from k_select, for act from this kernel's MODE 0 epilogue) are
+// copied to LDS once per block.
+#include "moe_common.h"
+#include "moe_internal.h"
+
+namespace {
+
+constexpr int BM = 128;               // tokens per tile
+constexpr int BN = 128;               // weight rows per block
+constexpr int STAGES = 3;
+constexpr int A_STAGE = BM * 256;     // bytes
+constexpr int B_STAGE = BN * 64;      // bytes
+constexpr int STAGE = A_STAGE + B_STAGE;
+constexpr int DMA_PER_STAGE = (A_STAGE + B_STAGE) / (256 * 16);  // per thread: 10
+
+__device__ __forceinline__ void dma16(const void *g, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(g), "s"(lds_addr)
+               : "memory", "m0");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
+__device__ __forceinline__ void block_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// B chunk swizzle: 2-bit function of the row such that 8 consecutive rows
+// (32 banks x 4 B) and 16 consecutive rows (64 banks) both land the 16-byte
+// chunks of one logical column in distinct bank groups.
+__device__ __forceinline__ int bswz(int r) {
+  return (((r >> 1) ^ (r >> 3)) & 1) | (((r >> 2) & 1) << 1);
+}
+
+__device__ __forceinline__ u32x4 nib_slice3(u32x4 b, int j, uint32_t magic) {
+  const uint32_t mask = 0x000F000Fu;
+  return u32x4{((b[0] >> (4 * j)) & mask) | magic, ((b[1] >> (4 * j)) & mask) | magic,
+               ((b[2] >> (4 * j)) & mask) | magic, ((b[3] >> (4 * j)) & mask) | magic};
+}
+
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  return g / (1.0f + expf(-g)) * u;
+}
+
+template <int SD, int MODE>
+__global__ __launch_bounds__(256) void k_expert_gemm(GemmArgs a) {
+  // dynamic LDS: STAGES x (A | B) ring, scales[G][BN] fp16, xs[G][BM] fp32
+  // (group-major: a lane's 4 rows are one 16-byte read), red_sum[2][BM] fp32
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int n_nb = a.n_nblk;
+  const int n_items = *a.n_tiles * n_nb;  // the grid is an upper bound
+  if ((int)blockIdx.x >= n_items) return;
+  const int lb = xcd_remap(blockIdx.x, n_items);
+  const int tile_id = lb / n_nb, nb = lb % n_nb;
+  const int4 t = a.tiles[tile_id];
+  const int e = t.x, pos0 = t.y, mcnt = t.z;
+  const bool shared = e == a.E;
+  // MODE 0: N = act columns (I or Is), block covers 64 of them; MODE 1: N = H, 128 rows
+  const int N = MODE == 0 ? (shared ? a.Is : a.I) : a.H;
+  const int K = MODE == 0 ? a.H : (shared ? a.Is : a.I);
+  const int G = K >> 7;
+  if (nb * (MODE == 0 ? 64 : 128) >= N) return;
+
+  const uint32_t lds0 = (uint32_t)(uintptr_t)lds;
+  uint16_t *sc_lds = (uint16_t *)(lds + STAGES * STAGE);
+  float *xs_lds = (float *)(lds + STAGES * STAGE + ((BN * G * 2 + 15) & ~15));
+  float *red_sum = xs_lds + BM * G;
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int m16 = lane & 15, q = lane >> 4;
+
+  // ---- per-thread DMA sources: 8 A slots and 2 B slots per stage ----------
+  // slot s = (i*4 + wave)*64 + lane, 16 bytes each
+  const uint8_t *asrc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int s = (i * 4 + wave) * 64 + lane;
+    const int r = s >> 4, c = (s & 15) ^ (r & 15);
+    const int rr = min(r, mcnt - 1);
+    const uint16_t *row;
+    if (MODE == 0) {
+      const int tok = shared ? pos0 + rr : a.ptok[pos0 + rr];
+      row = a.a_routed + (size_t)tok * a.H;
+    } else {
+      row = (shared ? a.a_shared : a.a_routed) + (size_t)(pos0 + rr) * K;
+    }
+    asrc[i] = (const uint8_t *)row + c * 16;
+  }
+  const size_t rowb = (size_t)K / 2;
+  const uint8_t *bsrc[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int s = (i * 4 + wave) * 64 + lane;
+    const int r = s >> 2, qq = (s & 3) ^ bswz(r);
+    const uint8_t *w;
+    int row;
+    if (MODE == 0) {
+      w = r < 64 ? (shared ? a.ws0 : a.w0 + (size_t)e * N * rowb)
+                 : (shared ? a.ws1 : a.w1 + (size_t)e * N * rowb);
+      row = nb * 64 + (r & 63);
+    } else {
+      w = shared ? a.ws0 : a.w0 + (size_t)e * N * rowb;
+      row = nb * 128 + r;
+    }
+    row = min(row, N - 1);
+    bsrc[i] = w + (size_t)row * rowb + qq * 16;
+  }
+  auto issue = [&](int g) {  // DMA of group g into stage g % STAGES
+    const uint32_t base = lds0 + (uint32_t)(g % STAGES) * STAGE;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      dma16(asrc[i] + g * 256, base + (uint32_t)((i * 4 + wave) * 1024));
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      dma16(bsrc[i] + g * 64, base + A_STAGE + (uint32_t)((i * 4 + wave) * 1024));
+  };
+
+  // ---- prologue: groups 0 and 1 in flight; scales and group sums to LDS ---
+  issue(0);
+  if (G > 1) issue(1);
+  for (int idx = tid; idx < BN * G; idx += 256) {
+    const int r = idx / G, g = idx % G;
+    const uint16_t *sc;
+    int row;
+    if (MODE == 0) {
+      sc = r < 64 ? (shared ? a.ss0 : a.s0 + (size_t)e * N * G)
+                  : (shared ? a.ss1 : a.s1 + (size_t)e * N * G);
+      row = nb * 64 + (r & 63);
+    } else {
+      sc = shared ? a.ss0 : a.s0 + (size_t)e * N * G;
+      row = nb * 128 + r;
+    }
+    sc_lds[g * BN + r] = sc[(size_t)min(row, N - 1) * G + g];
+  }
+  for (int idx = tid; idx < BM * G; idx += 256) {
+    const int row = idx / G, g = idx % G;
+    float v = 0.0f;
+    if (row < mcnt) {
+      if (MODE == 0) {
+        const int tok = shared ? pos0 + row : a.ptok[pos0 + row];
+        v = a.xsum[(size_t)tok * G + g];
+      } else {
+        const float *as = (shared ? a.asum_s : a.asum) + (size_t)(pos0 + row) * (2 * G);
+        v = as[2 * g] + as[2 * g + 1];
+      }
+    }
+    xs_lds[g * BM + row] = -136.0f * v;
+  }
+
+  // B rows of this wave's 4 N-subtiles
+  int brow[4];
+#pragma unroll
+  for (int ns = 0; ns < 4; ++ns)
+    brow[ns] = MODE == 0 ? (ns < 2 ? wn * 32 + ns * 16 : 64 + wn * 32 + (ns - 2) * 16) + m16
+                         : wn * 64 + ns * 16 + m16;
+
+  f32x4 tot[4][4];
+#pragma unroll
+  for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+    for (int ns = 0; ns < 4; ++ns) tot[ms][ns] = f32x4{0.f, 0.f, 0.f, 0.f};
+  uint32_t magic;
+  asm volatile("v_mov_b32 %0, 0x43004300" : "=v"(magic));
+
+  for (int g = 0; g < G; ++g) {
+    if (g + 2 < G) {
+      issue(g + 2);
+      wait_vm<2 * DMA_PER_STAGE>();
+    } else if (g + 1 < G) {
+      wait_vm<DMA_PER_STAGE>();
+    } else {
+      wait_vm<0>();
+    }
+    // stage g complete for every thread (and, at g = 0, the LDS tables)
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    block_barrier();
+    const uint8_t *sa = lds + (g % STAGES) * STAGE;
+    const uint8_t *sb = sa + A_STAGE;
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int ms = 0; ms < 4; ++ms) {
+      const f32x4 c0 = *(const f32x4 *)(xs_lds + g * BM + wm * 64 + ms * 16 + 4 * q);
+#pragma unroll
+      for (int ns = 0; ns < 4; ++ns) acc[ms][ns] = c0;
+    }
+    u32x4 bx[4];
+#pragma unroll
+    for (int ns = 0; ns < 4; ++ns)
+      bx[ns] = *(const u32x4 *)(sb + brow[ns] * 64 + ((q ^ bswz(brow[ns])) << 4)) ^ 0x88888888u;
+    const uint8_t *arow = sa + (wm * 64 + m16) * 256;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      u32x4 af[4], bf[4];
+      const int chunk = ((4 * q + j) ^ m16) << 4;
+#pragma unroll
+      for (int ms = 0; ms < 4; ++ms) af[ms] = *(const u32x4 *)(arow + ms * 16 * 256 + chunk);
+#pragma unroll
+      for (int ns = 0; ns < 4; ++ns) bf[ns] = nib_slice3(bx[ns], j, magic);
+#pragma unroll
+      for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+        for (int ns = 0; ns < 4; ++ns) acc[ms][ns] = mfma_bf16_16x16x32(af[ms], bf[ns], acc[ms][ns]);
+    }
+#pragma unroll
+    for (int ns = 0; ns < 4; ++ns) {
+      const float s = scale_to_f32<SD>(sc_lds[g * BN + brow[ns]]);
+#pragma unroll
+      for (int ms = 0; ms < 4; ++ms) tot[ms][ns] += s * acc[ms][ns];
+    }
+    block_barrier();  // stage g may be overwritten by the DMA issued next iteration
+  }
+
+  // ---- epilogue -------------------------------------------------------
+  // lane (q, m16) of tile (ms, ns) holds rows wm*64 + ms*16 + 4q + r, column m16
+  if (MODE == 0) {
+    uint16_t *dst = shared ? a.act_s : a.act;
+    float rowsum[4][4];
+#pragma unroll
+    for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) rowsum[ms][r] = 0.0f;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int col = nb * 64 + wn * 32 + h * 16 + m16;
+#pragma unroll
+      for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = wm * 64 + ms * 16 + 4 * q + r;
+          const uint16_t v = f32_to_bf16(silu_mul(tot[ms][h][r], tot[ms][h + 2][r]));
+          rowsum[ms][r] += bf16_to_f32(v);
+          if (row < mcnt) dst[(size_t)(pos0 + row) * N + perm32_pos(col)] = v;
+        }
+    }
+    // per-row sum over this wave's 32 columns: reduce over the 16 lanes m16
+#pragma unroll
+    for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float v = rowsum[ms][r];
+        v += __shfl_xor(v, 1, 64);
+        v += __shfl_xor(v, 2, 64);
+        v += __shfl_xor(v, 4, 64);
+        v += __shfl_xor(v, 8, 64);
+        rowsum[ms][r] = v;
+      }
+    if (m16 == 0)
+#pragma unroll
+      for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red_sum[wn * BM + wm * 64 + ms * 16 + 4 * q + r] = rowsum[ms][r];
+    __syncthreads();
+    if (tid < BM && tid < mcnt) {
+      float *as = shared ? a.asum_s : a.asum;
+      // one partial per 64 act columns: slot nb (= group nb/2, half nb%2)
+      as[(size_t)(pos0 + tid) * (N / 64) + nb] = red_sum[tid] + red_sum[BM + tid];
+    }
+  } else {
+    uint16_t *o = a.o;
+#pragma unroll
+    for (int ns = 0; ns < 4; ++ns) {
+      const int col = nb * 128 + wn * 64 + 16 * ns + m16;
+#pragma unroll
+      for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = wm * 64 + ms * 16 + 4 * q + r;
+          if (row < mcnt && col < N) {
+            const size_t orow = shared ? (size_t)a.T * a.k + pos0 + row : (size_t)(pos0 + row);
+            o[orow * a.H + col] = f32_to_bf16(tot[ms][ns][r]);
+          }
+        }
+    }
+  }
+}
+
+}  // namespace
+
+hipError_t launch_expert_gemm(int mode, int scale_dtype, GemmArgs a, int max_tiles,
+                              hipStream_t s) {
+  if (max_tiles <= 0) return hipSuccess;
+  const int Nmax = mode == 0 ? (a.I > a.Is ? a.I : a.Is) : a.H;
+  a.n_nblk = mode == 0 ? (Nmax + 63) / 64 : (Nmax + BN - 1) / BN;
+  const long grid = (long)max_tiles * a.n_nblk;
+  if (grid > 0x7FFFFFFF) return hipErrorInvalidValue;
+  const int Gmax = (mode == 0 ? a.H : (a.I > a.Is ? a.I : a.Is)) / 128;
+  const size_t lds = (size_t)STAGES * STAGE + (((size_t)BN * Gmax * 2 + 15) & ~(size_t)15) +
+                     sizeof(float) * ((size_t)BM * Gmax + 2 * BM);
+  if (lds > 160 * 1024) return hipErrorInvalidValue;
+  if (mode == 0) {
+    if (scale_dtype == AINFER_SCALE_FP16)
+      k_expert_gemm<AINFER_SCALE_FP16, 0><<<(unsigned)grid, 256, lds, s>>>(a);
+    else
+      k_expert_gemm<AINFER_SCALE_BF16, 0><<<(unsigned)grid, 256, lds, s>>>(a);
+  } else {
+    if (scale_dtype == AINFER_SCALE_FP16)
+      k_expert_gemm<AINFER_SCALE_FP16, 1><<<(unsigned)grid, 256, lds, s>>>(a);
+    else
+      k_expert_gemm<AINFER_SCALE_BF16, 1><<<(unsigned)grid, 256, lds, s>>>(a);
+  }
+  return hipGetLastError();
+}

@@ -16,13 +16,37 @@ struct ExpertArgs {
   const uint16_t *a_shared;   // MODE 0: same x; MODE 1: act_s [T][Is]
   uint16_t *act;              // MODE 0 out: [Tk][I] bf16, MFMA order
   uint16_t *act_s;            // MODE 0 out: [T][Is]
-  float *o;                   // MODE 1 out: [Tk + T][H] fp32
+  uint16_t *o;                // MODE 1 out: [Tk + T][H] bf16
   const int32_t *ptok;        // token of each dispatch position
   const int4 *tiles;          // (expert, first position, rows, first row)
   const int32_t *n_tiles;
   int T, k, E, H, I, Is;
   int WK, WR, n_slabs;        // set by the launcher
 };
+
+// Arguments of the prefill GEMM (moe_gemm.hip).
+struct GemmArgs {
+  const uint8_t *w0, *w1;
+  const uint16_t *s0, *s1;
+  const uint8_t *ws0, *ws1;
+  const uint16_t *ss0, *ss1;
+  const uint16_t *a_routed;   // MODE 0: x in MFMA order [T][H]; MODE 1: act [Tk][I]
+  const uint16_t *a_shared;   // MODE 1: act_s [T][Is]
+  uint16_t *act, *act_s;      // MODE 0 out
+  uint16_t *o;                // MODE 1 out: [Tk + T][H] bf16
+  const float *xsum;          // [T][H/128] group sums of x
+  float *asum, *asum_s;       // [Tk][I/64], [T][Is/64] partial sums of act
+  const int32_t *ptok;
+  const int4 *tiles;
+  const int32_t *n_tiles;
+  int T, k, E, H, I, Is;
+  int n_nblk;                 // set by the launcher
+};
+hipError_t launch_expert_gemm(int mode, int scale_dtype, GemmArgs a, int max_tiles,
+                              hipStream_t s);
+// token-tile height of the prefill GEMM and the T above which it is used
+constexpr int GEMM_MT = 128;
+constexpr int GEMM_MIN_T = 256;
 
 // Outputs of the dispatch stage.  tiles: (expert, first position, rows,
 // first row within the expert); shared-expert tiles carry expert id E and a
@@ -51,10 +75,11 @@ hipError_t launch_router(const void *x, const void *rw, const float *bias, const
 // the last block also runs the dispatch.  approx [T][E] and wnorm [E] are
 // scratch.
 bool router_supported(int H, int E);
+// xsum (may be NULL): [T][H/128] group sums of x for the prefill GEMM.
 hipError_t launch_router_fast(const void *x, const void *rw, const float *bias, const void *gw,
                               float *approx, float *wnorm, int32_t *idx, float *w, float *sg,
-                              void *xperm, int T, int H, int E, int k, int has_shared,
-                              const DispatchOut *fused, hipStream_t s);
+                              void *xperm, float *xsum, int T, int H, int E, int k,
+                              int has_shared, const DispatchOut *fused, hipStream_t s);
 // Small T: canonical logits of all experts on VALU (k_router_logits), then the
 // same selection without the refine.  logits [T][E], sg_logit [T] out.
 hipError_t launch_router_exact(const void *x, const void *rw, const float *bias, const void *gw,
@@ -66,7 +91,7 @@ constexpr int EXACT_ROUTER_MAX_T = 16;
 hipError_t launch_dispatch(const int32_t *idx, int T, int k, int E, int mt, int has_shared,
                            int32_t *chunk_counts, int32_t *rank, const DispatchOut &ds,
                            hipStream_t s);
-hipError_t launch_combine(const float *o, const int32_t *inv, const float *w, const float *sg,
+hipError_t launch_combine(const uint16_t *o, const int32_t *inv, const float *w, const float *sg,
                           int has_shared, const void *resid, void *y, int T, int k, int H,
                           hipStream_t s);
 // false when the shape has no wave geometry (more than 8 waves along K)

@@ -331,7 +331,7 @@ hipError_t launch_dispatch(const int32_t *idx, int T, int k, int E, int mt, int 
 // (+ residual), in slot order with fp32 fma, bf16 out.  One thread per 4
 // columns.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_combine(const float *__restrict__ o,
+__global__ __launch_bounds__(256) void k_combine(const uint16_t *__restrict__ o,
                                                  const int32_t *__restrict__ inv,
                                                  const float *__restrict__ w,
                                                  const float *__restrict__ sg, int has_shared,
@@ -353,13 +353,17 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ o,
 #pragma unroll
   for (int j = 0; j < 32; ++j)
     if (j < k) {
-      const f32x4 v = *(const f32x4 *)(o + (size_t)pos[j] * H + h0);
+      const uint2 r = *(const uint2 *)(o + (size_t)pos[j] * H + h0);
+      const float v[4] = {__uint_as_float(r.x << 16), __uint_as_float(r.x & 0xFFFF0000u),
+                          __uint_as_float(r.y << 16), __uint_as_float(r.y & 0xFFFF0000u)};
 #pragma unroll
       for (int q = 0; q < 4; ++q) acc[q] = __builtin_fmaf(wj[j], v[q], acc[q]);
     }
   if (has_shared) {
     const float g = sg[t];
-    const f32x4 v = *(const f32x4 *)(o + ((size_t)T * k + t) * H + h0);
+    const uint2 r = *(const uint2 *)(o + ((size_t)T * k + t) * H + h0);
+    const float v[4] = {__uint_as_float(r.x << 16), __uint_as_float(r.x & 0xFFFF0000u),
+                        __uint_as_float(r.y << 16), __uint_as_float(r.y & 0xFFFF0000u)};
 #pragma unroll
     for (int q = 0; q < 4; ++q) acc[q] = __builtin_fmaf(g, v[q], acc[q]);
   }
@@ -376,7 +380,7 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ o,
   *(uint2 *)(y + (size_t)t * H + h0) = out;
 }
 
-hipError_t launch_combine(const float *o, const int32_t *inv, const float *w, const float *sg,
+hipError_t launch_combine(const uint16_t *o, const int32_t *inv, const float *w, const float *sg,
                           int has_shared, const void *resid, void *y, int T, int k, int H,
                           hipStream_t s) {
   if (T == 0) return hipSuccess;

@@ -201,7 +201,8 @@ __global__ __launch_bounds__(256) void k_select(const float *__restrict__ approx
                                                 int32_t *__restrict__ topk_idx,
                                                 float *__restrict__ topk_w,
                                                 float *__restrict__ sgate,
-                                                uint16_t *__restrict__ xperm, int T, int E,
+                                                uint16_t *__restrict__ xperm,
+                                                float *__restrict__ xsum, int T, int E,
                                                 int k, int H, int has_shared, DispatchOut ds,
                                                 int fused) {
   __shared__ int cl[SEL_WAVES][1024];
@@ -348,6 +349,17 @@ __global__ __launch_bounds__(256) void k_select(const float *__restrict__ approx
         dst[1] = u32x4{out[4], out[5], out[6], out[7]};
         dst[2] = u32x4{out[8], out[9], out[10], out[11]};
         dst[3] = u32x4{out[12], out[13], out[14], out[15]};
+        if (xsum) {
+          // sum of the 128-wide group: this block's 32 values, then the 4
+          // consecutive lanes holding the group's blocks (fixed order)
+          float bs = 0.0f;
+#pragma unroll
+          for (int i2 = 0; i2 < 16; ++i2)
+            bs += __uint_as_float(in[i2] << 16) + __uint_as_float(in[i2] & 0xFFFF0000u);
+          bs += __shfl_xor(bs, 1, 64);
+          bs += __shfl_xor(bs, 2, 64);
+          if ((b & 3) == 0) xsum[(size_t)t * (H >> 7) + (b >> 2)] = bs;
+        }
       }
     }
   }
@@ -370,12 +382,12 @@ template <int NV, bool EXACT>
 hipError_t launch_select_nv(int ch, unsigned grid, const float *approx, const float *sgl,
                             const float *wnorm,
                             const void *x, const void *rw, const float *bias, const void *gw,
-                            int32_t *idx, float *w, float *sg, void *xperm, int T, int E,
-                            int k, int H, int has_shared, const DispatchOut &ds, int fused,
+                            int32_t *idx, float *w, float *sg, void *xperm, float *xsum, int T,
+                            int E, int k, int H, int has_shared, const DispatchOut &ds, int fused,
                             hipStream_t s) {
 #define SEL_ARGS                                                                            \
   approx, sgl, wnorm, (const uint16_t *)x, (const uint16_t *)rw, bias, (const uint16_t *)gw, idx, \
-      w, sg, (uint16_t *)xperm, T, E, k, H, has_shared, ds, fused
+      w, sg, (uint16_t *)xperm, xsum, T, E, k, H, has_shared, ds, fused
   switch (ch) {
   case 1: k_select<NV, 1, EXACT><<<grid, 256, 0, s>>>(SEL_ARGS); break;
   case 2: k_select<NV, 2, EXACT><<<grid, 256, 0, s>>>(SEL_ARGS); break;
@@ -393,8 +405,9 @@ bool router_supported(int H, int E) { return H % 128 == 0 && H <= 4096 && E <= 1
 template <bool EXACT>
 hipError_t launch_select(const float *approx, const float *sgl, const float *wnorm,
                          const void *x, const void *rw, const float *bias, const void *gw,
-                         int32_t *idx, float *w, float *sg, void *xperm, int T, int H, int E,
-                         int k, int has_shared, const DispatchOut *fused, hipStream_t s) {
+                         int32_t *idx, float *w, float *sg, void *xperm, float *xsum, int T,
+                         int H, int E, int k, int has_shared, const DispatchOut *fused,
+                         hipStream_t s) {
   const int ch = (H / 8 + 63) / 64;  // chunks per lane
   const int chp = ch <= 1 ? 1 : (ch <= 2 ? 2 : (ch <= 4 ? 4 : 8));
   const int nv = (E + 63) / 64;
@@ -405,7 +418,7 @@ hipError_t launch_select(const float *approx, const float *sgl, const float *wno
   const int fz = fused ? 1 : 0;
 #define SEL_CALL(NVV)                                                                        \
   launch_select_nv<NVV, EXACT>(chp, g, approx, sgl, wnorm, x, rw, bias, gw, idx, w, sg, xperm, \
-                               T, E, k, H, has_shared, ds, fz, s)
+                               xsum, T, E, k, H, has_shared, ds, fz, s)
   if (nv <= 1) return SEL_CALL(1);
   if (nv <= 2) return SEL_CALL(2);
   if (nv <= 4) return SEL_CALL(4);
@@ -416,8 +429,8 @@ hipError_t launch_select(const float *approx, const float *sgl, const float *wno
 
 hipError_t launch_router_fast(const void *x, const void *rw, const float *bias, const void *gw,
                               float *approx, float *wnorm, int32_t *idx, float *w, float *sg,
-                              void *xperm, int T, int H, int E, int k, int has_shared,
-                              const DispatchOut *fused, hipStream_t s) {
+                              void *xperm, float *xsum, int T, int H, int E, int k,
+                              int has_shared, const DispatchOut *fused, hipStream_t s) {
   if (T == 0) return hipSuccess;
   // ---- approximate logits + row norms ------------------------------------
   const int MS = T <= 16 ? 1 : (T <= 32 ? 2 : 4);
@@ -443,8 +456,8 @@ hipError_t launch_router_fast(const void *x, const void *rw, const float *bias, 
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
   // ---- refine + select ------------------------------------------------------
-  return launch_select<false>(approx, nullptr, wnorm, x, rw, bias, gw, idx, w, sg, xperm, T, H,
-                              E, k, has_shared, fused, s);
+  return launch_select<false>(approx, nullptr, wnorm, x, rw, bias, gw, idx, w, sg, xperm, xsum,
+                              T, H, E, k, has_shared, fused, s);
 }
 
 hipError_t launch_router_exact(const void *x, const void *rw, const float *bias, const void *gw,
@@ -455,6 +468,6 @@ hipError_t launch_router_exact(const void *x, const void *rw, const float *bias,
   hipError_t err = launch_router(x, rw, bias, gw, logits, sg_logit,
                                  fused ? fused->ticket : nullptr, T, H, E, s);
   if (err != hipSuccess) return err;
-  return launch_select<true>(logits, sg_logit, nullptr, x, rw, bias, gw, idx, w, sg, xperm, T, H,
-                             E, k, has_shared, fused, s);
+  return launch_select<true>(logits, sg_logit, nullptr, x, rw, bias, gw, idx, w, sg, xperm,
+                             nullptr, T, H, E, k, has_shared, fused, s);
 }

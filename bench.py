@@ -151,6 +151,7 @@ def main():
     ap.add_argument("--tokens", default="1,4,16", help="c1 decode batch sizes")
     ap.add_argument("--prefill-steps", type=int, default=10)
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     args = ap.parse_args()
@@ -172,7 +173,7 @@ def main():
     torch.cuda.synchronize()
 
     decode = {}
-    for T in [int(v) for v in args.tokens.split(",")]:
+    for T in ([] if args.no_decode else [int(v) for v in args.tokens.split(",")]):
         log(f"[bench] c1 decode T={T}")
         ms, st, U = run_decode(layers, c1, T, args.steps, args.warmup, 64, stream)
         nbytes = algorithmic_bytes(c1, T, round(U))
@@ -215,6 +216,9 @@ def main():
         cpu = cpu_baseline(layers[0], c1, 1, args.cpu_seconds)
         log(f"[bench]   {json.dumps(cpu)}")
 
+    if not decode:
+        print(json.dumps({"prefill_c2_T4096": prefill}), flush=True)
+        return
     d1 = decode[min(decode)]
     out = {
         "metric": METRIC,
