@@ -110,8 +110,8 @@ Layout layout_of(const ainfer_moe_shape &s, int Tm) {
   L.h = take(T * H * 2);
   L.wnorm = take(E * 4);
   L.xsum = take(T * (H / 128) * 4);
-  L.asum = take(T * k * (s.inter / 64) * 4);
-  L.asum_s = take(T * (size_t)(s.shared_inter > 0 ? s.shared_inter / 64 : 1) * 4);
+  L.asum = take(T * k * (s.inter / 32) * 4);
+  L.asum_s = take(T * (size_t)(s.shared_inter > 0 ? s.shared_inter / 32 : 1) * 4);
   L.total = off;
   return L;
 }

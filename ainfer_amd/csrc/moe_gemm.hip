@@ -29,13 +29,23 @@
 
 namespace {
 
-constexpr int BM = 128;               // tokens per tile
-constexpr int BN = 128;               // weight rows per block
-constexpr int STAGES = 3;
-constexpr int A_STAGE = BM * 256;     // bytes
-constexpr int B_STAGE = BN * 64;      // bytes
-constexpr int STAGE = A_STAGE + B_STAGE;
-constexpr int DMA_PER_STAGE = (A_STAGE + B_STAGE) / (256 * 16);  // per thread: 10
+constexpr int BM = 128;  // tokens per tile
+
+// Block geometry: 2 x WN waves; BN = 64 * WN weight rows per block.
+template <int WN, int STAGES_>
+struct Geo {
+  static constexpr int NW = 2 * WN;                  // waves
+  static constexpr int THREADS = 64 * NW;
+  static constexpr int BN = 64 * WN;                 // weight rows
+  static constexpr int STAGES = STAGES_;
+  static constexpr int A_STAGE = BM * 256;           // bytes per group
+  static constexpr int B_STAGE = BN * 64;            // bytes per group
+  static constexpr int STAGE = A_STAGE + B_STAGE;
+  static constexpr int A_DMA = A_STAGE / (THREADS * 16);  // DMA per thread per stage
+  static constexpr int B_DMA = B_STAGE / (THREADS * 16);
+  static constexpr int DMA = A_DMA + B_DMA;
+  static constexpr int COLS = 32 * WN;               // MODE 0: act columns per block
+};
 
 __device__ __forceinline__ void dma16(const void *g, uint32_t lds_addr) {
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
@@ -72,8 +82,11 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
   return g / (1.0f + expf(-g)) * u;
 }
 
-template <int SD, int MODE>
-__global__ __launch_bounds__(256) void k_expert_gemm(GemmArgs a) {
+template <int SD, int MODE, int WN, int STAGES_>
+__global__ __launch_bounds__(128 * WN) void k_expert_gemm(GemmArgs a) {
+  using Gm = Geo<WN, STAGES_>;
+  constexpr int BN = Gm::BN, STAGES = Gm::STAGES, A_STAGE = Gm::A_STAGE, STAGE = Gm::STAGE;
+  constexpr int NW = Gm::NW, THREADS = Gm::THREADS, COLS = Gm::COLS;
   // dynamic LDS: STAGES x (A | B) ring, scales[G][BN] fp16, xs[G][BM] fp32
   // (group-major: a lane's 4 rows are one 16-byte read), red_sum[2][BM] fp32
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -89,7 +102,7 @@ __global__ __launch_bounds__(256) void k_expert_gemm(GemmArgs a) {
   const int N = MODE == 0 ? (shared ? a.Is : a.I) : a.H;
   const int K = MODE == 0 ? a.H : (shared ? a.Is : a.I);
   const int G = K >> 7;
-  if (nb * (MODE == 0 ? 64 : 128) >= N) return;
+  if (nb * (MODE == 0 ? COLS : BN) >= N) return;
 
   const uint32_t lds0 = (uint32_t)(uintptr_t)lds;
   uint16_t *sc_lds = (uint16_t *)(lds + STAGES * STAGE);
@@ -99,15 +112,15 @@ __global__ __launch_bounds__(256) void k_expert_gemm(GemmArgs a) {
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
-  const int wm = wave & 1, wn = wave >> 1;
+  const int wm = wave & 1, wn = wave >> 1;  // 2 token waves x WN row waves
   const int m16 = lane & 15, q = lane >> 4;
 
-  // ---- per-thread DMA sources: 8 A slots and 2 B slots per stage ----------
-  // slot s = (i*4 + wave)*64 + lane, 16 bytes each
-  const uint8_t *asrc[8];
+  // ---- per-thread DMA sources: A_DMA A slots and B_DMA B slots per stage ---
+  // slot s = (i*NW + wave)*64 + lane, 16 bytes each
+  const uint8_t *asrc[Gm::A_DMA];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int s = (i * 4 + wave) * 64 + lane;
+  for (int i = 0; i < Gm::A_DMA; ++i) {
+    const int s = (i * NW + wave) * 64 + lane;
     const int r = s >> 4, c = (s & 15) ^ (r & 15);
     const int rr = min(r, mcnt - 1);
     const uint16_t *row;
@@ -120,20 +133,20 @@ __global__ __launch_bounds__(256) void k_expert_gemm(GemmArgs a) {
     asrc[i] = (const uint8_t *)row + c * 16;
   }
   const size_t rowb = (size_t)K / 2;
-  const uint8_t *bsrc[2];
+  const uint8_t *bsrc[Gm::B_DMA];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int s = (i * 4 + wave) * 64 + lane;
+  for (int i = 0; i < Gm::B_DMA; ++i) {
+    const int s = (i * NW + wave) * 64 + lane;
     const int r = s >> 2, qq = (s & 3) ^ bswz(r);
     const uint8_t *w;
     int row;
-    if (MODE == 0) {
-      w = r < 64 ? (shared ? a.ws0 : a.w0 + (size_t)e * N * rowb)
-                 : (shared ? a.ws1 : a.w1 + (size_t)e * N * rowb);
-      row = nb * 64 + (r & 63);
+    if (MODE == 0) {  // B-rows [0, COLS) gate, [COLS, 2 COLS) up
+      w = r < COLS ? (shared ? a.ws0 : a.w0 + (size_t)e * N * rowb)
+                   : (shared ? a.ws1 : a.w1 + (size_t)e * N * rowb);
+      row = nb * COLS + (r % COLS);
     } else {
       w = shared ? a.ws0 : a.w0 + (size_t)e * N * rowb;
-      row = nb * 128 + r;
+      row = nb * BN + r;
     }
     row = min(row, N - 1);
     bsrc[i] = w + (size_t)row * rowb + qq * 16;
@@ -141,31 +154,31 @@ __global__ __launch_bounds__(256) void k_expert_gemm(GemmArgs a) {
   auto issue = [&](int g) {  // DMA of group g into stage g % STAGES
     const uint32_t base = lds0 + (uint32_t)(g % STAGES) * STAGE;
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      dma16(asrc[i] + g * 256, base + (uint32_t)((i * 4 + wave) * 1024));
+    for (int i = 0; i < Gm::A_DMA; ++i)
+      dma16(asrc[i] + g * 256, base + (uint32_t)((i * NW + wave) * 1024));
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-      dma16(bsrc[i] + g * 64, base + A_STAGE + (uint32_t)((i * 4 + wave) * 1024));
+    for (int i = 0; i < Gm::B_DMA; ++i)
+      dma16(bsrc[i] + g * 64, base + A_STAGE + (uint32_t)((i * NW + wave) * 1024));
   };
 
-  // ---- prologue: groups 0 and 1 in flight; scales and group sums to LDS ---
+  // ---- prologue: the first STAGES-1 groups in flight; tables to LDS -------
   issue(0);
-  if (G > 1) issue(1);
-  for (int idx = tid; idx < BN * G; idx += 256) {
+  if (STAGES > 2 && G > 1) issue(1);
+  for (int idx = tid; idx < BN * G; idx += THREADS) {
     const int r = idx / G, g = idx % G;
     const uint16_t *sc;
     int row;
     if (MODE == 0) {
-      sc = r < 64 ? (shared ? a.ss0 : a.s0 + (size_t)e * N * G)
-                  : (shared ? a.ss1 : a.s1 + (size_t)e * N * G);
-      row = nb * 64 + (r & 63);
+      sc = r < COLS ? (shared ? a.ss0 : a.s0 + (size_t)e * N * G)
+                    : (shared ? a.ss1 : a.s1 + (size_t)e * N * G);
+      row = nb * COLS + (r % COLS);
     } else {
       sc = shared ? a.ss0 : a.s0 + (size_t)e * N * G;
-      row = nb * 128 + r;
+      row = nb * BN + r;
     }
     sc_lds[g * BN + r] = sc[(size_t)min(row, N - 1) * G + g];
   }
-  for (int idx = tid; idx < BM * G; idx += 256) {
+  for (int idx = tid; idx < BM * G; idx += THREADS) {
     const int row = idx / G, g = idx % G;
     float v = 0.0f;
     if (row < mcnt) {
@@ -173,8 +186,9 @@ __global__ __launch_bounds__(256) void k_expert_gemm(GemmArgs a) {
         const int tok = shared ? pos0 + row : a.ptok[pos0 + row];
         v = a.xsum[(size_t)tok * G + g];
       } else {
-        const float *as = (shared ? a.asum_s : a.asum) + (size_t)(pos0 + row) * (2 * G);
-        v = as[2 * g] + as[2 * g + 1];
+        // act partial sums: a.aslots per 128-wide group, added in order
+        const float *as = (shared ? a.asum_s : a.asum) + (size_t)(pos0 + row) * (a.aslots * G);
+        for (int j = 0; j < a.aslots; ++j) v += as[a.aslots * g + j];
       }
     }
     xs_lds[g * BM + row] = -136.0f * v;
@@ -184,7 +198,7 @@ __global__ __launch_bounds__(256) void k_expert_gemm(GemmArgs a) {
   int brow[4];
 #pragma unroll
   for (int ns = 0; ns < 4; ++ns)
-    brow[ns] = MODE == 0 ? (ns < 2 ? wn * 32 + ns * 16 : 64 + wn * 32 + (ns - 2) * 16) + m16
+    brow[ns] = MODE == 0 ? (ns < 2 ? wn * 32 + ns * 16 : COLS + wn * 32 + (ns - 2) * 16) + m16
                          : wn * 64 + ns * 16 + m16;
 
   f32x4 tot[4][4];
@@ -196,11 +210,12 @@ __global__ __launch_bounds__(256) void k_expert_gemm(GemmArgs a) {
   asm volatile("v_mov_b32 %0, 0x43004300" : "=v"(magic));
 
   for (int g = 0; g < G; ++g) {
-    if (g + 2 < G) {
-      issue(g + 2);
-      wait_vm<2 * DMA_PER_STAGE>();
-    } else if (g + 1 < G) {
-      wait_vm<DMA_PER_STAGE>();
+    // keep STAGES-1 groups in flight; wait for group g
+    if (g + STAGES - 1 < G) {
+      issue(g + STAGES - 1);
+      wait_vm<(STAGES - 1) * Gm::DMA>();
+    } else if (STAGES > 2 && g + 1 < G) {
+      wait_vm<Gm::DMA>();
     } else {
       wait_vm<0>();
     }
@@ -254,7 +269,7 @@ __global__ __launch_bounds__(256) void k_expert_gemm(GemmArgs a) {
       for (int r = 0; r < 4; ++r) rowsum[ms][r] = 0.0f;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const int col = nb * 64 + wn * 32 + h * 16 + m16;
+      const int col = nb * COLS + wn * 32 + h * 16 + m16;
 #pragma unroll
       for (int ms = 0; ms < 4; ++ms)
 #pragma unroll
@@ -285,14 +300,17 @@ __global__ __launch_bounds__(256) void k_expert_gemm(GemmArgs a) {
     __syncthreads();
     if (tid < BM && tid < mcnt) {
       float *as = shared ? a.asum_s : a.asum;
-      // one partial per 64 act columns: slot nb (= group nb/2, half nb%2)
-      as[(size_t)(pos0 + tid) * (N / 64) + nb] = red_sum[tid] + red_sum[BM + tid];
+      // one partial per COLS act columns (slot nb), row waves summed in order
+      float v = 0.0f;
+#pragma unroll
+      for (int w = 0; w < WN; ++w) v += red_sum[w * BM + tid];
+      as[(size_t)(pos0 + tid) * (N / COLS) + nb] = v;
     }
   } else {
     uint16_t *o = a.o;
 #pragma unroll
     for (int ns = 0; ns < 4; ++ns) {
-      const int col = nb * 128 + wn * 64 + 16 * ns + m16;
+      const int col = nb * BN + wn * 64 + 16 * ns + m16;
 #pragma unroll
       for (int ms = 0; ms < 4; ++ms)
 #pragma unroll
@@ -307,29 +325,39 @@ __global__ __launch_bounds__(256) void k_expert_gemm(GemmArgs a) {
   }
 }
 
-}  // namespace
-
-hipError_t launch_expert_gemm(int mode, int scale_dtype, GemmArgs a, int max_tiles,
-                              hipStream_t s) {
-  if (max_tiles <= 0) return hipSuccess;
+template <int WN, int STAGES_>
+hipError_t launch_geo(int mode, int scale_dtype, GemmArgs a, int max_tiles, hipStream_t s) {
+  using Gm = Geo<WN, STAGES_>;
   const int Nmax = mode == 0 ? (a.I > a.Is ? a.I : a.Is) : a.H;
-  a.n_nblk = mode == 0 ? (Nmax + 63) / 64 : (Nmax + BN - 1) / BN;
+  a.n_nblk = mode == 0 ? (Nmax + Gm::COLS - 1) / Gm::COLS : (Nmax + Gm::BN - 1) / Gm::BN;
+  a.aslots = 128 / Gm::COLS;  // act partial sums per 128-wide group (MODE 0 writes them)
   const long grid = (long)max_tiles * a.n_nblk;
   if (grid > 0x7FFFFFFF) return hipErrorInvalidValue;
   const int Gmax = (mode == 0 ? a.H : (a.I > a.Is ? a.I : a.Is)) / 128;
-  const size_t lds = (size_t)STAGES * STAGE + (((size_t)BN * Gmax * 2 + 15) & ~(size_t)15) +
-                     sizeof(float) * ((size_t)BM * Gmax + 2 * BM);
+  const size_t lds = (size_t)Gm::STAGES * Gm::STAGE +
+                     (((size_t)Gm::BN * Gmax * 2 + 15) & ~(size_t)15) +
+                     sizeof(float) * ((size_t)BM * Gmax + (size_t)WN * BM);
   if (lds > 160 * 1024) return hipErrorInvalidValue;
   if (mode == 0) {
     if (scale_dtype == AINFER_SCALE_FP16)
-      k_expert_gemm<AINFER_SCALE_FP16, 0><<<(unsigned)grid, 256, lds, s>>>(a);
+      k_expert_gemm<AINFER_SCALE_FP16, 0, WN, STAGES_><<<(unsigned)grid, Gm::THREADS, lds, s>>>(a);
     else
-      k_expert_gemm<AINFER_SCALE_BF16, 0><<<(unsigned)grid, 256, lds, s>>>(a);
+      k_expert_gemm<AINFER_SCALE_BF16, 0, WN, STAGES_><<<(unsigned)grid, Gm::THREADS, lds, s>>>(a);
   } else {
     if (scale_dtype == AINFER_SCALE_FP16)
-      k_expert_gemm<AINFER_SCALE_FP16, 1><<<(unsigned)grid, 256, lds, s>>>(a);
+      k_expert_gemm<AINFER_SCALE_FP16, 1, WN, STAGES_><<<(unsigned)grid, Gm::THREADS, lds, s>>>(a);
     else
-      k_expert_gemm<AINFER_SCALE_BF16, 1><<<(unsigned)grid, 256, lds, s>>>(a);
+      k_expert_gemm<AINFER_SCALE_BF16, 1, WN, STAGES_><<<(unsigned)grid, Gm::THREADS, lds, s>>>(a);
   }
   return hipGetLastError();
+}
+
+}  // namespace
+
+// Both GEMM modes of one forward must use the same geometry (MODE 1 reads
+// the act partial sums MODE 0 wrote).
+hipError_t launch_expert_gemm(int mode, int scale_dtype, GemmArgs a, int max_tiles,
+                              hipStream_t s) {
+  if (max_tiles <= 0) return hipSuccess;
+  return launch_geo<GEMM_WN, GEMM_STAGES>(mode, scale_dtype, a, max_tiles, s);
 }

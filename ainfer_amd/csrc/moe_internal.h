@@ -35,17 +35,23 @@ struct GemmArgs {
   uint16_t *act, *act_s;      // MODE 0 out
   uint16_t *o;                // MODE 1 out: [Tk + T][H] bf16
   const float *xsum;          // [T][H/128] group sums of x
-  float *asum, *asum_s;       // [Tk][I/64], [T][Is/64] partial sums of act
+  float *asum, *asum_s;       // [Tk][I/32], [T][Is/32] (max) partial sums of act
   const int32_t *ptok;
   const int4 *tiles;
   const int32_t *n_tiles;
   int T, k, E, H, I, Is;
-  int n_nblk;                 // set by the launcher
+  int n_nblk, aslots;         // set by the launcher
 };
 hipError_t launch_expert_gemm(int mode, int scale_dtype, GemmArgs a, int max_tiles,
                               hipStream_t s);
 // token-tile height of the prefill GEMM and the T above which it is used
 constexpr int GEMM_MT = 128;
+#ifndef GEMM_WN
+#define GEMM_WN 4       // row waves per GEMM block (2 x GEMM_WN waves)
+#endif
+#ifndef GEMM_STAGES
+#define GEMM_STAGES 2   // LDS ring depth
+#endif
 constexpr int GEMM_MIN_T = 256;
 
 // Outputs of the dispatch stage.  tiles: (expert, first position, rows,
