@@ -164,34 +164,74 @@ __global__ __launch_bounds__(128 * WN) void k_expert_gemm(GemmArgs a) {
   // ---- prologue: the first STAGES-1 groups in flight; tables to LDS -------
   issue(0);
   if (STAGES > 2 && G > 1) issue(1);
-  for (int idx = tid; idx < BN * G; idx += THREADS) {
-    const int r = idx / G, g = idx % G;
-    const uint16_t *sc;
-    int row;
-    if (MODE == 0) {
-      sc = r < COLS ? (shared ? a.ss0 : a.s0 + (size_t)e * N * G)
-                    : (shared ? a.ss1 : a.s1 + (size_t)e * N * G);
-      row = nb * COLS + (r % COLS);
-    } else {
-      sc = shared ? a.ss0 : a.s0 + (size_t)e * N * G;
-      row = nb * BN + r;
-    }
-    sc_lds[g * BN + r] = sc[(size_t)min(row, N - 1) * G + g];
-  }
-  for (int idx = tid; idx < BM * G; idx += THREADS) {
-    const int row = idx / G, g = idx % G;
-    float v = 0.0f;
-    if (row < mcnt) {
+  // Tables: every load is issued before the first use (unrolled, clamped
+  // indices, no per-lane branches), so the block pays one latency, not one
+  // per element.  G <= 32.
+  {
+    // idx / G through a float reciprocal: idx < 2^13 and G <= 32, so
+    // (idx + 0.5) / G is at least 1/64 away from an integer and the float
+    // product truncates to the exact quotient.
+    const float rG = 1.0f / (float)G;
+    auto divG = [&](int idx) { return (int)(((float)idx + 0.5f) * rG); };
+    constexpr int SC_IT = BN * 32 / THREADS;
+    const int nsc = BN * G;
+    uint16_t scv[SC_IT];
+#pragma unroll
+    for (int i = 0; i < SC_IT; ++i) {
+      const int idx = min(tid + i * THREADS, nsc - 1);
+      const int r = divG(idx), g = idx - r * G;
+      const uint16_t *sc;
+      int row;
       if (MODE == 0) {
-        const int tok = shared ? pos0 + row : a.ptok[pos0 + row];
-        v = a.xsum[(size_t)tok * G + g];
+        sc = r < COLS ? (shared ? a.ss0 : a.s0 + (size_t)e * N * G)
+                      : (shared ? a.ss1 : a.s1 + (size_t)e * N * G);
+        row = nb * COLS + (r % COLS);
       } else {
-        // act partial sums: a.aslots per 128-wide group, added in order
-        const float *as = (shared ? a.asum_s : a.asum) + (size_t)(pos0 + row) * (a.aslots * G);
-        for (int j = 0; j < a.aslots; ++j) v += as[a.aslots * g + j];
+        sc = shared ? a.ss0 : a.s0 + (size_t)e * N * G;
+        row = nb * BN + r;
+      }
+      scv[i] = sc[(size_t)min(row, N - 1) * G + g];
+    }
+    constexpr int XS_IT = BM * 32 / THREADS;
+    const int nxs = BM * G;
+    float xv[XS_IT];
+    if (MODE == 0) {
+      int tok[XS_IT];
+#pragma unroll
+      for (int i = 0; i < XS_IT; ++i) {
+        const int row = min(divG(min(tid + i * THREADS, nxs - 1)), mcnt - 1);
+        tok[i] = shared ? pos0 + row : a.ptok[pos0 + row];
+      }
+#pragma unroll
+      for (int i = 0; i < XS_IT; ++i) {
+        const int idx = min(tid + i * THREADS, nxs - 1);
+        xv[i] = a.xsum[(size_t)tok[i] * G + (idx - divG(idx) * G)];
+      }
+    } else {
+      // act partial sums: a.aslots per 128-wide group, added in order
+      const float *asb = shared ? a.asum_s : a.asum;
+#pragma unroll
+      for (int i = 0; i < XS_IT; ++i) {
+        const int idx = min(tid + i * THREADS, nxs - 1);
+        const int q0 = divG(idx), row = min(q0, mcnt - 1), g = idx - q0 * G;
+        const float *as = asb + (size_t)(pos0 + row) * (a.aslots * G) + a.aslots * g;
+        float v = as[0];
+        for (int j = 1; j < a.aslots; ++j) v += as[j];
+        xv[i] = v;
       }
     }
-    xs_lds[g * BM + row] = -136.0f * v;
+#pragma unroll
+    for (int i = 0; i < SC_IT; ++i) {
+      const int idx = tid + i * THREADS;
+      const int r = divG(idx);
+      if (idx < nsc) sc_lds[(idx - r * G) * BN + r] = scv[i];
+    }
+#pragma unroll
+    for (int i = 0; i < XS_IT; ++i) {
+      const int idx = tid + i * THREADS;
+      const int row = divG(idx);
+      if (idx < nxs) xs_lds[(idx - row * G) * BM + row] = row < mcnt ? -136.0f * xv[i] : 0.0f;
+    }
   }
 
   // B rows of this wave's 4 N-subtiles
@@ -259,9 +299,13 @@ __global__ __launch_bounds__(128 * WN) void k_expert_gemm(GemmArgs a) {
   }
 
   // ---- epilogue -------------------------------------------------------
-  // lane (q, m16) of tile (ms, ns) holds rows wm*64 + ms*16 + 4q + r, column m16
+  // lane (q, m16) of tile (ms, ns) holds rows wm*64 + ms*16 + 4q + r, column
+  // m16.  Results are staged in the (now idle) LDS ring and leave as 16-byte
+  // row chunks.  The loop's final barrier orders the staging after every
+  // wave's last read of the ring.
   if (MODE == 0) {
-    uint16_t *dst = shared ? a.act_s : a.act;
+    constexpr int OST = COLS * 2 + 16;  // staged row stride, bytes
+    static_assert(BM * OST <= STAGES * STAGE, "staging exceeds the ring");
     float rowsum[4][4];
 #pragma unroll
     for (int ms = 0; ms < 4; ++ms)
@@ -269,7 +313,8 @@ __global__ __launch_bounds__(128 * WN) void k_expert_gemm(GemmArgs a) {
       for (int r = 0; r < 4; ++r) rowsum[ms][r] = 0.0f;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const int col = nb * COLS + wn * 32 + h * 16 + m16;
+      // within a 32-aligned block of columns, MFMA order is block-local
+      const int p = perm32_pos(wn * 32 + h * 16 + m16);
 #pragma unroll
       for (int ms = 0; ms < 4; ++ms)
 #pragma unroll
@@ -277,7 +322,7 @@ __global__ __launch_bounds__(128 * WN) void k_expert_gemm(GemmArgs a) {
           const int row = wm * 64 + ms * 16 + 4 * q + r;
           const uint16_t v = f32_to_bf16(silu_mul(tot[ms][h][r], tot[ms][h + 2][r]));
           rowsum[ms][r] += bf16_to_f32(v);
-          if (row < mcnt) dst[(size_t)(pos0 + row) * N + perm32_pos(col)] = v;
+          *(uint16_t *)(lds + row * OST + p * 2) = v;
         }
     }
     // per-row sum over this wave's 32 columns: reduce over the 16 lanes m16
@@ -298,6 +343,15 @@ __global__ __launch_bounds__(128 * WN) void k_expert_gemm(GemmArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) red_sum[wn * BM + wm * 64 + ms * 16 + 4 * q + r] = rowsum[ms][r];
     __syncthreads();
+    uint16_t *dst = shared ? a.act_s : a.act;
+    constexpr int CPR = COLS / 8;  // 16-byte chunks per row
+#pragma unroll
+    for (int i = 0; i < BM * CPR / THREADS; ++i) {
+      const int idx = tid + i * THREADS, row = idx / CPR, c = idx % CPR;
+      if (row < mcnt)
+        *(u32x4 *)(dst + (size_t)(pos0 + row) * N + nb * COLS + c * 8) =
+            *(const u32x4 *)(lds + row * OST + c * 16);
+    }
     if (tid < BM && tid < mcnt) {
       float *as = shared ? a.asum_s : a.asum;
       // one partial per COLS act columns (slot nb), row waves summed in order
@@ -307,20 +361,29 @@ __global__ __launch_bounds__(128 * WN) void k_expert_gemm(GemmArgs a) {
       as[(size_t)(pos0 + tid) * (N / COLS) + nb] = v;
     }
   } else {
-    uint16_t *o = a.o;
+    constexpr int OST = BN * 2 + 16;
+    static_assert(BM * OST <= STAGES * STAGE, "staging exceeds the ring");
 #pragma unroll
     for (int ns = 0; ns < 4; ++ns) {
-      const int col = nb * BN + wn * 64 + 16 * ns + m16;
+      const int cl = wn * 64 + 16 * ns + m16;
 #pragma unroll
       for (int ms = 0; ms < 4; ++ms)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int row = wm * 64 + ms * 16 + 4 * q + r;
-          if (row < mcnt && col < N) {
-            const size_t orow = shared ? (size_t)a.T * a.k + pos0 + row : (size_t)(pos0 + row);
-            o[orow * a.H + col] = f32_to_bf16(tot[ms][ns][r]);
-          }
+          *(uint16_t *)(lds + row * OST + cl * 2) = f32_to_bf16(tot[ms][ns][r]);
         }
+    }
+    __syncthreads();
+    constexpr int CPR = BN / 8;
+#pragma unroll
+    for (int i = 0; i < BM * CPR / THREADS; ++i) {
+      const int idx = tid + i * THREADS, row = idx / CPR, c = idx % CPR;
+      const int col = nb * BN + c * 8;
+      if (row < mcnt && col < N) {
+        const size_t orow = shared ? (size_t)a.T * a.k + pos0 + row : (size_t)(pos0 + row);
+        *(u32x4 *)(a.o + orow * a.H + col) = *(const u32x4 *)(lds + row * OST + c * 16);
+      }
     }
   }
 }
@@ -334,6 +397,7 @@ hipError_t launch_geo(int mode, int scale_dtype, GemmArgs a, int max_tiles, hipS
   const long grid = (long)max_tiles * a.n_nblk;
   if (grid > 0x7FFFFFFF) return hipErrorInvalidValue;
   const int Gmax = (mode == 0 ? a.H : (a.I > a.Is ? a.I : a.Is)) / 128;
+  if (Gmax > 32) return hipErrorInvalidValue;  // table loads assume K <= 4096
   const size_t lds = (size_t)Gm::STAGES * Gm::STAGE +
                      (((size_t)Gm::BN * Gmax * 2 + 15) & ~(size_t)15) +
                      sizeof(float) * ((size_t)BM * Gmax + (size_t)WN * BM);
