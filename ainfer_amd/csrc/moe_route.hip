@@ -147,55 +147,58 @@ __global__ __launch_bounds__(256) void k_router_logits(const uint16_t *__restric
                                                        int32_t *__restrict__ ticket, int T,
                                                        int H, int E) {
   const int lane = threadIdx.x & 63;
-  if (ticket && blockIdx.x == 0 && threadIdx.x == 0) *ticket = 0;
+  if (ticket && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *ticket = 0;
   const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   const int nrows = E + (gw ? 1 : 0);
   if (row >= nrows) return;
   const uint16_t *wr = row < E ? rw + (size_t)row * H : gw;
   const int nch = H >> 3;
-  for (int t0 = 0; t0 < T; t0 += ROUTER_TT) {
-    float acc[ROUTER_TT];
+  // blockIdx.y selects ROUTER_TT tokens.  Token rows past T are clamped to
+  // T - 1 so that every load is unconditional and the compiler can issue a
+  // chunk's ROUTER_TT loads back to back; only the stores are guarded.
+  const int t0 = blockIdx.y * ROUTER_TT;
+  float acc[ROUTER_TT];
 #pragma unroll
-    for (int i = 0; i < ROUTER_TT; ++i) acc[i] = 0.0f;
-    for (int c = lane; c < nch; c += 64) {
-      u32x4 wv = *(const u32x4 *)(wr + (size_t)c * 8);
-      float wf[8];
+  for (int i = 0; i < ROUTER_TT; ++i) acc[i] = 0.0f;
+  for (int c = lane; c < nch; c += 64) {
+    u32x4 wv = *(const u32x4 *)(wr + (size_t)c * 8);
+    u32x4 xv[ROUTER_TT];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        wf[2 * q] = __uint_as_float(wv[q] << 16);
-        wf[2 * q + 1] = __uint_as_float(wv[q] & 0xFFFF0000u);
-      }
+    for (int i = 0; i < ROUTER_TT; ++i)
+      xv[i] = *(const u32x4 *)(x + (size_t)min(t0 + i, T - 1) * H + (size_t)c * 8);
+    float wf[8];
 #pragma unroll
-      for (int i = 0; i < ROUTER_TT; ++i) {
-        if (t0 + i < T) {
-          u32x4 xv = *(const u32x4 *)(x + (size_t)(t0 + i) * H + (size_t)c * 8);
-          float a = acc[i];
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            a = __builtin_fmaf(__uint_as_float(xv[q] << 16), wf[2 * q], a);
-            a = __builtin_fmaf(__uint_as_float(xv[q] & 0xFFFF0000u), wf[2 * q + 1], a);
-          }
-          acc[i] = a;
-        }
-      }
+    for (int q = 0; q < 4; ++q) {
+      wf[2 * q] = __uint_as_float(wv[q] << 16);
+      wf[2 * q + 1] = __uint_as_float(wv[q] & 0xFFFF0000u);
     }
 #pragma unroll
     for (int i = 0; i < ROUTER_TT; ++i) {
-      float v = acc[i];
+      float a = acc[i];
 #pragma unroll
-      for (int m = 32; m >= 1; m >>= 1) v = v + __shfl_xor(v, m, 64);
-      acc[i] = v;
+      for (int q = 0; q < 4; ++q) {
+        a = __builtin_fmaf(__uint_as_float(xv[i][q] << 16), wf[2 * q], a);
+        a = __builtin_fmaf(__uint_as_float(xv[i][q] & 0xFFFF0000u), wf[2 * q + 1], a);
+      }
+      acc[i] = a;
     }
-    if (lane == 0) {
+  }
 #pragma unroll
-      for (int i = 0; i < ROUTER_TT; ++i) {
-        int t = t0 + i;
-        if (t < T) {
-          if (row < E)
-            logits[(size_t)t * E + row] = bias ? acc[i] + bias[row] : acc[i];
-          else
-            sg_logit[t] = acc[i];
-        }
+  for (int i = 0; i < ROUTER_TT; ++i) {
+    float v = acc[i];
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = v + __shfl_xor(v, m, 64);
+    acc[i] = v;
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int i = 0; i < ROUTER_TT; ++i) {
+      int t = t0 + i;
+      if (t < T) {
+        if (row < E)
+          logits[(size_t)t * E + row] = bias ? acc[i] + bias[row] : acc[i];
+        else
+          sg_logit[t] = acc[i];
       }
     }
   }
@@ -206,7 +209,8 @@ hipError_t launch_router(const void *x, const void *rw, const float *bias, const
                          hipStream_t s) {
   if (T == 0) return hipSuccess;
   int rows = E + (gw ? 1 : 0);
-  k_router_logits<<<(rows + 3) / 4, 256, 0, s>>>((const uint16_t *)x, (const uint16_t *)rw,
+  const dim3 grid((rows + 3) / 4, (T + ROUTER_TT - 1) / ROUTER_TT);
+  k_router_logits<<<grid, 256, 0, s>>>((const uint16_t *)x, (const uint16_t *)rw,
                                                  bias, (const uint16_t *)gw, logits,
                                                  sg_logit, ticket, T, H, E);
   return hipGetLastError();

@@ -205,8 +205,9 @@ __global__ __launch_bounds__(256) void k_select(const float *__restrict__ approx
                                                 float *__restrict__ xsum, int T, int E,
                                                 int k, int H, int has_shared, DispatchOut ds,
                                                 int fused) {
-  __shared__ int cl[SEL_WAVES][1024];
-  __shared__ float cv[SEL_WAVES][1024];
+  // candidate lists (fast path only)
+  __shared__ int cl[SEL_WAVES][EXACT ? 1 : 1024];
+  __shared__ float cv[SEL_WAVES][EXACT ? 1 : 1024];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int t = blockIdx.x * SEL_WAVES + wave;
   if (t < T) {
@@ -220,99 +221,108 @@ __global__ __launch_bounds__(256) void k_select(const float *__restrict__ approx
       key[i] = e < E ? ordered_key(ar[e]) : 0u;
       if (!EXACT && e < E) wn = fmaxf(wn, wnorm[e]);
     }
+    // k rounds of (largest key, then lowest expert among equal keys): the
+    // exact top-k in value-descending, expert-ascending order.  Lane j keeps
+    // the j-th pick.
     uint32_t taken = 0, kth = 0;
+    int seli = 0;
     for (int j = 0; j < k; ++j) {
       uint32_t bk = 0;
       int bi = 0x7FFFFFFF;
 #pragma unroll
       for (int i = 0; i < NV; ++i)
-        if (!(taken & (1u << i)) && (bi == 0x7FFFFFFF || key[i] > bk)) {
+        if (lane + 64 * i < E && !(taken & (1u << i)) && (bi == 0x7FFFFFFF || key[i] > bk)) {
           bk = key[i];
           bi = i;
         }
-      const uint32_t wk = wave_max_u32(bk);
-      const int wl = (int)wave_min_u32(bk == wk ? (uint32_t)lane : 64u);
-      if (lane == wl) taken |= 1u << bi;
+      const uint32_t wk = wave_max_u32(bi == 0x7FFFFFFF ? 0u : bk);
+      const uint32_t we = wave_min_u32(bi != 0x7FFFFFFF && bk == wk ? (uint32_t)(lane + 64 * bi)
+                                                                     : 0xFFFFFFFFu);
+      if ((int)(we & 63) == lane) taken |= 1u << (we >> 6);
+      if (lane == j) seli = (int)we;
       kth = wk;
     }
-    // ---- x row in registers (canonical chunk layout) and its norm ------
-    const int nch = H >> 3;
+    float selv = 0.0f, sgv = 0.0f;
     const uint16_t *xrow = x + (size_t)t * H;
-    u32x4 xc[CH];
-    float xs = 0.0f;
-#pragma unroll
-    for (int j = 0; j < CH; ++j) {
-      const int c = min(lane + 64 * j, nch - 1);
-      xc[j] = *(const u32x4 *)(xrow + (size_t)c * 8);
-      if (lane + 64 * j < nch) {
-#pragma unroll
-        for (int d = 0; d < 4; ++d) {
-          const float lo = __uint_as_float(xc[j][d] << 16), hi = __uint_as_float(xc[j][d] & 0xFFFF0000u);
-          xs = __builtin_fmaf(lo, lo, xs);
-          xs = __builtin_fmaf(hi, hi, xs);
-        }
-      }
-    }
-    for (int m = 32; m >= 1; m >>= 1) xs += __shfl_xor(xs, m, 64);
-    for (int m = 32; m >= 1; m >>= 1) wn = fmaxf(wn, __shfl_xor(wn, m, 64));
-    // ---- candidate threshold --------------------------------------------
-    const float lk = key_to_float(kth);
-    const float nrm = sqrtf(xs) * wn * 1.0625f;
-    const float d = EXACT ? 0.0f : 2.0f * (float)(H + 64) * 0x1p-23f * nrm;  // |approx - canonical|
-    const float thr = EXACT ? lk
-                            : lk - 2.0f * d - 0x1p-21f * (fabsf(lk) + 2.0f * d) - 1e-30f * (float)H;
-    // ---- candidate list, expert-ascending -------------------------------
-    int nc = 0;
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const int e = lane + 64 * i;
-      const bool c = e < E && key_to_float(key[i]) >= thr;
-      const uint64_t b = __ballot(c);
-      if (c) cl[wave][nc + __popcll(b & ((1ull << lane) - 1ull))] = e;
-      nc += __popcll(b);
-    }
-    __builtin_amdgcn_wave_barrier();
-    // ---- canonical logits of the candidates ------------------------------
     if (EXACT) {
-      for (int c = lane; c < nc; c += 64) cv[wave][c] = ar[cl[wave][c]];
+      // canonical logits already: the picks above are the top-k
+      if (lane < k) selv = ar[seli];
+      if (gw) sgv = sgl[t];
     } else {
-      for (int c0 = 0; c0 < nc; c0 += 4) {
-        const uint16_t *rows[4];
-        int ee[4];
+      // ---- x row in registers (canonical chunk layout) and its norm ------
+      const int nch = H >> 3;
+      u32x4 xc[CH];
+      float xs = 0.0f;
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          ee[b] = cl[wave][min(c0 + b, nc - 1)];
-          rows[b] = rw + (size_t)ee[b] * H;
-        }
-        float v[4];
-        canon_dot_batch<CH, 4>(xc, rows, lane, nch, v);
+      for (int j = 0; j < CH; ++j) {
+        const int c = min(lane + 64 * j, nch - 1);
+        xc[j] = *(const u32x4 *)(xrow + (size_t)c * 8);
+        if (lane + 64 * j < nch) {
 #pragma unroll
-        for (int b = 0; b < 4; ++b)
-          if (lane == 0 && c0 + b < nc) cv[wave][c0 + b] = bias ? v[b] + bias[ee[b]] : v[b];
-      }
-    }
-    __builtin_amdgcn_wave_barrier();
-    // ---- top-k among candidates (value desc, expert asc) ----------------
-    uint32_t tmask = 0;  // taken bits per lane slot (nc <= 1024: 16 slots)
-    int seli = 0;
-    float selv = 0.0f;
-    for (int j = 0; j < k; ++j) {
-      uint32_t bk = 0;
-      int bs = 0x7FFFFFFF;
-      for (int i = 0; i < 16 && lane + 64 * i < nc; ++i) {
-        const uint32_t kk = ordered_key(cv[wave][lane + 64 * i]);
-        if (!(tmask & (1u << i)) && (bs == 0x7FFFFFFF || kk > bk)) {
-          bk = kk;
-          bs = lane + 64 * i;
+          for (int d = 0; d < 4; ++d) {
+            const float lo = __uint_as_float(xc[j][d] << 16), hi = __uint_as_float(xc[j][d] & 0xFFFF0000u);
+            xs = __builtin_fmaf(lo, lo, xs);
+            xs = __builtin_fmaf(hi, hi, xs);
+          }
         }
       }
-      const uint32_t wk = wave_max_u32(bk);
-      const int ws = (int)wave_min_u32(bk == wk && bs != 0x7FFFFFFF ? (uint32_t)bs : 0xFFFFFFFFu);
-      if ((ws & 63) == lane) tmask |= 1u << (ws >> 6);
-      if (lane == j) {
-        seli = cl[wave][ws];
-        selv = cv[wave][ws];
+      for (int m = 32; m >= 1; m >>= 1) xs += __shfl_xor(xs, m, 64);
+      for (int m = 32; m >= 1; m >>= 1) wn = fmaxf(wn, __shfl_xor(wn, m, 64));
+      // ---- candidate threshold --------------------------------------------
+      const float lk = key_to_float(kth);
+      const float nrm = sqrtf(xs) * wn * 1.0625f;
+      const float d = 2.0f * (float)(H + 64) * 0x1p-23f * nrm;  // |approx - canonical|
+      const float thr = lk - 2.0f * d - 0x1p-21f * (fabsf(lk) + 2.0f * d) - 1e-30f * (float)H;
+      // ---- candidate list, expert-ascending -------------------------------
+      int nc = 0;
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int e = lane + 64 * i;
+        const bool c = e < E && key_to_float(key[i]) >= thr;
+        const uint64_t b = __ballot(c);
+        if (c) cl[wave][nc + __popcll(b & ((1ull << lane) - 1ull))] = e;
+        nc += __popcll(b);
       }
+      __builtin_amdgcn_wave_barrier();
+      // ---- canonical logits of the candidates ------------------------------
+      {
+        for (int c0 = 0; c0 < nc; c0 += 4) {
+          const uint16_t *rows[4];
+          int ee[4];
+#pragma unroll
+          for (int b = 0; b < 4; ++b) {
+            ee[b] = cl[wave][min(c0 + b, nc - 1)];
+            rows[b] = rw + (size_t)ee[b] * H;
+          }
+          float v[4];
+          canon_dot_batch<CH, 4>(xc, rows, lane, nch, v);
+#pragma unroll
+          for (int b = 0; b < 4; ++b)
+            if (lane == 0 && c0 + b < nc) cv[wave][c0 + b] = bias ? v[b] + bias[ee[b]] : v[b];
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+      // ---- top-k among candidates (value desc, expert asc) ----------------
+      uint32_t tmask = 0;  // taken bits per lane slot (nc <= 1024: 16 slots)
+      for (int j = 0; j < k; ++j) {
+        uint32_t bk = 0;
+        int bs = 0x7FFFFFFF;
+        for (int i = 0; i < 16 && lane + 64 * i < nc; ++i) {
+          const uint32_t kk = ordered_key(cv[wave][lane + 64 * i]);
+          if (!(tmask & (1u << i)) && (bs == 0x7FFFFFFF || kk > bk)) {
+            bk = kk;
+            bs = lane + 64 * i;
+          }
+        }
+        const uint32_t wk = wave_max_u32(bk);
+        const int ws = (int)wave_min_u32(bk == wk && bs != 0x7FFFFFFF ? (uint32_t)bs : 0xFFFFFFFFu);
+        if ((ws & 63) == lane) tmask |= 1u << (ws >> 6);
+        if (lane == j) {
+          seli = cl[wave][ws];
+          selv = cv[wave][ws];
+        }
+      }
+      if (gw) sgv = canon_dot<CH>(xc, gw, lane, nch);
     }
     const float vmax = __shfl(selv, 0, 64);
     const float p = lane < k ? expf(selv - vmax) : 0.0f;
@@ -324,7 +334,7 @@ __global__ __launch_bounds__(256) void k_select(const float *__restrict__ approx
     }
     // ---- shared gate ----------------------------------------------------
     float g = 1.0f;
-    if (gw) g = 1.0f / (1.0f + expf(-(EXACT ? sgl[t] : canon_dot<CH>(xc, gw, lane, nch))));
+    if (gw) g = 1.0f / (1.0f + expf(-sgv));
     if (lane == 0) sgate[t] = g;
     // ---- MFMA-order copy of x: position 8*j+e <- k = 4*e+j --------------
     if (xperm) {

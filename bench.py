@@ -1,10 +1,15 @@
 #!/usr/bin/env python3
 """Benchmark of the INT4 MoE layer on one MI355X.
 
-Headline (the JSON line's `value`): config c1 decode, batch 1 -- layer
+Headline (the JSON line's `value`): config c1 decode, 16 tokens -- layer
 microseconds per token (H2048, 512 experts, top-10, I512, + shared expert,
-INT4 g128 fp16 scales).  `details` adds c1 at 4 and 16 tokens and the c2
+INT4 g128 fp16 scales).  `details` adds c1 at 1 and 4 tokens and the c2
 prefill (4096 tokens, Zipf(1.1) routing) in tokens/s and % of bf16 MFMA peak.
+
+`roofline.traffic` (HBM bytes per launch of the gate/up kernel) is read from
+the committed rocprofv3 PMC summary profiles/k_expert_gate_up_c1_T16_traffic.md
+(FETCH_SIZE + WRITE_SIZE, scaled by the same counters on a copy of known
+size, made with --calib-copy); null when that file is absent.
 
 Inputs are resident in HBM before the timed region.  Decode steps cycle over
 NL distinct layer copies and NX distinct token batches so the weights each
@@ -46,6 +51,17 @@ def gateup_bytes(cfg, U):
     shared expert, plus the bf16 tokens read."""
     per = lambda I: 2 * (cfg.hidden * I // 2 + cfg.hidden * I // 128 * 2)
     return U * per(cfg.inter) + (per(cfg.shared_inter) if cfg.shared_inter else 0)
+
+
+def measured_traffic(T):
+    """HBM bytes per gate/up launch from the committed PMC summary, or None."""
+    f = ROOT / "profiles" / f"k_expert_gate_up_c1_T{T}_traffic.md"
+    if not f.exists():
+        return None
+    for line in f.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(float(line.split(":", 1)[1]))
+    return None
 
 
 def run_decode(layers, cfg, T, steps, warmup, NX, stream):
@@ -154,6 +170,8 @@ def main():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
+                    help="finally copy MIB MiB device-to-device 5 times (PMC calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -186,6 +204,7 @@ def main():
             "layer_hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
             "stage_us": {k: round(v, 3) for k, v in st.items()},
             "gate_up_gbs": gu_gbs,
+            "gate_up_alg_bytes": gateup_bytes(c1, U),
         }
         log(f"[bench]   {json.dumps(decode[T])}")
 
@@ -210,16 +229,26 @@ def main():
         log(f"[bench]   {json.dumps(prefill)}")
         layers = [MoeLayer(c1, layer=0)]
 
-    cpu = None
-    if not args.no_cpu:
-        log("[bench] cpu baseline")
-        cpu = cpu_baseline(layers[0], c1, 1, args.cpu_seconds)
-        log(f"[bench]   {json.dumps(cpu)}")
+    if args.calib_copy > 0:
+        n = args.calib_copy << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] calibration copy: 5 x {n} bytes")
 
     if not decode:
         print(json.dumps({"prefill_c2_T4096": prefill}), flush=True)
         return
-    d1 = decode[min(decode)]
+    Th = 16 if 16 in decode else max(decode)
+    d1 = decode[Th]
+
+    cpu = None
+    if not args.no_cpu:
+        log(f"[bench] cpu baseline T={Th}")
+        cpu = cpu_baseline(layers[0], c1, Th, args.cpu_seconds)
+        log(f"[bench]   {json.dumps(cpu)}")
     out = {
         "metric": METRIC,
         "value": round(d1["us_per_token"], 3),
@@ -233,17 +262,19 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (seeded counter-based generator; random-init INT4 weights)",
-        "config": {"workload": "c1 decode T=1: H2048 E512 top-10 I512 + 1 shared expert "
+        "config": {"workload": f"c1 decode T={Th}: H2048 E512 top-10 I512 + 1 shared expert "
                                "(sigmoid gate), INT4 g128 fp16 scales",
-                   "layer_copies": args.layers, "global_batch": 1,
+                   "layer_copies": args.layers, "global_batch": Th,
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(d1["gate_up_gbs"], 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(d1["gate_up_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "k_expert_small<fp16, gate/up> (dominant decode kernel)"},
+                     "frac": round(d1["gate_up_gbs"] / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(Th),
+                     "kernel": "k_expert<fp16, gate/up> (dominant decode kernel)",
+                     "alg_bytes_per_launch": round(d1["gate_up_alg_bytes"])},
         "cpu_baseline": cpu,
         "details": {
-            "layer_hbm_frac_T1": round(d1["layer_hbm_frac"], 4),
+            f"layer_hbm_frac_T{Th}": round(d1["layer_hbm_frac"], 4),
             "decode": {str(T): {k: (round(v, 4) if isinstance(v, float) else v)
                                 for k, v in d.items()} for T, d in decode.items()},
             "prefill_c2_T4096": prefill,
