@@ -135,6 +135,13 @@ int check_weights(const ainfer_moe_shape *s, const ainfer_moe_weights *w) {
   if (s->shared_inter > 0 && (!w->ws_gate || !w->ss_gate || !w->ws_up || !w->ss_up ||
                               !w->ws_down || !w->ss_down))
     return AINFER_ERR_NULL;
+  // 16-byte vector loads of weights, 8-byte loads of scale runs
+  auto mis = [](const void *p, uintptr_t a) { return p && ((uintptr_t)p & (a - 1)); };
+  if (mis(w->w_gate, 16) || mis(w->w_up, 16) || mis(w->w_down, 16) || mis(w->ws_gate, 16) ||
+      mis(w->ws_up, 16) || mis(w->ws_down, 16) || mis(w->router_w, 16) ||
+      mis(w->shared_gate_w, 16) || mis(w->s_gate, 8) || mis(w->s_up, 8) || mis(w->s_down, 8) ||
+      mis(w->ss_gate, 8) || mis(w->ss_up, 8) || mis(w->ss_down, 8))
+    return AINFER_ERR_ARG;
   return AINFER_OK;
 }
 
@@ -244,7 +251,8 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
   a.I = s->inter;
   a.Is = s->shared_inter;
   const int max_tiles = max_tiles_bound(*s, T, SMALL_MT);
-  const int kbw = 4;  // measured best at T = 1, 4, 16 (k-groups per wave)
+  // k-groups per wave and 16-row groups per wave, measured at T = 1, 4, 16
+  const int kbw = 4, kbw_down = 2;
   // gate/up + SiLU-mul
   a.w0 = w->w_gate;
   a.w1 = w->w_up;
@@ -258,7 +266,7 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
   a.a_shared = at<uint16_t>(ws, L.xperm);
   a.act = at<uint16_t>(ws, L.act);
   a.act_s = at<uint16_t>(ws, L.act_s);
-  HIP_TRY(launch_expert_stream(0, s->scale_dtype, a, max_tiles, kbw, st));
+  HIP_TRY(launch_expert_stream(0, s->scale_dtype, a, max_tiles, kbw, RG_GATE_UP, st));
   pc->end(4);
   // down + combine
   a.w0 = w->w_down;
@@ -272,7 +280,7 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
   a.a_routed = at<uint16_t>(ws, L.act);
   a.a_shared = at<uint16_t>(ws, L.act_s);
   a.o = at<uint16_t>(ws, L.o);
-  HIP_TRY(launch_expert_stream(1, s->scale_dtype, a, max_tiles, kbw, st));
+  HIP_TRY(launch_expert_stream(1, s->scale_dtype, a, max_tiles, kbw_down, RG_DOWN, st));
   pc->end(5);
   HIP_TRY(launch_combine(at<uint16_t>(ws, L.o), d.inv, at<float>(ws, L.w), at<float>(ws, L.sg),
                          has_shared, resid, y, T, k, H, st));

@@ -50,14 +50,32 @@ __device__ __forceinline__ u32x4 nib_slice(u32x4 b, int j, uint32_t magic) {
                ((b[2] >> (4 * j)) & mask) | magic, ((b[3] >> (4 * j)) & mask) | magic};
 }
 
+// The KBW scales of one row and k-range in one load (KB is a multiple of
+// KBW, so the address is KBW * 2-byte aligned).
+template <int KBW>
+__device__ __forceinline__ void load_scales(const uint16_t *p, uint16_t (&S)[KBW]) {
+  if constexpr (KBW == 4) {
+    const uint2 v = *(const uint2 *)p;
+    S[0] = (uint16_t)v.x; S[1] = (uint16_t)(v.x >> 16);
+    S[2] = (uint16_t)v.y; S[3] = (uint16_t)(v.y >> 16);
+  } else if constexpr (KBW == 2) {
+    const uint32_t v = *(const uint32_t *)p;
+    S[0] = (uint16_t)v; S[1] = (uint16_t)(v >> 16);
+  } else {
+    S[0] = *p;
+  }
+}
+
 __device__ __forceinline__ float silu_mul(float g, float u) {
   return g / (1.0f + expf(-g)) * u;
 }
 
-template <int SD, int KBW, int MODE>
+template <int SD, int KBW, int RG, int MODE>
 __global__ __launch_bounds__(1024) void k_expert(ExpertArgs a) {
-  __shared__ float red[2][MAX_WAVES][256];
-  const int n_rg = a.n_slabs;  // row groups of 16*WR rows per tile
+  // K-split partial sums: [2][waves][RG][256] floats (dynamic)
+  extern __shared__ float red[];
+  const int nw = a.WK * a.WR;
+  const int n_rg = a.n_slabs;  // slabs of 16*RG*WR rows per tile
   const int tile_id = blockIdx.x / n_rg, slab = blockIdx.x % n_rg;
   if (tile_id >= *a.n_tiles) return;
   const int4 t = a.tiles[tile_id];
@@ -66,17 +84,16 @@ __global__ __launch_bounds__(1024) void k_expert(ExpertArgs a) {
   const int N = MODE == 0 ? (shared ? a.Is : a.I) : a.H;
   const int K = MODE == 0 ? a.H : (shared ? a.Is : a.I);
   const int KB = K >> 7;
-  if (slab * a.WR * 16 >= N) return;
+  if (slab * a.WR * RG * 16 >= N) return;
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int kw = wave % a.WK, wr = wave / a.WK;
   const int m = lane & 15, q = lane >> 4;
-  const int n0 = (slab * a.WR + wr) * 16;
+  const int n0 = (slab * a.WR + wr) * RG * 16;  // first of this wave's RG row groups
   // wave-uniform: this wave has rows and k-groups in this item
   const bool act = n0 < N && kw * KBW < KB;
   const int kb0 = act ? kw * KBW : 0;
-  const int n = act ? n0 + m : m;
 
   // ---- A row of this lane's token (a buffer offset; lanes past the tile's
   // token count get an out-of-range offset and read zeros) ----------------
@@ -84,7 +101,16 @@ __global__ __launch_bounds__(1024) void k_expert(ExpertArgs a) {
   uint32_t aoff;
   const uint16_t *abase;
   if (MODE == 0) {
-    const int tok = shared ? pos0 + mm : a.ptok[pos0 + mm];
+    int tok;
+    if (shared) {
+      tok = pos0 + mm;
+    } else if (t.w != 0) {  // token set carried by the tile: the mm-th set bit
+      uint32_t bits = (uint32_t)t.w;
+      for (int i = 0; i < mm; ++i) bits &= bits - 1u;
+      tok = __builtin_ctz(bits);
+    } else {
+      tok = a.ptok[pos0 + mm];
+    }
     abase = a.a_routed;
     aoff = (uint32_t)tok * (uint32_t)a.H * 2u;
   } else {
@@ -93,25 +119,30 @@ __global__ __launch_bounds__(1024) void k_expert(ExpertArgs a) {
   }
   if (m >= mcnt) aoff = BUF_OOB;
   const __amdgpu_buffer_rsrc_t arsrc = make_rsrc(abase, 0x7FFFFFFFu);
-  // ---- weight loads ------------------------------------------------------
+  // ---- weight loads: RG row groups x KBW k-groups (rows past N are clamped:
+  // their results are never stored) ------------------------------------------
   const size_t rowb = (size_t)K / 2;
   const uint8_t *w0 = shared ? a.ws0 : a.w0 + (size_t)e * N * rowb;
   const uint16_t *s0 = shared ? a.ss0 : a.s0 + (size_t)e * N * KB;
-  const size_t rb = (size_t)n * rowb + q * 16;
-  u32x4 B0[KBW], B1[KBW];
-  uint16_t S0[KBW], S1[KBW];
-#pragma unroll
-  for (int i = 0; i < KBW; ++i) {
-    B0[i] = ldg_stream(w0 + rb + (size_t)(kb0 + i) * 64);
-    S0[i] = s0[(size_t)n * KB + kb0 + i];
-  }
+  const uint8_t *w1 = nullptr;
+  const uint16_t *s1 = nullptr;
   if (MODE == 0) {
-    const uint8_t *w1 = shared ? a.ws1 : a.w1 + (size_t)e * N * rowb;
-    const uint16_t *s1 = shared ? a.ss1 : a.s1 + (size_t)e * N * KB;
+    w1 = shared ? a.ws1 : a.w1 + (size_t)e * N * rowb;
+    s1 = shared ? a.ss1 : a.s1 + (size_t)e * N * KB;
+  }
+  u32x4 B0[RG][KBW], B1[RG][KBW];
+  uint16_t S0[RG][KBW], S1[RG][KBW];
 #pragma unroll
-    for (int i = 0; i < KBW; ++i) {
-      B1[i] = ldg_stream(w1 + rb + (size_t)(kb0 + i) * 64);
-      S1[i] = s1[(size_t)n * KB + kb0 + i];
+  for (int g = 0; g < RG; ++g) {
+    const int n = act ? min(n0 + g * 16 + m, N - 1) : m;
+    const size_t rb = (size_t)n * rowb + q * 16;
+#pragma unroll
+    for (int i = 0; i < KBW; ++i) B0[g][i] = ldg_stream(w0 + rb + (size_t)(kb0 + i) * 64);
+    load_scales<KBW>(s0 + (size_t)n * KB + kb0, S0[g]);
+    if (MODE == 0) {
+#pragma unroll
+      for (int i = 0; i < KBW; ++i) B1[g][i] = ldg_stream(w1 + rb + (size_t)(kb0 + i) * 64);
+      load_scales<KBW>(s1 + (size_t)n * KB + kb0, S1[g]);
     }
   }
   u32x4 A[KBW][4];
@@ -122,7 +153,9 @@ __global__ __launch_bounds__(1024) void k_expert(ExpertArgs a) {
       A[i][j] = buf_load16(arsrc, aoff + (uint32_t)(((kb0 + i) * 128 + q * 32 + j * 8) * 2));
 
   // ---- MFMA ---------------------------------------------------------------
-  f32x4 tot0 = {0.f, 0.f, 0.f, 0.f}, tot1 = {0.f, 0.f, 0.f, 0.f};
+  f32x4 tot0[RG], tot1[RG];
+#pragma unroll
+  for (int g = 0; g < RG; ++g) tot0[g] = tot1[g] = f32x4{0.f, 0.f, 0.f, 0.f};
   if (act) {
     uint32_t magic;
     asm volatile("v_mov_b32 %0, 0x43004300" : "=v"(magic));
@@ -133,46 +166,54 @@ __global__ __launch_bounds__(1024) void k_expert(ExpertArgs a) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) xs = mfma_bf16_16x16x32(A[i][j], ones, xs);
       const f32x4 c0 = xs * -136.0f;
-      {
-        const u32x4 b = B0[i] ^ 0x88888888u;
-        f32x4 acc = c0;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc = mfma_bf16_16x16x32(A[i][j], nib_slice(b, j, magic), acc);
-        tot0 += scale_to_f32<SD>(S0[i]) * acc;
-      }
-      if (MODE == 0) {
-        const u32x4 b = B1[i] ^ 0x88888888u;
-        f32x4 acc = c0;
+      for (int g = 0; g < RG; ++g) {
+        {
+          const u32x4 b = B0[g][i] ^ 0x88888888u;
+          f32x4 acc = c0;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc = mfma_bf16_16x16x32(A[i][j], nib_slice(b, j, magic), acc);
-        tot1 += scale_to_f32<SD>(S1[i]) * acc;
+          for (int j = 0; j < 4; ++j) acc = mfma_bf16_16x16x32(A[i][j], nib_slice(b, j, magic), acc);
+          tot0[g] += scale_to_f32<SD>(S0[g][i]) * acc;
+        }
+        if (MODE == 0) {
+          const u32x4 b = B1[g][i] ^ 0x88888888u;
+          f32x4 acc = c0;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc = mfma_bf16_16x16x32(A[i][j], nib_slice(b, j, magic), acc);
+          tot1[g] += scale_to_f32<SD>(S1[g][i]) * acc;
+        }
       }
     }
   }
   // ---- K split meets in LDS: D layout lane (q, m) holds tokens 4q+r, row m
+  float *red0 = red, *red1 = red + nw * RG * 256;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    red[0][wave][(4 * q + r) * 16 + m] = tot0[r];
-    if (MODE == 0) red[1][wave][(4 * q + r) * 16 + m] = tot1[r];
-  }
+  for (int g = 0; g < RG; ++g)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      red0[(wave * RG + g) * 256 + (4 * q + r) * 16 + m] = tot0[g][r];
+      if (MODE == 0) red1[(wave * RG + g) * 256 + (4 * q + r) * 16 + m] = tot1[g][r];
+    }
   __syncthreads();
-  const int nthr = a.WK * a.WR * 64;
-  for (int idx = threadIdx.x; idx < a.WR * 256; idx += nthr) {
-    const int rwr = idx >> 8, cell = idx & 255;
+  const int nthr = nw * 64;
+  for (int idx = threadIdx.x; idx < a.WR * RG * 256; idx += nthr) {
+    const int rgrp = idx >> 8, cell = idx & 255;  // rgrp = wr * RG + g
+    const int rwr = rgrp / RG, g = rgrp % RG;
     const int tm = cell >> 4, tn = cell & 15;
-    const int row = (slab * a.WR + rwr) * 16 + tn;
+    const int row = (slab * a.WR + rwr) * RG * 16 + g * 16 + tn;
     if (tm >= mcnt || row >= N) continue;
-    float g = 0.f, u = 0.f;
+    float gs = 0.f, u = 0.f;
     for (int w = 0; w < a.WK; ++w) {
-      g += red[0][rwr * a.WK + w][cell];
-      if (MODE == 0) u += red[1][rwr * a.WK + w][cell];
+      const int src = ((rwr * a.WK + w) * RG + g) * 256 + cell;
+      gs += red0[src];
+      if (MODE == 0) u += red1[src];
     }
     if (MODE == 0) {
       uint16_t *dst = shared ? a.act_s : a.act;
-      dst[(size_t)(pos0 + tm) * N + perm32_pos(row)] = f32_to_bf16(silu_mul(g, u));
+      dst[(size_t)(pos0 + tm) * N + perm32_pos(row)] = f32_to_bf16(silu_mul(gs, u));
     } else {
       const size_t orow = shared ? (size_t)a.T * a.k + pos0 + tm : (size_t)(pos0 + tm);
-      a.o[orow * a.H + row] = f32_to_bf16(g);
+      a.o[orow * a.H + row] = f32_to_bf16(gs);
     }
   }
 }
@@ -200,37 +241,51 @@ bool expert_geometry(int mode, int H, int I, int Is, int pref_kbw, int *KBW, int
   return true;
 }
 
-template <int SD, int MODE>
-void launch_kbw(int kbw, unsigned grid, int threads, const ExpertArgs &a, hipStream_t s) {
+template <int SD, int MODE, int RG>
+void launch_kbw(int kbw, unsigned grid, int threads, size_t lds, const ExpertArgs &a,
+                hipStream_t s) {
   if (kbw == 1)
-    k_expert<SD, 1, MODE><<<grid, threads, 0, s>>>(a);
+    k_expert<SD, 1, RG, MODE><<<grid, threads, lds, s>>>(a);
   else if (kbw == 2)
-    k_expert<SD, 2, MODE><<<grid, threads, 0, s>>>(a);
+    k_expert<SD, 2, RG, MODE><<<grid, threads, lds, s>>>(a);
   else
-    k_expert<SD, 4, MODE><<<grid, threads, 0, s>>>(a);
+    k_expert<SD, 4, RG, MODE><<<grid, threads, lds, s>>>(a);
+}
+
+template <int SD, int MODE>
+void launch_rg(int rg, int kbw, unsigned grid, int threads, size_t lds, const ExpertArgs &a,
+               hipStream_t s) {
+  if (rg == 1)
+    launch_kbw<SD, MODE, 1>(kbw, grid, threads, lds, a, s);
+  else if (rg == 2)
+    launch_kbw<SD, MODE, 2>(kbw, grid, threads, lds, a, s);
+  else
+    launch_kbw<SD, MODE, 4>(kbw, grid, threads, lds, a, s);
 }
 
 hipError_t launch_expert_stream(int mode, int scale_dtype, ExpertArgs a, int max_tiles,
-                                int pref_kbw, hipStream_t s) {
+                                int pref_kbw, int rg, hipStream_t s) {
   if (max_tiles <= 0) return hipSuccess;
+  if (rg != 1 && rg != 2 && rg != 4) return hipErrorInvalidValue;
   int kbw;
   if (!expert_geometry(mode, a.H, a.I, a.Is, pref_kbw, &kbw, &a.WK, &a.WR))
     return hipErrorInvalidValue;
   const int Nmax = mode == 0 ? (a.I > a.Is ? a.I : a.Is) : a.H;
-  a.n_slabs = (Nmax + 16 * a.WR - 1) / (16 * a.WR);
+  a.n_slabs = (Nmax + 16 * rg * a.WR - 1) / (16 * rg * a.WR);
   const int threads = a.WK * a.WR * 64;
+  const size_t lds = sizeof(float) * 2 * (size_t)a.WK * a.WR * rg * 256;
   const long grid = (long)max_tiles * a.n_slabs;
   if (grid > 0x7FFFFFFF) return hipErrorInvalidValue;
   if (mode == 0) {
     if (scale_dtype == AINFER_SCALE_FP16)
-      launch_kbw<AINFER_SCALE_FP16, 0>(kbw, (unsigned)grid, threads, a, s);
+      launch_rg<AINFER_SCALE_FP16, 0>(rg, kbw, (unsigned)grid, threads, lds, a, s);
     else
-      launch_kbw<AINFER_SCALE_BF16, 0>(kbw, (unsigned)grid, threads, a, s);
+      launch_rg<AINFER_SCALE_BF16, 0>(rg, kbw, (unsigned)grid, threads, lds, a, s);
   } else {
     if (scale_dtype == AINFER_SCALE_FP16)
-      launch_kbw<AINFER_SCALE_FP16, 1>(kbw, (unsigned)grid, threads, a, s);
+      launch_rg<AINFER_SCALE_FP16, 1>(rg, kbw, (unsigned)grid, threads, lds, a, s);
     else
-      launch_kbw<AINFER_SCALE_BF16, 1>(kbw, (unsigned)grid, threads, a, s);
+      launch_rg<AINFER_SCALE_BF16, 1>(rg, kbw, (unsigned)grid, threads, lds, a, s);
   }
   return hipGetLastError();
 }

@@ -18,7 +18,7 @@ struct ExpertArgs {
   uint16_t *act_s;            // MODE 0 out: [T][Is]
   uint16_t *o;                // MODE 1 out: [Tk + T][H] bf16
   const int32_t *ptok;        // token of each dispatch position
-  const int4 *tiles;          // (expert, first position, rows, first row)
+  const int4 *tiles;          // (expert, first position, rows, token mask or 0)
   const int32_t *n_tiles;
   int T, k, E, H, I, Is;
   int WK, WR, n_slabs;        // set by the launcher
@@ -106,8 +106,15 @@ bool expert_geometry(int mode, int H, int I, int Is, int pref_kbw, int *KBW, int
 // mode 0: gate/up + SiLU-mul; mode 1: down.  max_tiles bounds
 // the tile list.
 // pref_kbw: preferred 128-wide k-groups per wave (1, 2 or 4).
+#ifndef RG_GATE_UP
+#define RG_GATE_UP 1
+#endif
+#ifndef RG_DOWN
+#define RG_DOWN 2
+#endif
+// rg: 16-row groups per wave (1, 2 or 4) sharing one load of the token rows
 hipError_t launch_expert_stream(int mode, int scale_dtype, ExpertArgs a, int max_tiles,
-                                int pref_kbw, hipStream_t s);
+                                int pref_kbw, int rg, hipStream_t s);
 
 // tile height of the small-M expert kernels
 constexpr int SMALL_MT = 16;

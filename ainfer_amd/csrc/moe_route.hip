@@ -286,7 +286,7 @@ __global__ __launch_bounds__(1024) void k_dispatch_scan(int32_t *__restrict__ ch
     for (int c = 0; c < nchunks; ++c) chunk_counts[(size_t)c * E + e] += base;
     if (ds.tiles)
       for (int i = 0; i < ntile; ++i)
-        ds.tiles[tbase + i] = make_int4(e, base + i * mt, min(mt, total - i * mt), i * mt);
+        ds.tiles[tbase + i] = make_int4(e, base + i * mt, min(mt, total - i * mt), 0);
   }
   if (e == 0) ds.offsets[E] = sc[1023];
   __syncthreads();
@@ -294,7 +294,7 @@ __global__ __launch_bounds__(1024) void k_dispatch_scan(int32_t *__restrict__ ch
   const int nsh = has_shared ? (T + mt - 1) / mt : 0;
   if (ds.tiles)
     for (int i = e; i < nsh; i += blockDim.x)
-      ds.tiles[routed_tiles + i] = make_int4(E, i * mt, min(mt, T - i * mt), i * mt);
+      ds.tiles[routed_tiles + i] = make_int4(E, i * mt, min(mt, T - i * mt), 0);
   if (e == 0 && ds.n_tiles) *ds.n_tiles = routed_tiles + nsh;
 }
 

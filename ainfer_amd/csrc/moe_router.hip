@@ -190,6 +190,76 @@ constexpr int SEL_WAVES = 4;
 
 // EXACT: `approx` already holds the canonical logits (k_router_logits) and
 // `sgl` the canonical shared-gate logits; the refine is skipped.
+// k rounds of (largest key, then lowest expert among equal keys): the exact
+// top-k of key[] (lane l, slot i = expert l + 64 i) in value-descending,
+// expert-ascending order.  Lane j < k returns the j-th pick; the return value
+// is the k-th largest key.
+template <int NV>
+__device__ __forceinline__ uint32_t wave_topk(const uint32_t (&key)[NV], int E, int k, int lane,
+                                              int &seli) {
+  uint32_t taken = 0, kth = 0;
+  seli = 0;
+  for (int j = 0; j < k; ++j) {
+    uint32_t bk = 0;
+    int bi = 0x7FFFFFFF;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      if (lane + 64 * i < E && !(taken & (1u << i)) && (bi == 0x7FFFFFFF || key[i] > bk)) {
+        bk = key[i];
+        bi = i;
+      }
+    const uint32_t wk = wave_max_u32(bi == 0x7FFFFFFF ? 0u : bk);
+    const uint32_t we = wave_min_u32(bi != 0x7FFFFFFF && bk == wk ? (uint32_t)(lane + 64 * bi)
+                                                                   : 0xFFFFFFFFu);
+    if ((int)(we & 63) == lane) taken |= 1u << (we >> 6);
+    if (lane == j) seli = (int)we;
+    kth = wk;
+  }
+  return kth;
+}
+
+// MFMA-order copy of one token row (position 8*j+e <- k = 4*e+j inside every
+// 32-element block) and, when xsum is non-null, its 128-wide group sums.
+__device__ __forceinline__ void write_xperm(const uint16_t *__restrict__ xrow,
+                                            uint16_t *__restrict__ xperm,
+                                            float *__restrict__ xsum, int t, int H, int lane) {
+  {
+    uint16_t *xo = xperm + (size_t)t * H;
+    for (int b = lane; b < (H >> 5); b += 64) {
+      const u32x4 *src = (const u32x4 *)(xrow + b * 32);
+      const u32x4 s0 = src[0], s1 = src[1], s2 = src[2], s3 = src[3];
+      const uint32_t in[16] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3],
+                               s2[0], s2[1], s2[2], s2[3], s3[0], s3[1], s3[2], s3[3]};
+      uint32_t out[16];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) {
+          const int ka = 8 * e2 + j, kb = ka + 4;
+          const uint32_t lo = (in[ka >> 1] >> (16 * (ka & 1))) & 0xFFFFu;
+          const uint32_t hi = (in[kb >> 1] >> (16 * (kb & 1))) & 0xFFFFu;
+          out[4 * j + e2] = lo | (hi << 16);
+        }
+      u32x4 *dst = (u32x4 *)(xo + b * 32);
+      dst[0] = u32x4{out[0], out[1], out[2], out[3]};
+      dst[1] = u32x4{out[4], out[5], out[6], out[7]};
+      dst[2] = u32x4{out[8], out[9], out[10], out[11]};
+      dst[3] = u32x4{out[12], out[13], out[14], out[15]};
+      if (xsum) {
+        // sum of the 128-wide group: this block's 32 values, then the 4
+        // consecutive lanes holding the group's blocks (fixed order)
+        float bs = 0.0f;
+#pragma unroll
+        for (int i2 = 0; i2 < 16; ++i2)
+          bs += __uint_as_float(in[i2] << 16) + __uint_as_float(in[i2] & 0xFFFF0000u);
+        bs += __shfl_xor(bs, 1, 64);
+        bs += __shfl_xor(bs, 2, 64);
+        if ((b & 3) == 0) xsum[(size_t)t * (H >> 7) + (b >> 2)] = bs;
+      }
+    }
+  }
+}
+
 template <int NV, int CH, bool EXACT>
 __global__ __launch_bounds__(256) void k_select(const float *__restrict__ approx,
                                                 const float *__restrict__ sgl,
@@ -221,27 +291,8 @@ __global__ __launch_bounds__(256) void k_select(const float *__restrict__ approx
       key[i] = e < E ? ordered_key(ar[e]) : 0u;
       if (!EXACT && e < E) wn = fmaxf(wn, wnorm[e]);
     }
-    // k rounds of (largest key, then lowest expert among equal keys): the
-    // exact top-k in value-descending, expert-ascending order.  Lane j keeps
-    // the j-th pick.
-    uint32_t taken = 0, kth = 0;
-    int seli = 0;
-    for (int j = 0; j < k; ++j) {
-      uint32_t bk = 0;
-      int bi = 0x7FFFFFFF;
-#pragma unroll
-      for (int i = 0; i < NV; ++i)
-        if (lane + 64 * i < E && !(taken & (1u << i)) && (bi == 0x7FFFFFFF || key[i] > bk)) {
-          bk = key[i];
-          bi = i;
-        }
-      const uint32_t wk = wave_max_u32(bi == 0x7FFFFFFF ? 0u : bk);
-      const uint32_t we = wave_min_u32(bi != 0x7FFFFFFF && bk == wk ? (uint32_t)(lane + 64 * bi)
-                                                                     : 0xFFFFFFFFu);
-      if ((int)(we & 63) == lane) taken |= 1u << (we >> 6);
-      if (lane == j) seli = (int)we;
-      kth = wk;
-    }
+    int seli;
+    const uint32_t kth = wave_topk<NV>(key, E, k, lane, seli);
     float selv = 0.0f, sgv = 0.0f;
     const uint16_t *xrow = x + (size_t)t * H;
     if (EXACT) {
@@ -336,42 +387,7 @@ __global__ __launch_bounds__(256) void k_select(const float *__restrict__ approx
     float g = 1.0f;
     if (gw) g = 1.0f / (1.0f + expf(-sgv));
     if (lane == 0) sgate[t] = g;
-    // ---- MFMA-order copy of x: position 8*j+e <- k = 4*e+j --------------
-    if (xperm) {
-      uint16_t *xo = xperm + (size_t)t * H;
-      for (int b = lane; b < (H >> 5); b += 64) {
-        const u32x4 *src = (const u32x4 *)(xrow + b * 32);
-        const u32x4 s0 = src[0], s1 = src[1], s2 = src[2], s3 = src[3];
-        const uint32_t in[16] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3],
-                                 s2[0], s2[1], s2[2], s2[3], s3[0], s3[1], s3[2], s3[3]};
-        uint32_t out[16];
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-          for (int e2 = 0; e2 < 4; ++e2) {
-            const int ka = 8 * e2 + j, kb = ka + 4;
-            const uint32_t lo = (in[ka >> 1] >> (16 * (ka & 1))) & 0xFFFFu;
-            const uint32_t hi = (in[kb >> 1] >> (16 * (kb & 1))) & 0xFFFFu;
-            out[4 * j + e2] = lo | (hi << 16);
-          }
-        u32x4 *dst = (u32x4 *)(xo + b * 32);
-        dst[0] = u32x4{out[0], out[1], out[2], out[3]};
-        dst[1] = u32x4{out[4], out[5], out[6], out[7]};
-        dst[2] = u32x4{out[8], out[9], out[10], out[11]};
-        dst[3] = u32x4{out[12], out[13], out[14], out[15]};
-        if (xsum) {
-          // sum of the 128-wide group: this block's 32 values, then the 4
-          // consecutive lanes holding the group's blocks (fixed order)
-          float bs = 0.0f;
-#pragma unroll
-          for (int i2 = 0; i2 < 16; ++i2)
-            bs += __uint_as_float(in[i2] << 16) + __uint_as_float(in[i2] & 0xFFFF0000u);
-          bs += __shfl_xor(bs, 1, 64);
-          bs += __shfl_xor(bs, 2, 64);
-          if ((b & 3) == 0) xsum[(size_t)t * (H >> 7) + (b >> 2)] = bs;
-        }
-      }
-    }
+    if (xperm) write_xperm(xrow, xperm, xsum, t, H, lane);
   }
   if (!fused) return;
   // ---- the last block runs the dispatch ---------------------------------
@@ -386,6 +402,104 @@ __global__ __launch_bounds__(256) void k_select(const float *__restrict__ approx
   __threadfence();
   if (threadIdx.x == 0) atomicExch(ds.ticket, 0);
   dispatch_small_block(topk_idx, T, k, E, has_shared, ds);
+}
+
+// Decode routing for T <= 16 in one block, one wave per token: the exact
+// top-k of the canonical logits, softmax weights, the shared-expert gate and
+// the MFMA-order copy of x; then wave 0 builds the dispatch from the picks
+// kept in LDS (one tile per routed expert, the token set in the tile's .w).
+__device__ __forceinline__ void dispatch_wave(const int *__restrict__ s_idx, int T, int k, int E,
+                                              int has_shared, const DispatchOut &ds,
+                                              uint32_t *msk, int *off, int lane) {
+  for (int e = lane; e < E; e += 64) msk[e] = 0u;
+  __builtin_amdgcn_wave_barrier();
+  for (int i = lane; i < T * k; i += 64) atomicOr(&msk[s_idx[i]], 1u << (i / k));
+  __builtin_amdgcn_wave_barrier();
+  // lane owns experts [e0, e1): counts, then one tile per expert with tokens
+  const int npl = (E + 63) / 64, e0 = lane * npl, e1 = min(e0 + npl, E);
+  int c_loc = 0, t_loc = 0;
+  for (int e = e0; e < e1; ++e) {
+    const int c = __popc(msk[e]);
+    c_loc += c;
+    t_loc += c > 0;
+  }
+  int c_inc = c_loc, t_inc = t_loc;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int a = __shfl_up(c_inc, d, 64), b = __shfl_up(t_inc, d, 64);
+    if (lane >= d) {
+      c_inc += a;
+      t_inc += b;
+    }
+  }
+  int o = c_inc - c_loc, tb = t_inc - t_loc;
+  for (int e = e0; e < e1; ++e) {
+    const uint32_t m = msk[e];
+    const int c = __popc(m);
+    ds.counts[e] = c;
+    ds.offsets[e] = o;
+    off[e] = o;
+    if (c) ds.tiles[tb++] = make_int4(e, o, c, (int)m);
+    o += c;
+  }
+  const int total = __shfl(c_inc, 63, 64), routed = __shfl(t_inc, 63, 64);
+  if (lane == 0) {
+    ds.offsets[E] = total;
+    if (has_shared) ds.tiles[routed] = make_int4(E, 0, T, 0);
+    *ds.n_tiles = routed + (has_shared ? 1 : 0);
+  }
+  __builtin_amdgcn_wave_barrier();
+  // placement: rank of token t among the tokens of expert e
+  for (int i = lane; i < T * k; i += 64) {
+    const int t = i / k, e = s_idx[i];
+    const int pos = off[e] + __popc(msk[e] & ((1u << t) - 1u));
+    ds.perm[pos] = i;
+    ds.inv[i] = pos;
+    ds.ptok[pos] = t;
+  }
+  for (int i = lane; i < ds.n_cnt; i += 64) ds.cnt[i] = 0;
+}
+
+template <int NV>
+__global__ __launch_bounds__(1024) void k_select_small(const float *__restrict__ logits,
+                                                       const float *__restrict__ sgl,
+                                                       const uint16_t *__restrict__ x,
+                                                       int32_t *__restrict__ topk_idx,
+                                                       float *__restrict__ topk_w,
+                                                       float *__restrict__ sgate,
+                                                       uint16_t *__restrict__ xperm, int T, int E,
+                                                       int k, int H, int has_shared, int has_gate,
+                                                       DispatchOut ds, int fused) {
+  __shared__ int s_idx[SMALL_MT * 32];
+  __shared__ uint32_t s_msk[1024];
+  __shared__ int s_off[1024];
+  const int t = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (t < T) {
+    const float *ar = logits + (size_t)t * E;
+    uint32_t key[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int e = lane + 64 * i;
+      key[i] = e < E ? ordered_key(ar[e]) : 0u;
+    }
+    int seli;
+    wave_topk<NV>(key, E, k, lane, seli);
+    const float selv = lane < k ? ar[seli] : 0.0f;
+    const float vmax = __shfl(selv, 0, 64);
+    const float p = lane < k ? expf(selv - vmax) : 0.0f;
+    float sum = 0.0f;
+    for (int j = 0; j < k; ++j) sum += __shfl(p, j, 64);
+    if (lane < k) {
+      topk_idx[(size_t)t * k + lane] = seli;
+      topk_w[(size_t)t * k + lane] = p / sum;
+      s_idx[t * k + lane] = seli;
+    }
+    if (lane == 0) sgate[t] = has_gate ? 1.0f / (1.0f + expf(-sgl[t])) : 1.0f;
+    if (xperm) write_xperm(x + (size_t)t * H, xperm, nullptr, t, H, lane);
+  }
+  if (!fused) return;
+  __syncthreads();
+  if (t == 0) dispatch_wave(s_idx, T, k, E, has_shared, ds, s_msk, s_off, lane);
 }
 
 template <int NV, bool EXACT>
@@ -478,6 +592,20 @@ hipError_t launch_router_exact(const void *x, const void *rw, const float *bias,
   hipError_t err = launch_router(x, rw, bias, gw, logits, sg_logit,
                                  fused ? fused->ticket : nullptr, T, H, E, s);
   if (err != hipSuccess) return err;
-  return launch_select<true>(logits, sg_logit, nullptr, x, rw, bias, gw, idx, w, sg, xperm,
-                             nullptr, T, H, E, k, has_shared, fused, s);
+  if (T > SMALL_MT) return hipErrorInvalidValue;
+  DispatchOut ds;
+  memset(&ds, 0, sizeof ds);
+  if (fused) ds = *fused;
+  const int nv = (E + 63) / 64;
+#define SMALL_CALL(NVV)                                                                      \
+  k_select_small<NVV><<<1, 64 * T, 0, s>>>(logits, sg_logit, (const uint16_t *)x, idx, w, sg,  \
+                                          (uint16_t *)xperm, T, E, k, H, has_shared,          \
+                                          gw ? 1 : 0, ds, fused ? 1 : 0)
+  if (nv <= 1) SMALL_CALL(1);
+  else if (nv <= 2) SMALL_CALL(2);
+  else if (nv <= 4) SMALL_CALL(4);
+  else if (nv <= 8) SMALL_CALL(8);
+  else SMALL_CALL(16);
+#undef SMALL_CALL
+  return hipGetLastError();
 }

@@ -87,6 +87,8 @@ typedef struct ainfer_moe_shape {
   int32_t reserved;     /* must be 0                                        */
 } ainfer_moe_shape;
 
+/* Device pointers.  Weight and router tensors must be 16-byte aligned, scale
+ * tensors 8-byte aligned (AINFER_ERR_ARG otherwise). */
 typedef struct ainfer_moe_weights {
   const void *router_w;      /* [E][H] bf16                                 */
   const float *router_bias;  /* [E] fp32 added to the logits, or NULL       */
