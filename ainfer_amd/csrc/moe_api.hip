@@ -100,7 +100,7 @@ Layout layout_of(const ainfer_moe_shape &s, int Tm) {
   L.perm = take(T * k * 4);
   L.inv = take(T * k * 4);
   L.ptok = take(T * k * 4);
-  L.tiles = take((size_t)max_tiles_bound(s, (int)T, SMALL_MT) * 16);  // >= the GEMM_MT bound
+  L.tiles = take((size_t)max_tiles_bound(s, (int)T, DEC_MT) * 16);  // >= every other bound
   L.n_tiles = take(4);
   L.cnt = take(T * (H / 16) * 4);
   L.ticket = take(4);
@@ -250,7 +250,8 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
   a.H = H;
   a.I = s->inter;
   a.Is = s->shared_inter;
-  const int max_tiles = max_tiles_bound(*s, T, SMALL_MT);
+  const int smt = T <= EXACT_ROUTER_MAX_T ? DEC_MT : SMALL_MT;  // tiles of the dispatch above
+  const int max_tiles = max_tiles_bound(*s, T, smt);
   // k-groups per wave and 16-row groups per wave, measured at T = 1, 4, 16
   const int kbw = 4, kbw_down = 2;
   // gate/up + SiLU-mul
@@ -266,7 +267,7 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
   a.a_shared = at<uint16_t>(ws, L.xperm);
   a.act = at<uint16_t>(ws, L.act);
   a.act_s = at<uint16_t>(ws, L.act_s);
-  HIP_TRY(launch_expert_stream(0, s->scale_dtype, a, max_tiles, kbw, RG_GATE_UP, st));
+  HIP_TRY(launch_expert_stream(0, s->scale_dtype, a, max_tiles, kbw, RG_GATE_UP, smt, st));
   pc->end(4);
   // down + combine
   a.w0 = w->w_down;
@@ -280,7 +281,7 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
   a.a_routed = at<uint16_t>(ws, L.act);
   a.a_shared = at<uint16_t>(ws, L.act_s);
   a.o = at<uint16_t>(ws, L.o);
-  HIP_TRY(launch_expert_stream(1, s->scale_dtype, a, max_tiles, kbw_down, RG_DOWN, st));
+  HIP_TRY(launch_expert_stream(1, s->scale_dtype, a, max_tiles, kbw_down, RG_DOWN, smt, st));
   pc->end(5);
   HIP_TRY(launch_combine(at<uint16_t>(ws, L.o), d.inv, at<float>(ws, L.w), at<float>(ws, L.sg),
                          has_shared, resid, y, T, k, H, st));

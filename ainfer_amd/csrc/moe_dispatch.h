@@ -45,17 +45,8 @@ __device__ __forceinline__ void dispatch_small_block(const int32_t *__restrict__
     ds.counts[e] = c;
     ds.offsets[e] = off_e;
     off_lds[e] = off_e;
-    // .w: for T <= 32 the tile's token set as a bit mask (lane m of an
-    // expert kernel takes the m-th set bit, no ptok load); 0 = use ptok
-    unsigned long long rest = mask[e];
-    for (int m0 = 0; m0 < c; m0 += SMALL_MT) {
-      uint32_t tm = 0;
-      for (int i = 0; i < SMALL_MT && rest; ++i) {
-        tm |= (uint32_t)(rest & (~rest + 1ull));
-        rest &= rest - 1ull;
-      }
-      ds.tiles[tile++] = make_int4(e, off_e + m0, min(SMALL_MT, c - m0), T <= 32 ? (int)tm : 0);
-    }
+    for (int m0 = 0; m0 < c; m0 += SMALL_MT)
+      ds.tiles[tile++] = make_int4(e, off_e + m0, min(SMALL_MT, c - m0), 0);
     off_e += c;
   }
   const int routed_tiles = scan_t[255];

@@ -101,16 +101,7 @@ __global__ __launch_bounds__(1024) void k_expert(ExpertArgs a) {
   uint32_t aoff;
   const uint16_t *abase;
   if (MODE == 0) {
-    int tok;
-    if (shared) {
-      tok = pos0 + mm;
-    } else if (t.w != 0) {  // token set carried by the tile: the mm-th set bit
-      uint32_t bits = (uint32_t)t.w;
-      for (int i = 0; i < mm; ++i) bits &= bits - 1u;
-      tok = __builtin_ctz(bits);
-    } else {
-      tok = a.ptok[pos0 + mm];
-    }
+    const int tok = shared ? pos0 + mm : a.ptok[pos0 + mm];
     abase = a.a_routed;
     aoff = (uint32_t)tok * (uint32_t)a.H * 2u;
   } else {
@@ -218,6 +209,170 @@ __global__ __launch_bounds__(1024) void k_expert(ExpertArgs a) {
   }
 }
 
+
+__device__ __forceinline__ void dma16(const void *g, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(g), "s"(lds_addr)
+               : "memory", "m0");
+}
+
+// Decode variant for tiles of at most MT tokens (MT = 4): the same work
+// item and arithmetic as k_expert, but each wave copies its tile rows
+// (MT tokens x its KBW k-groups, MT * KBW * 256 bytes) into a private LDS
+// region with global->LDS DMA before the weight loads, and reads the A
+// fragments from LDS per k-group.  A then holds no registers while the
+// weight loads are in flight (more waves per SIMD) and costs MT * KBW / 4
+// vector-memory instructions instead of 4 * KBW.  Rows past the tile's
+// token count are copies of its last row; their results are never stored.
+template <int SD, int KBW, int RG, int MT, int MODE>
+__global__ __launch_bounds__(1024) void k_expert_lds(ExpertArgs a) {
+  constexpr int AROW = KBW * 256;  // bytes of one token row in this wave's k-range
+  constexpr int AW = MT * AROW;    // LDS bytes per wave
+  static_assert(AW % 1024 == 0, "one DMA instruction moves 1 KB");
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int nw = a.WK * a.WR;
+  float *red = (float *)(lds + nw * AW);  // K-split partial sums [2][nw][RG][256]
+  const int n_rg = a.n_slabs;
+  const int tile_id = blockIdx.x / n_rg, slab = blockIdx.x % n_rg;
+  if (tile_id >= *a.n_tiles) return;
+  const int4 t = a.tiles[tile_id];
+  const int e = t.x, pos0 = t.y, mcnt = t.z;
+  const bool shared = e == a.E;
+  const int N = MODE == 0 ? (shared ? a.Is : a.I) : a.H;
+  const int K = MODE == 0 ? a.H : (shared ? a.Is : a.I);
+  const int KB = K >> 7;
+  if (slab * a.WR * RG * 16 >= N) return;
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int kw = wave % a.WK, wr = wave / a.WK;
+  const int m = lane & 15, q = lane >> 4;
+  const int n0 = (slab * a.WR + wr) * RG * 16;
+  const bool act = n0 < N && kw * KBW < KB;
+  const int kb0 = act ? kw * KBW : 0;
+  const uint32_t alds = (uint32_t)(uintptr_t)lds + (uint32_t)(wave * AW);
+
+  // ---- sources of the A copy (the token ids are loaded first: waiting for
+  // them later must not wait for the weight loads) --------------------------
+  const uint8_t *asrc[AW / 1024];
+#pragma unroll
+  for (int d = 0; d < AW / 1024; ++d) {
+    const int off = d * 1024 + lane * 16, r = min(off / AROW, mcnt - 1), c = off % AROW;
+    const uint8_t *src;
+    if (MODE == 0) {
+      const int tok = shared ? pos0 + r : a.ptok[pos0 + r];
+      src = (const uint8_t *)(a.a_routed + (size_t)tok * a.H);
+    } else {
+      src = (const uint8_t *)((shared ? a.a_shared : a.a_routed) + (size_t)(pos0 + r) * K);
+    }
+    asrc[d] = src + kb0 * 256 + c;
+  }
+  // ---- weight loads ------------------------------------------------------
+  const size_t rowb = (size_t)K / 2;
+  const uint8_t *w0 = shared ? a.ws0 : a.w0 + (size_t)e * N * rowb;
+  const uint16_t *s0 = shared ? a.ss0 : a.s0 + (size_t)e * N * KB;
+  const uint8_t *w1 = nullptr;
+  const uint16_t *s1 = nullptr;
+  if (MODE == 0) {
+    w1 = shared ? a.ws1 : a.w1 + (size_t)e * N * rowb;
+    s1 = shared ? a.ss1 : a.s1 + (size_t)e * N * KB;
+  }
+  u32x4 B0[RG][KBW], B1[RG][KBW];
+  uint16_t S0[RG][KBW], S1[RG][KBW];
+#pragma unroll
+  for (int g = 0; g < RG; ++g) {
+    const int n = act ? min(n0 + g * 16 + m, N - 1) : m;
+    const size_t rb = (size_t)n * rowb + q * 16;
+#pragma unroll
+    for (int i = 0; i < KBW; ++i) B0[g][i] = ldg_stream(w0 + rb + (size_t)(kb0 + i) * 64);
+    load_scales<KBW>(s0 + (size_t)n * KB + kb0, S0[g]);
+    if (MODE == 0) {
+#pragma unroll
+      for (int i = 0; i < KBW; ++i) B1[g][i] = ldg_stream(w1 + rb + (size_t)(kb0 + i) * 64);
+      load_scales<KBW>(s1 + (size_t)n * KB + kb0, S1[g]);
+    }
+  }
+  // ---- A: this wave's tile rows -> LDS (row r at r * AROW), issued after the
+  // weight loads; their sources were resolved before them ---------------------
+  if (act) {
+#pragma unroll
+    for (int d = 0; d < AW / 1024; ++d) dma16(asrc[d], alds + d * 1024);
+  }
+  // every load and DMA of this wave has landed
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  // ---- MFMA ---------------------------------------------------------------
+  f32x4 tot0[RG], tot1[RG];
+#pragma unroll
+  for (int g = 0; g < RG; ++g) tot0[g] = tot1[g] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (act) {
+    uint32_t magic;
+    asm volatile("v_mov_b32 %0, 0x43004300" : "=v"(magic));
+    const u32x4 ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
+    const uint8_t *arow = lds + wave * AW + (m % MT) * AROW + q * 64;
+#pragma unroll
+    for (int i = 0; i < KBW; ++i) {
+      u32x4 A[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) A[j] = *(const u32x4 *)(arow + i * 256 + j * 16);
+      f32x4 xs = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xs = mfma_bf16_16x16x32(A[j], ones, xs);
+      const f32x4 c0 = xs * -136.0f;
+#pragma unroll
+      for (int g = 0; g < RG; ++g) {
+        {
+          const u32x4 b = B0[g][i] ^ 0x88888888u;
+          f32x4 acc = c0;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc = mfma_bf16_16x16x32(A[j], nib_slice(b, j, magic), acc);
+          tot0[g] += scale_to_f32<SD>(S0[g][i]) * acc;
+        }
+        if (MODE == 0) {
+          const u32x4 b = B1[g][i] ^ 0x88888888u;
+          f32x4 acc = c0;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc = mfma_bf16_16x16x32(A[j], nib_slice(b, j, magic), acc);
+          tot1[g] += scale_to_f32<SD>(S1[g][i]) * acc;
+        }
+      }
+    }
+  }
+  // ---- K split meets in LDS: D layout lane (q, m) holds tokens 4q+r, row m
+  float *red0 = red, *red1 = red + nw * RG * 256;
+#pragma unroll
+  for (int g = 0; g < RG; ++g)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      red0[(wave * RG + g) * 256 + (4 * q + r) * 16 + m] = tot0[g][r];
+      if (MODE == 0) red1[(wave * RG + g) * 256 + (4 * q + r) * 16 + m] = tot1[g][r];
+    }
+  __syncthreads();
+  // tokens < mcnt <= MT only
+  const int nthr = nw * 64;
+  for (int idx = threadIdx.x; idx < a.WR * RG * 16 * MT; idx += nthr) {
+    const int rgrp = idx / (16 * MT), cell = idx % (16 * MT);  // rgrp = wr * RG + g
+    const int rwr = rgrp / RG, g = rgrp % RG;
+    const int tm = cell >> 4, tn = cell & 15;
+    const int row = (slab * a.WR + rwr) * RG * 16 + g * 16 + tn;
+    if (tm >= mcnt || row >= N) continue;
+    float gs = 0.f, u = 0.f;
+    for (int w = 0; w < a.WK; ++w) {
+      const int src = ((rwr * a.WK + w) * RG + g) * 256 + cell;
+      gs += red0[src];
+      if (MODE == 0) u += red1[src];
+    }
+    if (MODE == 0) {
+      uint16_t *dst = shared ? a.act_s : a.act;
+      dst[(size_t)(pos0 + tm) * N + perm32_pos(row)] = f32_to_bf16(silu_mul(gs, u));
+    } else {
+      const size_t orow = shared ? (size_t)a.T * a.k + pos0 + tm : (size_t)(pos0 + tm);
+      a.o[orow * a.H + row] = f32_to_bf16(gs);
+    }
+  }
+}
+
 }  // namespace
 
 // KBW k-groups per wave (the preferred count, raised until one row group
@@ -242,8 +397,17 @@ bool expert_geometry(int mode, int H, int I, int Is, int pref_kbw, int *KBW, int
 }
 
 template <int SD, int MODE, int RG>
-void launch_kbw(int kbw, unsigned grid, int threads, size_t lds, const ExpertArgs &a,
+void launch_kbw(int kbw, int mt, unsigned grid, int threads, size_t lds, const ExpertArgs &a,
                 hipStream_t s) {
+  if (mt == DEC_MT) {
+    if (kbw == 1)
+      k_expert_lds<SD, 1, RG, DEC_MT, MODE><<<grid, threads, lds, s>>>(a);
+    else if (kbw == 2)
+      k_expert_lds<SD, 2, RG, DEC_MT, MODE><<<grid, threads, lds, s>>>(a);
+    else
+      k_expert_lds<SD, 4, RG, DEC_MT, MODE><<<grid, threads, lds, s>>>(a);
+    return;
+  }
   if (kbw == 1)
     k_expert<SD, 1, RG, MODE><<<grid, threads, lds, s>>>(a);
   else if (kbw == 2)
@@ -253,39 +417,42 @@ void launch_kbw(int kbw, unsigned grid, int threads, size_t lds, const ExpertArg
 }
 
 template <int SD, int MODE>
-void launch_rg(int rg, int kbw, unsigned grid, int threads, size_t lds, const ExpertArgs &a,
-               hipStream_t s) {
+void launch_rg(int rg, int kbw, int mt, unsigned grid, int threads, size_t lds,
+               const ExpertArgs &a, hipStream_t s) {
   if (rg == 1)
-    launch_kbw<SD, MODE, 1>(kbw, grid, threads, lds, a, s);
+    launch_kbw<SD, MODE, 1>(kbw, mt, grid, threads, lds, a, s);
   else if (rg == 2)
-    launch_kbw<SD, MODE, 2>(kbw, grid, threads, lds, a, s);
+    launch_kbw<SD, MODE, 2>(kbw, mt, grid, threads, lds, a, s);
   else
-    launch_kbw<SD, MODE, 4>(kbw, grid, threads, lds, a, s);
+    launch_kbw<SD, MODE, 4>(kbw, mt, grid, threads, lds, a, s);
 }
 
 hipError_t launch_expert_stream(int mode, int scale_dtype, ExpertArgs a, int max_tiles,
-                                int pref_kbw, int rg, hipStream_t s) {
+                                int pref_kbw, int rg, int mt, hipStream_t s) {
   if (max_tiles <= 0) return hipSuccess;
   if (rg != 1 && rg != 2 && rg != 4) return hipErrorInvalidValue;
+  if (mt != DEC_MT && mt != SMALL_MT) return hipErrorInvalidValue;
   int kbw;
   if (!expert_geometry(mode, a.H, a.I, a.Is, pref_kbw, &kbw, &a.WK, &a.WR))
     return hipErrorInvalidValue;
   const int Nmax = mode == 0 ? (a.I > a.Is ? a.I : a.Is) : a.H;
   a.n_slabs = (Nmax + 16 * rg * a.WR - 1) / (16 * rg * a.WR);
   const int threads = a.WK * a.WR * 64;
-  const size_t lds = sizeof(float) * 2 * (size_t)a.WK * a.WR * rg * 256;
+  size_t lds = sizeof(float) * 2 * (size_t)a.WK * a.WR * rg * 256;
+  if (mt == DEC_MT) lds += (size_t)a.WK * a.WR * DEC_MT * kbw * 256;  // A staging
+  if (lds > 160 * 1024) return hipErrorInvalidValue;
   const long grid = (long)max_tiles * a.n_slabs;
   if (grid > 0x7FFFFFFF) return hipErrorInvalidValue;
   if (mode == 0) {
     if (scale_dtype == AINFER_SCALE_FP16)
-      launch_rg<AINFER_SCALE_FP16, 0>(rg, kbw, (unsigned)grid, threads, lds, a, s);
+      launch_rg<AINFER_SCALE_FP16, 0>(rg, kbw, mt, (unsigned)grid, threads, lds, a, s);
     else
-      launch_rg<AINFER_SCALE_BF16, 0>(rg, kbw, (unsigned)grid, threads, lds, a, s);
+      launch_rg<AINFER_SCALE_BF16, 0>(rg, kbw, mt, (unsigned)grid, threads, lds, a, s);
   } else {
     if (scale_dtype == AINFER_SCALE_FP16)
-      launch_rg<AINFER_SCALE_FP16, 1>(rg, kbw, (unsigned)grid, threads, lds, a, s);
+      launch_rg<AINFER_SCALE_FP16, 1>(rg, kbw, mt, (unsigned)grid, threads, lds, a, s);
     else
-      launch_rg<AINFER_SCALE_BF16, 1>(rg, kbw, (unsigned)grid, threads, lds, a, s);
+      launch_rg<AINFER_SCALE_BF16, 1>(rg, kbw, mt, (unsigned)grid, threads, lds, a, s);
   }
   return hipGetLastError();
 }

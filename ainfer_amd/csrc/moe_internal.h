@@ -18,7 +18,7 @@ struct ExpertArgs {
   uint16_t *act_s;            // MODE 0 out: [T][Is]
   uint16_t *o;                // MODE 1 out: [Tk + T][H] bf16
   const int32_t *ptok;        // token of each dispatch position
-  const int4 *tiles;          // (expert, first position, rows, token mask or 0)
+  const int4 *tiles;          // (expert, first position, rows, 0)
   const int32_t *n_tiles;
   int T, k, E, H, I, Is;
   int WK, WR, n_slabs;        // set by the launcher
@@ -112,11 +112,13 @@ bool expert_geometry(int mode, int H, int I, int Is, int pref_kbw, int *KBW, int
 #ifndef RG_DOWN
 #define RG_DOWN 2
 #endif
-// rg: 16-row groups per wave (1, 2 or 4) sharing one load of the token rows
+// rg: 16-row groups per wave (1, 2 or 4) sharing one load of the token rows;
+// mt: tokens per tile the dispatch produced (DEC_MT: A staged in LDS, or SMALL_MT)
 hipError_t launch_expert_stream(int mode, int scale_dtype, ExpertArgs a, int max_tiles,
-                                int pref_kbw, int rg, hipStream_t s);
+                                int pref_kbw, int rg, int mt, hipStream_t s);
 
 // tile height of the small-M expert kernels
 constexpr int SMALL_MT = 16;
+constexpr int DEC_MT = 4;  // tile rows of the decode dispatch (T <= EXACT_ROUTER_MAX_T)
 // largest T routed by the fused top-k + dispatch launch
 constexpr int FUSED_DISPATCH_MAX_T = 64;

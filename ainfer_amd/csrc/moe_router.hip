@@ -193,25 +193,47 @@ constexpr int SEL_WAVES = 4;
 // k rounds of (largest key, then lowest expert among equal keys): the exact
 // top-k of key[] (lane l, slot i = expert l + 64 i) in value-descending,
 // expert-ascending order.  Lane j < k returns the j-th pick; the return value
-// is the k-th largest key.
+// is the k-th largest key.  Every lane keeps its best untaken slot; a round
+// is one wave max, then the winner from a ballot (a second reduction over
+// expert ids only when several lanes hold the maximum), and only the winning
+// lane rescans its slots.
 template <int NV>
 __device__ __forceinline__ uint32_t wave_topk(const uint32_t (&key)[NV], int E, int k, int lane,
                                               int &seli) {
-  uint32_t taken = 0, kth = 0;
+  uint32_t taken = 0;
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+    if (lane + 64 * i >= E) taken |= 1u << i;
+  uint32_t bk = 0;
+  int bs = -1;
+  auto rescan = [&]() {
+    bk = 0;
+    bs = -1;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const bool better = !((taken >> i) & 1u) && (bs < 0 || key[i] > bk);
+      bk = better ? key[i] : bk;
+      bs = better ? i : bs;
+    }
+  };
+  rescan();
+  uint32_t kth = 0;
   seli = 0;
   for (int j = 0; j < k; ++j) {
-    uint32_t bk = 0;
-    int bi = 0x7FFFFFFF;
-#pragma unroll
-    for (int i = 0; i < NV; ++i)
-      if (lane + 64 * i < E && !(taken & (1u << i)) && (bi == 0x7FFFFFFF || key[i] > bk)) {
-        bk = key[i];
-        bi = i;
-      }
-    const uint32_t wk = wave_max_u32(bi == 0x7FFFFFFF ? 0u : bk);
-    const uint32_t we = wave_min_u32(bi != 0x7FFFFFFF && bk == wk ? (uint32_t)(lane + 64 * bi)
-                                                                   : 0xFFFFFFFFu);
-    if ((int)(we & 63) == lane) taken |= 1u << (we >> 6);
+    const uint32_t wk = wave_max_u32(bs >= 0 ? bk : 0u);
+    const bool hold = bs >= 0 && bk == wk;
+    const uint64_t tie = __ballot(hold);
+    uint32_t we;
+    if (__popcll(tie) == 1) {
+      const int wl = __builtin_ctzll(tie);
+      we = (uint32_t)(wl + 64 * __builtin_amdgcn_readlane(bs, wl));
+    } else {
+      we = wave_min_u32(hold ? (uint32_t)(lane + 64 * bs) : 0xFFFFFFFFu);
+    }
+    if (lane == (int)(we & 63)) {
+      taken |= 1u << (we >> 6);
+      rescan();
+    }
     if (lane == j) seli = (int)we;
     kth = wk;
   }
@@ -288,8 +310,9 @@ __global__ __launch_bounds__(256) void k_select(const float *__restrict__ approx
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int e = lane + 64 * i;
-      key[i] = e < E ? ordered_key(ar[e]) : 0u;
-      if (!EXACT && e < E) wn = fmaxf(wn, wnorm[e]);
+      const float v = ar[min(e, E - 1)];  // unconditional: loads issue together
+      key[i] = e < E ? ordered_key(v) : 0u;
+      if (!EXACT) wn = fmaxf(wn, e < E ? wnorm[min(e, E - 1)] : 0.0f);
     }
     int seli;
     const uint32_t kth = wave_topk<NV>(key, E, k, lane, seli);
@@ -407,7 +430,7 @@ __global__ __launch_bounds__(256) void k_select(const float *__restrict__ approx
 // Decode routing for T <= 16 in one block, one wave per token: the exact
 // top-k of the canonical logits, softmax weights, the shared-expert gate and
 // the MFMA-order copy of x; then wave 0 builds the dispatch from the picks
-// kept in LDS (one tile per routed expert, the token set in the tile's .w).
+// kept in LDS (tiles of at most DEC_MT tokens).
 __device__ __forceinline__ void dispatch_wave(const int *__restrict__ s_idx, int T, int k, int E,
                                               int has_shared, const DispatchOut &ds,
                                               uint32_t *msk, int *off, int lane) {
@@ -421,7 +444,7 @@ __device__ __forceinline__ void dispatch_wave(const int *__restrict__ s_idx, int
   for (int e = e0; e < e1; ++e) {
     const int c = __popc(msk[e]);
     c_loc += c;
-    t_loc += c > 0;
+    t_loc += (c + DEC_MT - 1) / DEC_MT;
   }
   int c_inc = c_loc, t_inc = t_loc;
 #pragma unroll
@@ -439,14 +462,15 @@ __device__ __forceinline__ void dispatch_wave(const int *__restrict__ s_idx, int
     ds.counts[e] = c;
     ds.offsets[e] = o;
     off[e] = o;
-    if (c) ds.tiles[tb++] = make_int4(e, o, c, (int)m);
+    for (int m0 = 0; m0 < c; m0 += DEC_MT) ds.tiles[tb++] = make_int4(e, o + m0, min(DEC_MT, c - m0), 0);
     o += c;
   }
   const int total = __shfl(c_inc, 63, 64), routed = __shfl(t_inc, 63, 64);
+  const int nsh = has_shared ? (T + DEC_MT - 1) / DEC_MT : 0;
+  if (lane < nsh) ds.tiles[routed + lane] = make_int4(E, lane * DEC_MT, min(DEC_MT, T - lane * DEC_MT), 0);
   if (lane == 0) {
     ds.offsets[E] = total;
-    if (has_shared) ds.tiles[routed] = make_int4(E, 0, T, 0);
-    *ds.n_tiles = routed + (has_shared ? 1 : 0);
+    *ds.n_tiles = routed + nsh;
   }
   __builtin_amdgcn_wave_barrier();
   // placement: rank of token t among the tokens of expert e
@@ -480,7 +504,8 @@ __global__ __launch_bounds__(1024) void k_select_small(const float *__restrict__
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int e = lane + 64 * i;
-      key[i] = e < E ? ordered_key(ar[e]) : 0u;
+      const float v = ar[min(e, E - 1)];  // unconditional: loads issue together
+      key[i] = e < E ? ordered_key(v) : 0u;
     }
     int seli;
     wave_topk<NV>(key, E, k, lane, seli);
