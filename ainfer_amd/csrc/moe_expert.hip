@@ -16,12 +16,10 @@
 // weight row l%16 and k-quarter l/16 of every group: one 16-byte load per
 // lane per group and matrix.
 //
-// Why this shape on MI355X: at decode sizes every wave runs its code once,
-// and each dispatch starts with a cold instruction cache, so the code a
-// wave executes is kept short and the bytes in flight come from the number
-// of waves (up to 16 per block), not from deep per-wave pipelining.  Larger
-// batches use more k-groups per wave (more bytes in flight per wave).  Every
-// branch is wave-uniform and no load is predicated, so each wave issues all
+// Why this shape on MI355X: decode is bound by weight bytes in flight, so
+// every wave issues all its weight loads at once and the waves per SIMD
+// (register count) set the rate.  Larger batches use more k-groups per wave.
+// Every branch is wave-uniform and no load is predicated, so each wave issues
 // its loads back to back; token rows past the tile's count are read through
 // a buffer descriptor at an out-of-range offset, which returns zeros
 // without touching memory.
