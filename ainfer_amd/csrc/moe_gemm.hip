@@ -388,6 +388,134 @@ __global__ __launch_bounds__(128 * WN) void k_expert_gemm(GemmArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Router logits for prefill: approx[t][e] = sum_k x[t][k] * w[e][k] (+ bias)
+// on bf16 MFMA, fp32 accumulation.  Block tile: 64 tokens x 128 experts,
+// 4 waves as 2 (tokens) x 2 (experts), each 32 x 64 = 2 x 4 MFMA tiles.  K
+// streams through a 3-stage LDS ring in 64-wide steps (x rows and w rows,
+// 128 bytes each, 16-byte chunk c of row r stored at c ^ (r & 7)).  The
+// blocks after the GEMM tiles compute ||w_e|| (used only as the bound of
+// the canonical refine).
+// ---------------------------------------------------------------------------
+constexpr int RG_BM = 64, RG_BN = 128, RG_BK = 64, RG_ST = 3;
+constexpr int RG_A = RG_BM * RG_BK * 2, RG_B = RG_BN * RG_BK * 2;  // bytes per stage
+constexpr int RG_STAGE = RG_A + RG_B;
+constexpr int RG_DMA = RG_STAGE / (256 * 16);  // per thread per stage: 6
+constexpr int RG_NORM_ROWS = 16;                // experts per norm block
+
+__global__ __launch_bounds__(256) void k_router_gemm(const uint16_t *__restrict__ x,
+                                                     const uint16_t *__restrict__ rw,
+                                                     const float *__restrict__ bias,
+                                                     float *__restrict__ approx,
+                                                     float *__restrict__ wnorm, int T, int H,
+                                                     int E, int n_mt, int n_nt) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int n_items = n_mt * n_nt;
+  if ((int)blockIdx.x >= n_items) {
+    // ---- row norms: wave w takes rows e0 + 4w .. e0 + 4w + 3 -------------
+    const int e0 = ((int)blockIdx.x - n_items) * RG_NORM_ROWS + wave * 4;
+    for (int r = 0; r < 4; ++r) {
+      const int e = e0 + r;
+      if (e >= E) break;
+      const uint16_t *row = rw + (size_t)e * H;
+      float ss = 0.0f;
+      for (int c = lane; c < (H >> 3); c += 64) {
+        const u32x4 v = *(const u32x4 *)(row + 8 * c);
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const float lo = __uint_as_float(v[d] << 16), hi = __uint_as_float(v[d] & 0xFFFF0000u);
+          ss = __builtin_fmaf(lo, lo, ss);
+          ss = __builtin_fmaf(hi, hi, ss);
+        }
+      }
+      for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
+      if (lane == 0) wnorm[e] = sqrtf(ss);
+    }
+    return;
+  }
+  const int lb = xcd_remap(blockIdx.x, n_items);
+  const int mt = lb / n_nt, nt = lb % n_nt;  // the n_nt expert tiles of a token tile share an XCD
+  const int t0 = mt * RG_BM, e0 = nt * RG_BN;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int m16 = lane & 15, q = lane >> 4;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)lds;
+
+  // DMA sources: slot s = (i*4 + wave)*64 + lane; row s/8, stored chunk s%8
+  const uint8_t *src[RG_DMA];
+#pragma unroll
+  for (int i = 0; i < RG_DMA; ++i) {
+    const int sl = (i * 4 + wave) * 64 + lane;
+    const int r = sl >> 3, c = (sl & 7) ^ (r & 7);
+    if (r < RG_BM) {
+      src[i] = (const uint8_t *)(x + (size_t)min(t0 + r, T - 1) * H) + c * 16;
+    } else {
+      src[i] = (const uint8_t *)(rw + (size_t)min(e0 + r - RG_BM, E - 1) * H) + c * 16;
+    }
+  }
+  auto issue = [&](int g) {
+    const uint32_t base = lds0 + (uint32_t)(g % RG_ST) * RG_STAGE;
+#pragma unroll
+    for (int i = 0; i < RG_DMA; ++i)
+      dma16(src[i] + g * (RG_BK * 2), base + (uint32_t)((i * 4 + wave) * 1024));
+  };
+  const int G = H / RG_BK;
+  issue(0);
+  if (G > 1) issue(1);
+  f32x4 acc[2][4];
+#pragma unroll
+  for (int ms = 0; ms < 2; ++ms)
+#pragma unroll
+    for (int ns = 0; ns < 4; ++ns) acc[ms][ns] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int g = 0; g < G; ++g) {
+    if (g + 2 < G) {
+      issue(g + 2);
+      wait_vm<2 * RG_DMA>();
+    } else if (g + 1 < G) {
+      wait_vm<RG_DMA>();
+    } else {
+      wait_vm<0>();
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    block_barrier();
+    const uint8_t *sa = lds + (g % RG_ST) * RG_STAGE, *sb = sa + RG_A;
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {  // two 32-wide MFMA steps
+      u32x4 af[2], bf[4];
+#pragma unroll
+      for (int ms = 0; ms < 2; ++ms) {
+        const int r = wm * 32 + ms * 16 + m16;
+        af[ms] = *(const u32x4 *)(sa + r * 128 + (((4 * s2 + q) ^ (r & 7)) << 4));
+      }
+#pragma unroll
+      for (int ns = 0; ns < 4; ++ns) {
+        const int r = wn * 64 + ns * 16 + m16;
+        bf[ns] = *(const u32x4 *)(sb + r * 128 + (((4 * s2 + q) ^ (r & 7)) << 4));
+      }
+#pragma unroll
+      for (int ms = 0; ms < 2; ++ms)
+#pragma unroll
+        for (int ns = 0; ns < 4; ++ns) acc[ms][ns] = mfma_bf16_16x16x32(af[ms], bf[ns], acc[ms][ns]);
+    }
+    block_barrier();  // stage g may be overwritten by the DMA issued next iteration
+  }
+  // lane (q, m16) of tile (ms, ns): tokens wm*32 + ms*16 + 4q + r, expert wn*64 + ns*16 + m16
+#pragma unroll
+  for (int ns = 0; ns < 4; ++ns) {
+    const int e = e0 + wn * 64 + ns * 16 + m16;
+    if (e >= E) continue;
+    const float b = bias ? bias[e] : 0.0f;
+#pragma unroll
+    for (int ms = 0; ms < 2; ++ms)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = t0 + wm * 32 + ms * 16 + 4 * q + r;
+        if (t < T) approx[(size_t)t * E + e] = bias ? acc[ms][ns][r] + b : acc[ms][ns][r];
+      }
+  }
+}
+
 template <int WN, int STAGES_>
 hipError_t launch_geo(int mode, int scale_dtype, GemmArgs a, int max_tiles, hipStream_t s) {
   using Gm = Geo<WN, STAGES_>;
@@ -417,6 +545,19 @@ hipError_t launch_geo(int mode, int scale_dtype, GemmArgs a, int max_tiles, hipS
 }
 
 }  // namespace
+
+hipError_t launch_router_gemm(const void *x, const void *rw, const float *bias, float *approx,
+                              float *wnorm, int T, int H, int E, hipStream_t s) {
+  if (T <= 0) return hipSuccess;
+  if (H % RG_BK) return hipErrorInvalidValue;
+  const int n_mt = (T + RG_BM - 1) / RG_BM, n_nt = (E + RG_BN - 1) / RG_BN;
+  const int n_norm = (E + RG_NORM_ROWS - 1) / RG_NORM_ROWS;
+  const long grid = (long)n_mt * n_nt + n_norm;
+  if (grid > 0x7FFFFFFF) return hipErrorInvalidValue;
+  k_router_gemm<<<(unsigned)grid, 256, RG_ST * RG_STAGE, s>>>(
+      (const uint16_t *)x, (const uint16_t *)rw, bias, approx, wnorm, T, H, E, n_mt, n_nt);
+  return hipGetLastError();
+}
 
 // Both GEMM modes of one forward must use the same geometry (MODE 1 reads
 // the act partial sums MODE 0 wrote).

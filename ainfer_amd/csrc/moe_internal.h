@@ -42,6 +42,9 @@ struct GemmArgs {
   int T, k, E, H, I, Is;
   int n_nblk, aslots;         // set by the launcher
 };
+// Prefill router: approximate logits (+ bias) and router row norms, tiled bf16 MFMA GEMM.
+hipError_t launch_router_gemm(const void *x, const void *rw, const float *bias, float *approx,
+                              float *wnorm, int T, int H, int E, hipStream_t s);
 hipError_t launch_expert_gemm(int mode, int scale_dtype, GemmArgs a, int max_tiles,
                               hipStream_t s);
 // token-tile height of the prefill GEMM and the T above which it is used

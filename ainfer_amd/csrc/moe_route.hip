@@ -257,12 +257,16 @@ __global__ __launch_bounds__(1024) void k_dispatch_scan(int32_t *__restrict__ ch
   __shared__ int32_t sc[1024];
   __shared__ int32_t st[1024];
   const int e = threadIdx.x;
+  constexpr int CB = 16;  // chunk counts loaded together (independent loads)
   int total = 0;
   if (e < E) {
-    for (int c = 0; c < nchunks; ++c) {
-      int v = chunk_counts[(size_t)c * E + e];
-      chunk_counts[(size_t)c * E + e] = total;  // exclusive within expert
-      total += v;
+    for (int c0 = 0; c0 < nchunks; c0 += CB) {
+      int v[CB];
+#pragma unroll
+      for (int j = 0; j < CB; ++j)
+        v[j] = c0 + j < nchunks ? chunk_counts[(size_t)(c0 + j) * E + e] : 0;
+#pragma unroll
+      for (int j = 0; j < CB; ++j) total += v[j];
     }
   }
   int ntile = (e < E) ? (total + mt - 1) / mt : 0;
@@ -283,7 +287,19 @@ __global__ __launch_bounds__(1024) void k_dispatch_scan(int32_t *__restrict__ ch
   if (e < E) {
     ds.counts[e] = total;
     ds.offsets[e] = base;
-    for (int c = 0; c < nchunks; ++c) chunk_counts[(size_t)c * E + e] += base;
+    // chunk_counts[c][e] becomes the first position of chunk c's tokens of e
+    int run = base;
+    for (int c0 = 0; c0 < nchunks; c0 += CB) {
+      int v[CB];
+#pragma unroll
+      for (int j = 0; j < CB; ++j)
+        v[j] = c0 + j < nchunks ? chunk_counts[(size_t)(c0 + j) * E + e] : 0;
+#pragma unroll
+      for (int j = 0; j < CB; ++j) {
+        if (c0 + j < nchunks) chunk_counts[(size_t)(c0 + j) * E + e] = run;
+        run += v[j];
+      }
+    }
     if (ds.tiles)
       for (int i = 0; i < ntile; ++i)
         ds.tiles[tbase + i] = make_int4(e, base + i * mt, min(mt, total - i * mt), 0);

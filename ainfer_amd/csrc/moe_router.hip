@@ -582,6 +582,12 @@ hipError_t launch_router_fast(const void *x, const void *rw, const float *bias, 
                               int has_shared, const DispatchOut *fused, hipStream_t s) {
   if (T == 0) return hipSuccess;
   // ---- approximate logits + row norms ------------------------------------
+  if (T >= GEMM_MIN_T) {
+    hipError_t err = launch_router_gemm(x, rw, bias, approx, wnorm, T, H, E, s);
+    if (err != hipSuccess) return err;
+    return launch_select<false>(approx, nullptr, wnorm, x, rw, bias, gw, idx, w, sg, xperm,
+                                xsum, T, H, E, k, has_shared, fused, s);
+  }
   const int MS = T <= 16 ? 1 : (T <= 32 ? 2 : 4);
   const int mt = 16 * MS;
   // decode: one token tile, K split over up to 16 waves; prefill: 4 waves
