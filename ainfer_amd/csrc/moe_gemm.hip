@@ -161,9 +161,8 @@ __global__ __launch_bounds__(128 * WN) void k_expert_gemm(GemmArgs a) {
       dma16(bsrc[i] + g * 64, base + A_STAGE + (uint32_t)((i * NW + wave) * 1024));
   };
 
-  // ---- prologue: the first STAGES-1 groups in flight; tables to LDS -------
+  // ---- prologue: group 0 in flight; tables to LDS ---------------------------
   issue(0);
-  if (STAGES > 2 && G > 1) issue(1);
   // Tables: every load is issued before the first use (unrolled, clamped
   // indices, no per-lane branches), so the block pays one latency, not one
   // per element.  G <= 32.
@@ -249,32 +248,39 @@ __global__ __launch_bounds__(128 * WN) void k_expert_gemm(GemmArgs a) {
   uint32_t magic;
   asm volatile("v_mov_b32 %0, 0x43004300" : "=v"(magic));
 
+  // One barrier per group.  At the top of iteration g every wave has issued
+  // all its MFMAs of group g-1 (they may still be executing) and has read
+  // its last fragment of stage g-1, so after the barrier the DMA of group g+1
+  // may overwrite that stage.  The scale step of group g-1 runs after the
+  // first LDS reads of group g are issued, so the MFMA drain and the LDS
+  // latency overlap instead of adding up.
+  static_assert(STAGES == 2, "one barrier per group needs a 2-stage ring");
+  f32x4 acc[4][4];
+  float sprev[4] = {0.f, 0.f, 0.f, 0.f};
   for (int g = 0; g < G; ++g) {
-    // keep STAGES-1 groups in flight; wait for group g
-    if (g + STAGES - 1 < G) {
-      issue(g + STAGES - 1);
-      wait_vm<(STAGES - 1) * Gm::DMA>();
-    } else if (STAGES > 2 && g + 1 < G) {
-      wait_vm<Gm::DMA>();
-    } else {
-      wait_vm<0>();
-    }
+    wait_vm<0>();  // this thread's DMA of group g (issued one group ago)
     // stage g complete for every thread (and, at g = 0, the LDS tables)
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     block_barrier();
+    if (g + 1 < G) issue(g + 1);
     const uint8_t *sa = lds + (g % STAGES) * STAGE;
     const uint8_t *sb = sa + A_STAGE;
-    f32x4 acc[4][4];
+    f32x4 c0[4];
 #pragma unroll
-    for (int ms = 0; ms < 4; ++ms) {
-      const f32x4 c0 = *(const f32x4 *)(xs_lds + g * BM + wm * 64 + ms * 16 + 4 * q);
-#pragma unroll
-      for (int ns = 0; ns < 4; ++ns) acc[ms][ns] = c0;
-    }
+    for (int ms = 0; ms < 4; ++ms) c0[ms] = *(const f32x4 *)(xs_lds + g * BM + wm * 64 + ms * 16 + 4 * q);
     u32x4 bx[4];
+    float sg[4];
 #pragma unroll
-    for (int ns = 0; ns < 4; ++ns)
+    for (int ns = 0; ns < 4; ++ns) {
       bx[ns] = *(const u32x4 *)(sb + brow[ns] * 64 + ((q ^ bswz(brow[ns])) << 4)) ^ 0x88888888u;
+      sg[ns] = scale_to_f32<SD>(sc_lds[g * BN + brow[ns]]);
+    }
+    if (g > 0) {
+#pragma unroll
+      for (int ns = 0; ns < 4; ++ns)
+#pragma unroll
+        for (int ms = 0; ms < 4; ++ms) tot[ms][ns] += sprev[ns] * acc[ms][ns];
+    }
     const uint8_t *arow = sa + (wm * 64 + m16) * 256;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -284,25 +290,27 @@ __global__ __launch_bounds__(128 * WN) void k_expert_gemm(GemmArgs a) {
       for (int ms = 0; ms < 4; ++ms) af[ms] = *(const u32x4 *)(arow + ms * 16 * 256 + chunk);
 #pragma unroll
       for (int ns = 0; ns < 4; ++ns) bf[ns] = nib_slice3(bx[ns], j, magic);
+      // the first k-slice accumulates onto c0 directly (no copies of c0)
 #pragma unroll
       for (int ms = 0; ms < 4; ++ms)
 #pragma unroll
-        for (int ns = 0; ns < 4; ++ns) acc[ms][ns] = mfma_bf16_16x16x32(af[ms], bf[ns], acc[ms][ns]);
+        for (int ns = 0; ns < 4; ++ns)
+          acc[ms][ns] = mfma_bf16_16x16x32(af[ms], bf[ns], j == 0 ? c0[ms] : acc[ms][ns]);
     }
 #pragma unroll
-    for (int ns = 0; ns < 4; ++ns) {
-      const float s = scale_to_f32<SD>(sc_lds[g * BN + brow[ns]]);
-#pragma unroll
-      for (int ms = 0; ms < 4; ++ms) tot[ms][ns] += s * acc[ms][ns];
-    }
-    block_barrier();  // stage g may be overwritten by the DMA issued next iteration
+    for (int ns = 0; ns < 4; ++ns) sprev[ns] = sg[ns];
   }
+#pragma unroll
+  for (int ns = 0; ns < 4; ++ns)
+#pragma unroll
+    for (int ms = 0; ms < 4; ++ms) tot[ms][ns] += sprev[ns] * acc[ms][ns];
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  block_barrier();  // every wave's last read of the ring precedes the staging below
 
   // ---- epilogue -------------------------------------------------------
   // lane (q, m16) of tile (ms, ns) holds rows wm*64 + ms*16 + 4q + r, column
   // m16.  Results are staged in the (now idle) LDS ring and leave as 16-byte
-  // row chunks.  The loop's final barrier orders the staging after every
-  // wave's last read of the ring.
+  // row chunks.
   if (MODE == 0) {
     constexpr int OST = COLS * 2 + 16;  // staged row stride, bytes
     static_assert(BM * OST <= STAGES * STAGE, "staging exceeds the ring");
