@@ -17,6 +17,7 @@ MAX_TOKENS = 65536
 # every symbol include/ainfer_moe.h declares
 EXPORTS = (
     "ainfer_moe_strerror", "ainfer_moe_validate", "ainfer_moe_workspace_bytes",
+    "ainfer_moe_workspace_init",
     "ainfer_moe_forward", "ainfer_moe_block_forward", "ainfer_moe_route",
     "ainfer_moe_dispatch", "ainfer_moe_rmsnorm", "ainfer_moe_fill",
     "ainfer_moe_profile_enable", "ainfer_moe_profile_read",
@@ -59,6 +60,7 @@ def lib():
         L.ainfer_moe_validate.argtypes = [sp]
         L.ainfer_moe_workspace_bytes.restype = SZ
         L.ainfer_moe_workspace_bytes.argtypes = [sp, I32]
+        L.ainfer_moe_workspace_init.argtypes = [sp, P, SZ, P]
         L.ainfer_moe_forward.argtypes = [sp, wp, P, P, I32, P, SZ, P]
         L.ainfer_moe_block_forward.argtypes = [sp, wp, P, I32, F, P, P, I32, P, SZ, P]
         L.ainfer_moe_route.argtypes = [sp, wp, P, I32, P, P, P, P, P, SZ, P]

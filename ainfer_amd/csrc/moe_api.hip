@@ -64,15 +64,19 @@ struct ProfCall {
 };
 
 struct Layout {
-  size_t logits, sg_logit, idx, w, sg, xperm, chunk_counts, rank, counts, offsets, perm, inv,
-      ptok, tiles, n_tiles, cnt, ticket, act, act_s, o, h, wnorm, xsum, asum, asum_s, total;
+  size_t sync, sync_words, logits, sg_logit, idx, w, sg, xperm, chunk_counts, rank, counts, offsets, perm, inv,
+      ptok, tiles, n_tiles, ticket, act, act_s, o, h, wnorm, xsum, asum, asum_s, total;
 };
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
+// Tiles of at most mt rows over the experts a step selects: sum_e
+// ceil(c_e / mt) <= (T*k + (mt - 1) * min(T*k, E)) / mt, plus the shared
+// expert's ceil(T / mt).
 int max_tiles_bound(const ainfer_moe_shape &s, int T, int mt) {
   long tk = (long)T * s.top_k;
-  long routed = tk / mt + (tk < s.n_experts ? tk : s.n_experts);
+  long used = tk < s.n_experts ? tk : s.n_experts;
+  long routed = (tk + (mt - 1) * used + mt - 1) / mt;
   long sh = s.shared_inter > 0 ? (T + mt - 1) / mt : 0;
   return (int)(routed + sh);
 }
@@ -87,6 +91,14 @@ Layout layout_of(const ainfer_moe_shape &s, int Tm) {
   };
   const size_t T = (size_t)(Tm > 0 ? Tm : 1), E = s.n_experts, k = s.top_k, H = s.hidden;
   const size_t nchunks = (T + 63) / 64;
+  // decode sync region: the same place and size for every T
+  {
+    DecodeGeom g;
+    const int slabs = decode_geometry(s, &g) ? g.slabs_dn : 0;
+    L.sync_words = SY_TILES + SY_STRIDE * (2 * (size_t)max_tiles_bound(s, DECODE_MAX_T, DEC_MT) +
+                                           (size_t)DECODE_MAX_T * slabs);
+    L.sync = take(L.sync_words * 4);
+  }
   L.logits = take(T * E * 4);
   L.sg_logit = take(T * 4);
   L.idx = take(T * k * 4);
@@ -102,7 +114,6 @@ Layout layout_of(const ainfer_moe_shape &s, int Tm) {
   L.ptok = take(T * k * 4);
   L.tiles = take((size_t)max_tiles_bound(s, (int)T, DEC_MT) * 16);  // >= every other bound
   L.n_tiles = take(4);
-  L.cnt = take(T * (H / 16) * 4);
   L.ticket = take(4);
   L.act = take(T * k * s.inter * 2);
   L.act_s = take(T * (size_t)(s.shared_inter > 0 ? s.shared_inter : 1) * 2);
@@ -159,10 +170,48 @@ DispatchOut dispatch_out(const ainfer_moe_shape *s, const Layout &L, void *ws, i
   d.ptok = at<int32_t>(ws, L.ptok);
   d.tiles = at<int4>(ws, L.tiles);
   d.n_tiles = at<int32_t>(ws, L.n_tiles);
-  d.cnt = at<int32_t>(ws, L.cnt);
-  d.n_cnt = T * (s->hidden / 16);
   d.ticket = at<int32_t>(ws, L.ticket);
   return d;
+}
+
+// Arguments of the small-tile expert kernels: mode 0 = gate/up (+ SiLU), mode
+// 1 = down.
+ExpertArgs expert_args(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const Layout &L,
+                       void *ws, const DispatchOut &d, int T, int mode) {
+  ExpertArgs a;
+  memset(&a, 0, sizeof a);
+  a.ptok = d.ptok;
+  a.tiles = d.tiles;
+  a.n_tiles = d.n_tiles;
+  a.T = T;
+  a.k = s->top_k;
+  a.E = s->n_experts;
+  a.H = s->hidden;
+  a.I = s->inter;
+  a.Is = s->shared_inter;
+  if (mode == 0) {
+    a.w0 = w->w_gate;
+    a.w1 = w->w_up;
+    a.s0 = (const uint16_t *)w->s_gate;
+    a.s1 = (const uint16_t *)w->s_up;
+    a.ws0 = w->ws_gate;
+    a.ws1 = w->ws_up;
+    a.ss0 = (const uint16_t *)w->ss_gate;
+    a.ss1 = (const uint16_t *)w->ss_up;
+    a.a_routed = at<uint16_t>(ws, L.xperm);
+    a.a_shared = at<uint16_t>(ws, L.xperm);
+    a.act = at<uint16_t>(ws, L.act);
+    a.act_s = at<uint16_t>(ws, L.act_s);
+  } else {
+    a.w0 = w->w_down;
+    a.s0 = (const uint16_t *)w->s_down;
+    a.ws0 = w->ws_down;
+    a.ss0 = (const uint16_t *)w->ss_down;
+    a.a_routed = at<uint16_t>(ws, L.act);
+    a.a_shared = at<uint16_t>(ws, L.act_s);
+    a.o = at<uint16_t>(ws, L.o);
+  }
+  return a;
 }
 
 int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const void *x,
@@ -175,6 +224,23 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
   const bool gemm = T >= GEMM_MIN_T;
   const int mt = gemm ? GEMM_MT : SMALL_MT;
   DispatchOut d = dispatch_out(s, L, ws, T);
+  DecodeGeom dg;
+  if (T <= DECODE_MAX_T && decode_geometry(*s, &dg)) {
+    // decode: two launches (moe_decode.hip)
+    int32_t *sync = at<int32_t>(ws, L.sync);
+    HIP_TRY(launch_route_decode(x, w->router_w, w->router_bias, w->shared_gate_w,
+                                at<float>(ws, L.logits), at<float>(ws, L.sg_logit),
+                                at<int32_t>(ws, L.idx), at<float>(ws, L.w), at<float>(ws, L.sg),
+                                at<uint16_t>(ws, L.xperm), T, H, E, k, has_shared, &d, sync, st));
+    pc->end(2);
+    ExpertArgs gu = expert_args(s, w, L, ws, d, T, 0), dn = expert_args(s, w, L, ws, d, T, 1);
+    HIP_TRY(launch_experts_decode(s->scale_dtype, dg, gu, dn, at<float>(ws, L.w),
+                                  at<float>(ws, L.sg), d.inv, resid, y, sync,
+                                  max_tiles_bound(*s, T, DEC_MT),
+                                  max_tiles_bound(*s, DECODE_MAX_T, DEC_MT), st));
+    pc->end(5);
+    return AINFER_OK;
+  }
   if (T <= EXACT_ROUTER_MAX_T)
     HIP_TRY(launch_router_exact(x, w->router_w, w->router_bias, w->shared_gate_w,
                                 at<float>(ws, L.logits), at<float>(ws, L.sg_logit),
@@ -331,6 +397,16 @@ size_t ainfer_moe_workspace_bytes(const ainfer_moe_shape *s, int32_t max_tokens)
   return layout_of(*s, max_tokens).total;
 }
 
+int ainfer_moe_workspace_init(const ainfer_moe_shape *s, void *ws, size_t ws_bytes,
+                              void *stream) {
+  int rc = ainfer_moe_validate(s);
+  if (rc) return rc;
+  if ((rc = check_ws(s, 0, ws, ws_bytes))) return rc;
+  const Layout L = layout_of(*s, 0);
+  HIP_TRY(launch_zero_i32(at<int32_t>(ws, L.sync), (int)L.sync_words, (hipStream_t)stream));
+  return AINFER_OK;
+}
+
 int ainfer_moe_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const void *x,
                        void *y, int32_t T, void *ws, size_t ws_bytes, void *stream) {
   int rc = ainfer_moe_validate(s);
@@ -380,6 +456,16 @@ int ainfer_moe_route(const ainfer_moe_shape *s, const ainfer_moe_weights *w, con
   if ((rc = check_ws(s, T, ws, ws_bytes))) return rc;
   const Layout L = layout_of(*s, T);
   hipStream_t st = (hipStream_t)stream;
+  DecodeGeom dg;
+  if (T <= DECODE_MAX_T && decode_geometry(*s, &dg)) {
+    // the decode routing kernel, without its dispatch
+    HIP_TRY(launch_route_decode(x, w->router_w, w->router_bias, w->shared_gate_w,
+                                logits ? logits : at<float>(ws, L.logits),
+                                at<float>(ws, L.sg_logit), topk_idx, topk_w, shared_gate, nullptr,
+                                T, s->hidden, s->n_experts, s->top_k, s->shared_inter > 0,
+                                nullptr, at<int32_t>(ws, L.sync), st));
+    return AINFER_OK;
+  }
   if (T <= EXACT_ROUTER_MAX_T) {
     HIP_TRY(launch_router_exact(x, w->router_w, w->router_bias, w->shared_gate_w,
                                 logits ? logits : at<float>(ws, L.logits),

@@ -89,6 +89,31 @@ __device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t o
 }
 constexpr uint32_t BUF_OOB = 0x80000000u;
 
+// ---- device-coherent accesses ----------------------------------------------
+// The L2 of each XCD is write-back and not coherent with the other XCDs'.
+// Data one workgroup hands to another inside a kernel is written with sc1
+// stores (written through to the device coherence point) and read with sc1
+// loads, and a wait for the stores' completion precedes the counter atomic
+// that publishes them.  This replaces agent-scope release/acquire fences,
+// which write back or invalidate a whole L2 (about 20 ns each, serialised).
+constexpr int CPOL_SC1 = 16;  // cache-policy operand of the buffer builtins
+__device__ __forceinline__ uint16_t ld_dev_u16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, CPOL_SC1);
+}
+__device__ __forceinline__ void st_dev_u16(__amdgpu_buffer_rsrc_t r, uint32_t off, uint16_t v) {
+  __builtin_amdgcn_raw_buffer_store_b16(v, r, off, 0, CPOL_SC1);
+}
+template <typename V>
+__device__ __forceinline__ V ld_dev(const V *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename V>
+__device__ __forceinline__ void st_dev(V *p, V v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// every store this wave issued has completed
+__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 // ---- XCD-aware block order -------------------------------------------------
 // Workgroups are dispatched round-robin over the 8 XCDs (block b -> XCD b%8),
 // each with its own L2.  This bijection hands each XCD a contiguous range of
@@ -99,4 +124,46 @@ __device__ __forceinline__ int xcd_remap(int b, int G) {
   const int q = G / N_XCD, r = G % N_XCD;
   const int xcd = b % N_XCD, idx = b / N_XCD;
   return xcd < r ? xcd * (q + 1) + idx : r * (q + 1) + (xcd - r) * q + idx;
+}
+
+// MFMA-order copy of one token row (position 8*j+e <- k = 4*e+j inside every
+// 32-element block) and, when xsum is non-null, its 128-wide group sums.
+__device__ __forceinline__ void write_xperm(const uint16_t *__restrict__ xrow,
+                                            uint16_t *__restrict__ xperm,
+                                            float *__restrict__ xsum, int t, int H, int lane) {
+  {
+    uint16_t *xo = xperm + (size_t)t * H;
+    for (int b = lane; b < (H >> 5); b += 64) {
+      const u32x4 *src = (const u32x4 *)(xrow + b * 32);
+      const u32x4 s0 = src[0], s1 = src[1], s2 = src[2], s3 = src[3];
+      const uint32_t in[16] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3],
+                               s2[0], s2[1], s2[2], s2[3], s3[0], s3[1], s3[2], s3[3]};
+      uint32_t out[16];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) {
+          const int ka = 8 * e2 + j, kb = ka + 4;
+          const uint32_t lo = (in[ka >> 1] >> (16 * (ka & 1))) & 0xFFFFu;
+          const uint32_t hi = (in[kb >> 1] >> (16 * (kb & 1))) & 0xFFFFu;
+          out[4 * j + e2] = lo | (hi << 16);
+        }
+      u32x4 *dst = (u32x4 *)(xo + b * 32);
+      dst[0] = u32x4{out[0], out[1], out[2], out[3]};
+      dst[1] = u32x4{out[4], out[5], out[6], out[7]};
+      dst[2] = u32x4{out[8], out[9], out[10], out[11]};
+      dst[3] = u32x4{out[12], out[13], out[14], out[15]};
+      if (xsum) {
+        // sum of the 128-wide group: this block's 32 values, then the 4
+        // consecutive lanes holding the group's blocks (fixed order)
+        float bs = 0.0f;
+#pragma unroll
+        for (int i2 = 0; i2 < 16; ++i2)
+          bs += __uint_as_float(in[i2] << 16) + __uint_as_float(in[i2] & 0xFFFF0000u);
+        bs += __shfl_xor(bs, 1, 64);
+        bs += __shfl_xor(bs, 2, 64);
+        if ((b & 3) == 0) xsum[(size_t)t * (H >> 7) + (b >> 2)] = bs;
+      }
+    }
+  }
 }

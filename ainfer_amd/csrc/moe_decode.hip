@@ -1,0 +1,572 @@
+// moe_decode.hip - the decode layer (T <= 16 tokens) in two launches.
+//
+// Measured on MI355X: a dependent kernel launch costs about 2.5 us, a flag
+// handed from one workgroup to another through device memory about 0.8 us,
+// same-address device atomics serialise at about 11 ns each, and an
+// agent-scope release or acquire fence (a whole-L2 write-back or
+// invalidate) about 20 ns, serialised.  So the decode layer is two kernels
+// whose stages meet through counters that few workgroups touch, with data
+// handed over by sc1 stores and loads instead of fences (moe_common.h):
+//
+//  k_route_decode   workgroups [0, NR): canonical router logits, one
+//                   (RD_R rows x RD_TT tokens) unit per wave, one arrival per
+//                   workgroup on router_done; the last workgroup (one wave
+//                   per token) writes x in MFMA order, waits for
+//                   router_done == NR, takes the exact top-k, the weights and
+//                   the shared gate, and builds the dispatch (tiles of at
+//                   most DEC_MT tokens) from LDS.
+//  k_experts_decode one workgroup per item: first every gate/up + SiLU item
+//                   (tile-major, slab-minor), one arrival each on
+//                   gu_done[tile]; then every down item, which requests its
+//                   weights, waits for gu_done[tile] == gate/up slabs, reads
+//                   the tile's act rows, writes its o rows, and counts one
+//                   arrival per (token, row slab).  The (k+1)-th arrival of a
+//                   (token, slab) sums the token's k + 1 rows of that slab in
+//                   slot order (the combine).
+//
+// A wait only ever names work of lower workgroup index, and workgroups are
+// dispatched in index order, so every awaited workgroup is already running.
+// Waits are bounded (SPIN_MAX polls); one that runs out sets the error word
+// of the sync region and carries on.
+//
+// Every counter is reset by its last user (router_done by the selection
+// workgroup, gu_done/dn_done by a tile's last down item, a (token, slab)
+// counter by its last arrival), so the sync region is zero again when a call
+// ends.  It must be zero before the first call (ainfer_moe_workspace_init).
+//
+// Debug builds with -DAINFER_DECODE_TRACE record per-workgroup timestamps.
+#include <string.h>
+
+#include "moe_common.h"
+#include "moe_expert_item.h"
+#include "moe_internal.h"
+#include "moe_topk.h"
+
+#ifdef AINFER_DECODE_TRACE
+// debug builds only: per-workgroup timestamps (s_memrealtime, 100 MHz)
+__device__ unsigned long long g_dtrace[2][1 << 15][5];
+#define DTRACE_AT(K, X, I) \
+  if (threadIdx.x == 0 && (X) < (1 << 15)) g_dtrace[K][X][I] = __builtin_amdgcn_s_memrealtime()
+#define DTRACE(K, I) DTRACE_AT(K, blockIdx.x, I)
+extern "C" int ainfer_debug_trace(void *host) {
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_dtrace), sizeof(g_dtrace)) == hipSuccess ? 0 : -1;
+}
+#else
+#define DTRACE(K, I)
+#define DTRACE_AT(K, X, I)
+#endif
+
+namespace {
+
+constexpr int RD_WAVES = 16;  // waves per k_route_decode workgroup
+constexpr int RD_R = 2;      // router rows per wave
+constexpr int RD_TT = 4;     // tokens per router pass
+constexpr int SPIN_MAX = 1 << 20;
+#ifndef DEC_WAVES_PER_SIMD
+#define DEC_WAVES_PER_SIMD 6  // register budget of the expert kernel (<= 80 VGPRs)
+#endif
+#ifndef DEC_COH
+#define DEC_COH true
+#endif
+#ifndef DEC_PERSIST
+#define DEC_PERSIST 0     // 1: at most the resident workgroups, looping over items
+#endif
+#if DEC_PERSIST
+#define DEC_NEXT continue
+#else
+#define DEC_NEXT return
+#endif
+
+__device__ __forceinline__ bool spin_until_geq(const int32_t *p, int target) {
+  for (int it = 0; it < SPIN_MAX; ++it) {
+    if (__hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= target) return true;
+    __builtin_amdgcn_s_sleep(8);
+  }
+  return false;
+}
+
+// Workgroup-wide: thread 0 polls.  What the awaited workgroups published is
+// then read with sc1 loads (moe_common.h).
+__device__ __forceinline__ void block_wait_geq(const int32_t *p, int target, int32_t *err) {
+  if (threadIdx.x == 0 && !spin_until_geq(p, target)) atomicOr(err, 1);
+  __syncthreads();
+}
+
+// Workgroup-wide: every wave waits for its sc1 stores, then one arrival.
+// Returns the counter's previous value in every thread.
+__device__ __forceinline__ int block_arrive(int32_t *p) {
+  __shared__ int old;
+  wait_stores();
+  __syncthreads();
+  if (threadIdx.x == 0) old = atomicAdd(p, 1);
+  __syncthreads();
+  return old;
+}
+
+// A uniform 16-byte load through the scalar cache (the compiler cannot
+// prove the tile list read-only inside this kernel and would use a vector
+// load, whose wait also waits for every weight load in flight).
+__device__ __forceinline__ int4 sload_int4(const int4 *p) {
+  typedef int i32x4 __attribute__((ext_vector_type(4)));
+  i32x4 v;
+  asm volatile("s_load_dwordx4 %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p) : "memory");
+  return make_int4(v[0], v[1], v[2], v[3]);
+}
+
+struct RouteDecodeArgs {
+  const uint16_t *x, *rw, *gw;
+  const float *bias;
+  float *logits, *sgl;  // [T][E], [T]
+  int32_t *idx;
+  float *w, *sg;
+  uint16_t *xperm;
+  DispatchOut ds;
+  int32_t *sync;
+  int T, H, E, k, has_shared, NR;
+};
+
+// Dispatch of T <= 32 tokens by one workgroup (idx in LDS): 32-bit token masks
+// per expert (order-free atomic OR), counts, a workgroup exclusive scan over
+// experts, tiles of at most DEC_MT tokens, perm / inv / ptok.
+__device__ __forceinline__ void dispatch_decode(const int32_t *__restrict__ idx, int T, int k,
+                                                int E, int has_shared, const DispatchOut &ds) {
+  __shared__ uint32_t msk[1024];
+  __shared__ int offl[1024];
+  __shared__ int wsum_c[RD_WAVES], wsum_t[RD_WAVES];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  constexpr int NT = RD_WAVES * 64;
+  for (int e = tid; e < E; e += NT) msk[e] = 0u;
+  __syncthreads();
+  for (int i = tid; i < T * k; i += NT) atomicOr(&msk[idx[i]], 1u << (i / k));
+  __syncthreads();
+  const int per = (E + NT - 1) / NT;
+  const int e0 = tid * per, e1 = min(e0 + per, E);
+  int c_loc = 0, t_loc = 0;
+  for (int e = e0; e < e1; ++e) {
+    const int c = __popc(msk[e]);
+    c_loc += c;
+    t_loc += (c + DEC_MT - 1) / DEC_MT;
+  }
+  int ci = c_loc, ti = t_loc;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int a = __shfl_up(ci, d, 64), b = __shfl_up(ti, d, 64);
+    if (lane >= d) {
+      ci += a;
+      ti += b;
+    }
+  }
+  if (lane == 63) {
+    wsum_c[wv] = ci;
+    wsum_t[wv] = ti;
+  }
+  __syncthreads();
+  int cb = 0, tb0 = 0, ctot = 0, ttot = 0;
+#pragma unroll
+  for (int w = 0; w < RD_WAVES; ++w) {
+    if (w < wv) {
+      cb += wsum_c[w];
+      tb0 += wsum_t[w];
+    }
+    ctot += wsum_c[w];
+    ttot += wsum_t[w];
+  }
+  int o = cb + ci - c_loc, tb = tb0 + ti - t_loc;
+  for (int e = e0; e < e1; ++e) {
+    const int c = __popc(msk[e]);
+    ds.counts[e] = c;
+    ds.offsets[e] = o;
+    offl[e] = o;
+    for (int m0 = 0; m0 < c; m0 += DEC_MT) ds.tiles[tb++] = make_int4(e, o + m0, min(DEC_MT, c - m0), 0);
+    o += c;
+  }
+  const int nsh = has_shared ? (T + DEC_MT - 1) / DEC_MT : 0;
+  if (tid < nsh) ds.tiles[ttot + tid] = make_int4(E, tid * DEC_MT, min(DEC_MT, T - tid * DEC_MT), 0);
+  if (tid == 0) {
+    ds.offsets[E] = ctot;
+    *ds.n_tiles = ttot + nsh;
+  }
+  __syncthreads();
+  for (int i = tid; i < T * k; i += NT) {
+    const int t = i / k, e = idx[i];
+    const int pos = offl[e] + __popc(msk[e] & ((1u << t) - 1u));
+    ds.perm[pos] = i;
+    ds.inv[i] = pos;
+    ds.ptok[pos] = t;
+  }
+}
+
+template <int NV>
+__global__ __launch_bounds__(RD_WAVES * 64) void k_route_decode(RouteDecodeArgs a) {
+  __shared__ uint64_t s_cand[RD_WAVES][64];
+  __shared__ uint64_t s_sel[RD_WAVES][16];
+  __shared__ int s_idx[RD_WAVES * 32];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int T = a.T, H = a.H, E = a.E, k = a.k;
+  int32_t *router_done = a.sync + SY_ROUTER_DONE;
+  DTRACE(0, 0);
+  if ((int)blockIdx.x < a.NR) {
+    // ---- canonical logits of RD_R rows x RD_TT tokens per wave: lane l
+    // sums 8-element chunks l, l+64, ... with fma in order, then the xor
+    // butterfly (the oracle's mo_router_dot) ---------------------------------
+    const int nrows = E + (a.gw ? 1 : 0);
+    const int ngroups = (nrows + RD_R - 1) / RD_R;
+    const int u = blockIdx.x * RD_WAVES + wave;
+    const int rbase = (u % ngroups) * RD_R, t0 = (u / ngroups) * RD_TT;
+    if (t0 < T) {
+      const uint16_t *wr[RD_R];
+#pragma unroll
+      for (int i = 0; i < RD_R; ++i) {
+        const int r = min(rbase + i, nrows - 1);
+        wr[i] = r < E ? a.rw + (size_t)r * H : a.gw;
+      }
+      const int nch = H >> 3;
+      float acc[RD_R][RD_TT];
+#pragma unroll
+      for (int i = 0; i < RD_R; ++i)
+#pragma unroll
+        for (int j = 0; j < RD_TT; ++j) acc[i][j] = 0.0f;
+      for (int c = lane; c < nch; c += 64) {
+        u32x4 wv[RD_R], xv[RD_TT];
+#pragma unroll
+        for (int i = 0; i < RD_R; ++i) wv[i] = *(const u32x4 *)(wr[i] + (size_t)c * 8);
+#pragma unroll
+        for (int j = 0; j < RD_TT; ++j)
+          xv[j] = *(const u32x4 *)(a.x + (size_t)min(t0 + j, T - 1) * H + (size_t)c * 8);
+#pragma unroll
+        for (int i = 0; i < RD_R; ++i)
+#pragma unroll
+          for (int j = 0; j < RD_TT; ++j) {
+            float s = acc[i][j];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              s = __builtin_fmaf(__uint_as_float(xv[j][q] << 16), __uint_as_float(wv[i][q] << 16), s);
+              s = __builtin_fmaf(__uint_as_float(xv[j][q] & 0xFFFF0000u),
+                                 __uint_as_float(wv[i][q] & 0xFFFF0000u), s);
+            }
+            acc[i][j] = s;
+          }
+      }
+#pragma unroll
+      for (int m = 32; m >= 1; m >>= 1)
+#pragma unroll
+        for (int i = 0; i < RD_R; ++i)
+#pragma unroll
+          for (int j = 0; j < RD_TT; ++j) acc[i][j] = acc[i][j] + __shfl_xor(acc[i][j], m, 64);
+      if (lane == 0) {
+#pragma unroll
+        for (int i = 0; i < RD_R; ++i)
+#pragma unroll
+          for (int j = 0; j < RD_TT; ++j) {
+            const int r = rbase + i, t = t0 + j;
+            if (r >= nrows || t >= T) continue;
+            if (r < E)
+              st_dev(a.logits + (size_t)t * E + r, a.bias ? acc[i][j] + a.bias[r] : acc[i][j]);
+            else
+              st_dev(a.sgl + t, acc[i][j]);
+          }
+      }
+    }
+    DTRACE(0, 1);
+    block_arrive(router_done);
+    DTRACE(0, 3);
+    return;
+  }
+  // ---- the selection workgroup: one wave per token (T <= RD_WAVES) --------
+  const int t = wave;
+  // the MFMA-order copy of x does not depend on the routing
+  if (t < T && a.xperm) write_xperm(a.x + (size_t)t * H, a.xperm, nullptr, t, H, lane);
+  block_wait_geq(router_done, a.NR, a.sync + SY_ERR);
+  DTRACE(0, 1);
+  if (t < T) {
+    const float *ar = a.logits + (size_t)t * E;
+    uint32_t key[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int e = lane + 64 * i;
+      const float v = ld_dev(ar + min(e, E - 1));
+      key[i] = e < E ? ordered_key(v) : 0u;
+    }
+    const float sgl = a.gw ? ld_dev(a.sgl + t) : 0.0f;
+    int seli;
+    uint32_t selk;
+    wave_topk_fast<NV>(key, E, k, lane, seli, selk, s_cand[wave], s_sel[wave]);
+    const float selv = lane < k ? key_to_float(selk) : 0.0f;
+    const float vmax = __shfl(selv, 0, 64);
+    const float p = lane < k ? expf(selv - vmax) : 0.0f;
+    float sum = 0.0f;
+    for (int j = 0; j < k; ++j) sum += __shfl(p, j, 64);
+    if (lane < k) {
+      a.idx[(size_t)t * k + lane] = seli;
+      a.w[(size_t)t * k + lane] = p / sum;
+      s_idx[t * k + lane] = seli;
+    }
+    if (lane == 0) a.sg[t] = a.gw ? 1.0f / (1.0f + expf(-sgl)) : 1.0f;
+  }
+  DTRACE(0, 2);
+  __syncthreads();
+  if (threadIdx.x == 0) *router_done = 0;  // this workgroup was its only waiter
+  if (a.ds.tiles) dispatch_decode(s_idx, T, k, E, a.has_shared, a.ds);
+  DTRACE(0, 3);
+}
+
+struct ExpertsDecodeArgs {
+  ExpertArgs gu, dn;  // WK, WR, n_slabs set (WK * WR waves in both)
+  const float *w, *sg;
+  const int32_t *inv;
+  const uint16_t *resid;
+  uint16_t *y;
+  int32_t *sync;
+  int max_tiles, cap;  // grid tiles; capacity of the per-tile counter arrays
+};
+
+// Persistent: gridDim.x workgroups (all resident: the launcher sizes the
+// grid by the occupancy) take items it, it + gridDim.x, ...  A workgroup
+// only ever waits for gate/up items of lower index, which are held by
+// resident workgroups, so the waits end.  (One item per workgroup instead
+// would be bound by the workgroup dispatch rate, about 150 per us.)
+template <int SD, int KBW_GU, int RG_GU, int KBW_DN, int RG_DN>
+__global__ __launch_bounds__(1024, DEC_WAVES_PER_SIMD) void k_experts_decode(ExpertsDecodeArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  // one counter per 256-byte line: same-line atomics and polls serialise
+  int32_t *gu_done = a.sync + SY_TILES, *dn_done = gu_done + a.cap * SY_STRIDE,
+          *cnt = dn_done + a.cap * SY_STRIDE;
+  const int lane = threadIdx.x & 63;
+  const int sg = a.gu.n_slabs, sd = a.dn.n_slabs;
+  const int n_gu = a.max_tiles * sg, n_items = n_gu + a.max_tiles * sd;
+  const int n_tiles = *a.gu.n_tiles;
+#if DEC_PERSIST
+  for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
+#else
+  {
+    const int item = blockIdx.x;
+#endif
+    // ---- item -> (kind, tile, slab): all gate/up items (tile-major,
+    // slab-minor), then all down items ---------------------------------------
+    const int is_gu = item < n_gu;
+    const int r = is_gu ? item : item - n_gu, ns = is_gu ? sg : sd;
+    const int tile = r / ns, slab = r % ns;
+    if (tile >= n_tiles) DEC_NEXT;
+    DTRACE_AT(1, item, 0);
+#ifdef AINFER_DECODE_TRACE
+    if (threadIdx.x == 0) g_dtrace[1][item][4] = is_gu;
+#endif
+    // the previous item's partials (read by wave 0) are no longer needed
+    __syncthreads();
+    if (is_gu) {
+      // x (MFMA order) comes from the routing kernel: plain, cacheable loads
+      expert_lds_item<SD, KBW_GU, RG_GU, DEC_MT, 0, DEC_COH, NoWait, false>(a.gu, a.gu.tiles[tile],
+                                                                          slab, lds);
+      if (threadIdx.x >= 64) DEC_NEXT;
+      // wave 0: its act stores, then the arrival
+      DTRACE_AT(1, item, 2);
+      wait_stores();
+      if (lane == 0) atomicAdd(&gu_done[tile * SY_STRIDE], 1);
+      DTRACE_AT(1, item, 3);
+      DEC_NEXT;
+    }
+    const int4 td = sload_int4(a.dn.tiles + tile);
+    // the down weights are requested before the wait for the tile's act rows
+    const int32_t *gdone = &gu_done[tile * SY_STRIDE];
+    int32_t *err = a.sync + SY_ERR;
+    expert_lds_item<SD, KBW_DN, RG_DN, DEC_MT, 1, DEC_COH>(a.dn, td, slab, lds, [=]() {
+      block_wait_geq(gdone, sg, err);
+      DTRACE_AT(1, item, 1);
+    });
+    if (threadIdx.x >= 64) DEC_NEXT;
+    DTRACE_AT(1, item, 2);
+    // ---- wave 0: publish o; count this tile's down items and each token's
+    // arrivals on this row slab --------------------------------------------
+    wait_stores();
+    if (lane == 0 && atomicAdd(&dn_done[tile * SY_STRIDE], 1) == sd - 1) {
+      gu_done[tile * SY_STRIDE] = 0;  // all of the tile's down items have passed their wait
+      dn_done[tile * SY_STRIDE] = 0;
+    }
+    const bool shared = td.x == a.dn.E;
+    const int mcnt = td.z;
+    const int has_shared = a.dn.Is > 0;
+    const int k = a.dn.k, H = a.dn.H;
+    int tok = -1;
+    if (lane < mcnt) {
+      const int pos = td.y + lane;
+      const int tt = shared ? pos : a.dn.ptok[pos];
+      int32_t *c = &cnt[(tt * sd + slab) * SY_STRIDE];
+      if (atomicAdd(c, 1) == k + has_shared - 1) {
+        *c = 0;
+        tok = tt;
+      }
+    }
+    DTRACE_AT(1, item, 3);
+    if (__ballot(tok >= 0) == 0ull) DEC_NEXT;
+    // ---- combine of the completed (token, slab) pairs: slot order, as
+    // k_combine -------------------------------------------------------------
+    const __amdgpu_buffer_rsrc_t orr = make_rsrc(a.dn.o, 0x7FFFFFFFu);
+    const int rows = 16 * RG_DN * a.dn.WR, r0 = slab * rows;
+    const size_t Tk = (size_t)a.dn.T * k;
+    constexpr int CB = 4;  // slots whose loads are issued together
+    for (int i = 0; i < mcnt; ++i) {
+      const int t = __builtin_amdgcn_readfirstlane(__shfl(tok, i, 64));
+      if (t < 0) continue;
+      for (int hr = lane; hr < rows; hr += 64) {
+        const int h = min(r0 + hr, H - 1);
+        float acc = 0.0f;
+        for (int j0 = 0; j0 < k; j0 += CB) {
+          uint16_t ov[CB];
+          float wj[CB];
+#pragma unroll
+          for (int j = 0; j < CB; ++j) {
+            const int jj = min(j0 + j, k - 1);
+            const int pos = a.inv[(size_t)t * k + jj];
+            wj[j] = a.w[(size_t)t * k + jj];
+            ov[j] = ld_dev_u16(orr, (uint32_t)(((size_t)pos * H + h) * 2));
+          }
+#pragma unroll
+          for (int j = 0; j < CB; ++j)
+            if (j0 + j < k) acc = __builtin_fmaf(wj[j], bf16_to_f32(ov[j]), acc);
+        }
+        if (has_shared)
+          acc = __builtin_fmaf(a.sg[t],
+                               bf16_to_f32(ld_dev_u16(orr, (uint32_t)(((Tk + t) * H + h) * 2))), acc);
+        if (a.resid) acc += bf16_to_f32(a.resid[(size_t)t * H + h]);
+        if (r0 + hr < H) a.y[(size_t)t * H + h] = f32_to_bf16(acc);
+      }
+    }
+  }
+}
+
+}  // namespace
+
+int decode_geometry(const ainfer_moe_shape &s, DecodeGeom *g) {
+  int kbw, wk, wr;
+  if (!expert_geometry(0, s.hidden, s.inter, s.shared_inter, 4, &kbw, &wk, &wr) || kbw != 4)
+    return 0;
+  g->wk_gu = wk;
+  if (!expert_geometry(1, s.hidden, s.inter, s.shared_inter, 2, &kbw, &wk, &wr) || kbw != 2)
+    return 0;
+  g->wk_dn = wk;
+  g->nw = g->wk_gu > g->wk_dn ? g->wk_gu : g->wk_dn;
+  if (g->nw < 4) g->nw = 4;
+  if (g->nw % g->wk_gu || g->nw % g->wk_dn || g->nw > 16) return 0;
+  g->wr_gu = g->nw / g->wk_gu;
+  g->wr_dn = g->nw / g->wk_dn;
+  const int Ngu = s.inter > s.shared_inter ? s.inter : s.shared_inter;
+  g->slabs_gu = (Ngu + 16 * RG_GATE_UP * g->wr_gu - 1) / (16 * RG_GATE_UP * g->wr_gu);
+  g->slabs_dn = (s.hidden + 16 * RG_DOWN * g->wr_dn - 1) / (16 * RG_DOWN * g->wr_dn);
+  // A staging only: the K-split partials reuse it (expert_lds_item, COH)
+  const size_t lds_gu = (size_t)g->nw * DEC_MT * 4 * 256 + (DEC_COH ? 0 : 2ull * g->nw * RG_GATE_UP * 1024);
+  const size_t lds_dn = (size_t)g->nw * DEC_MT * 2 * 256 + (DEC_COH ? 0 : 2ull * g->nw * RG_DOWN * 1024);
+  g->lds = lds_gu > lds_dn ? lds_gu : lds_dn;
+  if (g->lds > 64 * 1024) return 0;
+  return 1;
+}
+
+hipError_t launch_route_decode(const void *x, const void *rw, const float *bias, const void *gw,
+                               float *logits, float *sgl, int32_t *idx, float *w, float *sg,
+                               void *xperm, int T, int H, int E, int k, int has_shared,
+                               const DispatchOut *ds, int32_t *sync, hipStream_t s) {
+  if (T <= 0) return hipSuccess;
+  if (T > DECODE_MAX_T || T > RD_WAVES || E > 1024) return hipErrorInvalidValue;
+  RouteDecodeArgs a;
+  memset(&a, 0, sizeof a);
+  a.x = (const uint16_t *)x;
+  a.rw = (const uint16_t *)rw;
+  a.gw = (const uint16_t *)gw;
+  a.bias = bias;
+  a.logits = logits;
+  a.sgl = sgl;
+  a.idx = idx;
+  a.w = w;
+  a.sg = sg;
+  a.xperm = (uint16_t *)xperm;
+  if (ds) a.ds = *ds;
+  a.sync = sync;
+  a.T = T;
+  a.H = H;
+  a.E = E;
+  a.k = k;
+  a.has_shared = has_shared;
+  const int nrows = E + (gw ? 1 : 0);
+  const int units = (nrows + RD_R - 1) / RD_R * ((T + RD_TT - 1) / RD_TT);
+  a.NR = (units + RD_WAVES - 1) / RD_WAVES;
+  const unsigned grid = a.NR + 1;
+  const int nv = (E + 63) / 64;
+  if (nv <= 1) k_route_decode<1><<<grid, RD_WAVES * 64, 0, s>>>(a);
+  else if (nv <= 2) k_route_decode<2><<<grid, RD_WAVES * 64, 0, s>>>(a);
+  else if (nv <= 4) k_route_decode<4><<<grid, RD_WAVES * 64, 0, s>>>(a);
+  else if (nv <= 8) k_route_decode<8><<<grid, RD_WAVES * 64, 0, s>>>(a);
+  else k_route_decode<16><<<grid, RD_WAVES * 64, 0, s>>>(a);
+  return hipGetLastError();
+}
+
+hipError_t launch_experts_decode(int scale_dtype, const DecodeGeom &g, ExpertArgs gu,
+                                 ExpertArgs dn, const float *w, const float *sg,
+                                 const int32_t *inv, const void *resid, void *y,
+                                 int32_t *sync, int max_tiles, int cap, hipStream_t s) {
+  if (max_tiles <= 0) return hipSuccess;
+  if (max_tiles > cap) return hipErrorInvalidValue;
+  ExpertsDecodeArgs a;
+  memset(&a, 0, sizeof a);
+  gu.WK = g.wk_gu;
+  gu.WR = g.wr_gu;
+  gu.n_slabs = g.slabs_gu;
+  dn.WK = g.wk_dn;
+  dn.WR = g.wr_dn;
+  dn.n_slabs = g.slabs_dn;
+  a.gu = gu;
+  a.dn = dn;
+  a.w = w;
+  a.sg = sg;
+  a.inv = inv;
+  a.resid = (const uint16_t *)resid;
+  a.y = (uint16_t *)y;
+  a.sync = sync;
+  a.max_tiles = max_tiles;
+  a.cap = cap;
+  const long grid = (long)max_tiles * (g.slabs_gu + g.slabs_dn);
+  if (grid > 0x7FFFFFFF) return hipErrorInvalidValue;
+  const int threads = g.nw * 64;
+  // resident workgroups = occupancy per CU x CUs, for this device, kernel,
+  // workgroup size and LDS size (a few configurations are cached)
+  struct Res {
+    int dev, sd, threads;
+    size_t lds;
+    int n;
+  };
+  static Res cache[16];
+  static int n_cache = 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return hipErrorInvalidDevice;
+  auto kern = scale_dtype == AINFER_SCALE_FP16
+                  ? k_experts_decode<AINFER_SCALE_FP16, 4, RG_GATE_UP, 2, RG_DOWN>
+                  : k_experts_decode<AINFER_SCALE_BF16, 4, RG_GATE_UP, 2, RG_DOWN>;
+  int resident = 0;
+  for (int i = 0; i < n_cache; ++i)
+    if (cache[i].dev == dev && cache[i].sd == scale_dtype && cache[i].threads == threads &&
+        cache[i].lds == g.lds)
+      resident = cache[i].n;
+  if (resident == 0) {
+    int per_cu = 0, cus = 0;
+    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, threads, g.lds);
+    if (e != hipSuccess) return e;
+    e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return e;
+    if (per_cu < 1 || cus < 1) return hipErrorInvalidConfiguration;
+    resident = per_cu * cus;
+    cache[n_cache % 16] = Res{dev, scale_dtype, threads, g.lds, resident};
+    ++n_cache;
+  }
+  const long wgs = (DEC_PERSIST && grid > resident) ? resident : grid;
+  kern<<<(unsigned)wgs, threads, g.lds, s>>>(a);
+  return hipGetLastError();
+}
+
+__global__ void k_zero_i32(int32_t *p, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0;
+}
+
+
+hipError_t launch_zero_i32(int32_t *p, int n, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  k_zero_i32<<<(n + 255) / 256 < 1024 ? (n + 255) / 256 : 1024, 256, 0, s>>>(p, n);
+  return hipGetLastError();
+}

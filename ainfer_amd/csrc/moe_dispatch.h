@@ -67,5 +67,4 @@ __device__ __forceinline__ void dispatch_small_block(const int32_t *__restrict__
     ds.inv[i] = pos;
     ds.ptok[pos] = t;
   }
-  for (int i = tid; i < ds.n_cnt; i += 256) ds.cnt[i] = 0;
 }

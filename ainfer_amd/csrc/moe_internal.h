@@ -5,6 +5,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "../../include/ainfer_moe.h"
+
 // Arguments of the grouped expert kernels (one launch covers the routed
 // experts and the shared expert, whose tiles carry expert id E).
 struct ExpertArgs {
@@ -59,15 +61,13 @@ constexpr int GEMM_MIN_T = 256;
 
 // Outputs of the dispatch stage.  tiles: (expert, first position, rows,
 // first row within the expert); shared-expert tiles carry expert id E and a
-// token base.  ptok[pos] = token of dispatch position pos.  cnt[n_cnt] are
+// token base.  ptok[pos] = token of dispatch position pos.
 // the combine arrival counters, zeroed by the dispatch.  ticket is the
 // last-block counter of the fused top-k + dispatch launch.
 struct DispatchOut {
   int32_t *counts, *offsets, *perm, *inv, *ptok;
   int4 *tiles;
   int32_t *n_tiles;
-  int32_t *cnt;
-  int n_cnt;
   int32_t *ticket;
 };
 
@@ -125,3 +125,30 @@ constexpr int SMALL_MT = 16;
 constexpr int DEC_MT = 4;  // tile rows of the decode dispatch (T <= EXACT_ROUTER_MAX_T)
 // largest T routed by the fused top-k + dispatch launch
 constexpr int FUSED_DISPATCH_MAX_T = 64;
+
+// ---- decode layer in two launches (moe_decode.hip), T <= DECODE_MAX_T ----
+constexpr int DECODE_MAX_T = EXACT_ROUTER_MAX_T;
+// sync region (int32 words at the start of the workspace, zero between calls)
+// Counters sit SY_STRIDE words (256 bytes) apart.
+enum { SY_STRIDE = 64, SY_ROUTER_DONE = 0, SY_SELECT = SY_STRIDE, SY_ERR = 2 * SY_STRIDE,
+       SY_TILES = 3 * SY_STRIDE };
+struct DecodeGeom {
+  int nw;                  // waves per expert workgroup
+  int wk_gu, wr_gu, wk_dn, wr_dn;
+  int slabs_gu, slabs_dn;  // row slabs per tile
+  size_t lds;              // dynamic LDS bytes
+};
+// 0 when the shape has no decode geometry (the staged path is used then)
+int decode_geometry(const ainfer_moe_shape &s, DecodeGeom *g);
+// router logits + top-k + weights + shared gate + x in MFMA order, and the
+// dispatch (tiles of DEC_MT tokens) when ds != NULL
+hipError_t launch_route_decode(const void *x, const void *rw, const float *bias, const void *gw,
+                               float *logits, float *sgl, int32_t *idx, float *w, float *sg,
+                               void *xperm, int T, int H, int E, int k, int has_shared,
+                               const DispatchOut *ds, int32_t *sync, hipStream_t s);
+// gate/up + SiLU, down and the combine (y = sum_j w_j o_j + g_s o_s (+ resid))
+hipError_t launch_experts_decode(int scale_dtype, const DecodeGeom &g, ExpertArgs gu,
+                                 ExpertArgs dn, const float *w, const float *sg,
+                                 const int32_t *inv, const void *resid, void *y,
+                                 int32_t *sync, int max_tiles, int cap, hipStream_t s);
+hipError_t launch_zero_i32(int32_t *p, int n, hipStream_t s);

@@ -319,7 +319,6 @@ __global__ void k_dispatch_place(const int32_t *__restrict__ idx,
                                  const int32_t *__restrict__ chunk_base, int T, int k, int E,
                                  DispatchOut ds) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  for (int c = i; c < ds.n_cnt; c += gridDim.x * blockDim.x) ds.cnt[c] = 0;
   if (i >= T * k) return;
   const int t = i / k, c = t >> 6;
   const int e = idx[i];

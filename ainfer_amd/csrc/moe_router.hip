@@ -28,6 +28,7 @@
 
 #include "moe_common.h"
 #include "moe_dispatch.h"
+#include "moe_topk.h"
 #include "moe_internal.h"
 
 namespace {
@@ -182,106 +183,11 @@ __device__ __forceinline__ void canon_dot_batch(const u32x4 (&xc)[CH], const uin
     for (int b = 0; b < NB; ++b) out[b] = out[b] + __shfl_xor(out[b], m, 64);
 }
 
-__device__ __forceinline__ float key_to_float(uint32_t k) {
-  return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
-}
 
 constexpr int SEL_WAVES = 4;
 
 // EXACT: `approx` already holds the canonical logits (k_router_logits) and
 // `sgl` the canonical shared-gate logits; the refine is skipped.
-// k rounds of (largest key, then lowest expert among equal keys): the exact
-// top-k of key[] (lane l, slot i = expert l + 64 i) in value-descending,
-// expert-ascending order.  Lane j < k returns the j-th pick; the return value
-// is the k-th largest key.  Every lane keeps its best untaken slot; a round
-// is one wave max, then the winner from a ballot (a second reduction over
-// expert ids only when several lanes hold the maximum), and only the winning
-// lane rescans its slots.
-template <int NV>
-__device__ __forceinline__ uint32_t wave_topk(const uint32_t (&key)[NV], int E, int k, int lane,
-                                              int &seli) {
-  uint32_t taken = 0;
-#pragma unroll
-  for (int i = 0; i < NV; ++i)
-    if (lane + 64 * i >= E) taken |= 1u << i;
-  uint32_t bk = 0;
-  int bs = -1;
-  auto rescan = [&]() {
-    bk = 0;
-    bs = -1;
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const bool better = !((taken >> i) & 1u) && (bs < 0 || key[i] > bk);
-      bk = better ? key[i] : bk;
-      bs = better ? i : bs;
-    }
-  };
-  rescan();
-  uint32_t kth = 0;
-  seli = 0;
-  for (int j = 0; j < k; ++j) {
-    const uint32_t wk = wave_max_u32(bs >= 0 ? bk : 0u);
-    const bool hold = bs >= 0 && bk == wk;
-    const uint64_t tie = __ballot(hold);
-    uint32_t we;
-    if (__popcll(tie) == 1) {
-      const int wl = __builtin_ctzll(tie);
-      we = (uint32_t)(wl + 64 * __builtin_amdgcn_readlane(bs, wl));
-    } else {
-      we = wave_min_u32(hold ? (uint32_t)(lane + 64 * bs) : 0xFFFFFFFFu);
-    }
-    if (lane == (int)(we & 63)) {
-      taken |= 1u << (we >> 6);
-      rescan();
-    }
-    if (lane == j) seli = (int)we;
-    kth = wk;
-  }
-  return kth;
-}
-
-// MFMA-order copy of one token row (position 8*j+e <- k = 4*e+j inside every
-// 32-element block) and, when xsum is non-null, its 128-wide group sums.
-__device__ __forceinline__ void write_xperm(const uint16_t *__restrict__ xrow,
-                                            uint16_t *__restrict__ xperm,
-                                            float *__restrict__ xsum, int t, int H, int lane) {
-  {
-    uint16_t *xo = xperm + (size_t)t * H;
-    for (int b = lane; b < (H >> 5); b += 64) {
-      const u32x4 *src = (const u32x4 *)(xrow + b * 32);
-      const u32x4 s0 = src[0], s1 = src[1], s2 = src[2], s3 = src[3];
-      const uint32_t in[16] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3],
-                               s2[0], s2[1], s2[2], s2[3], s3[0], s3[1], s3[2], s3[3]};
-      uint32_t out[16];
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int e2 = 0; e2 < 4; ++e2) {
-          const int ka = 8 * e2 + j, kb = ka + 4;
-          const uint32_t lo = (in[ka >> 1] >> (16 * (ka & 1))) & 0xFFFFu;
-          const uint32_t hi = (in[kb >> 1] >> (16 * (kb & 1))) & 0xFFFFu;
-          out[4 * j + e2] = lo | (hi << 16);
-        }
-      u32x4 *dst = (u32x4 *)(xo + b * 32);
-      dst[0] = u32x4{out[0], out[1], out[2], out[3]};
-      dst[1] = u32x4{out[4], out[5], out[6], out[7]};
-      dst[2] = u32x4{out[8], out[9], out[10], out[11]};
-      dst[3] = u32x4{out[12], out[13], out[14], out[15]};
-      if (xsum) {
-        // sum of the 128-wide group: this block's 32 values, then the 4
-        // consecutive lanes holding the group's blocks (fixed order)
-        float bs = 0.0f;
-#pragma unroll
-        for (int i2 = 0; i2 < 16; ++i2)
-          bs += __uint_as_float(in[i2] << 16) + __uint_as_float(in[i2] & 0xFFFF0000u);
-        bs += __shfl_xor(bs, 1, 64);
-        bs += __shfl_xor(bs, 2, 64);
-        if ((b & 3) == 0) xsum[(size_t)t * (H >> 7) + (b >> 2)] = bs;
-      }
-    }
-  }
-}
-
 template <int NV, int CH, bool EXACT>
 __global__ __launch_bounds__(256) void k_select(const float *__restrict__ approx,
                                                 const float *__restrict__ sgl,
@@ -315,7 +221,8 @@ __global__ __launch_bounds__(256) void k_select(const float *__restrict__ approx
       if (!EXACT) wn = fmaxf(wn, e < E ? wnorm[min(e, E - 1)] : 0.0f);
     }
     int seli;
-    const uint32_t kth = wave_topk<NV>(key, E, k, lane, seli);
+    uint32_t selk_unused;
+    const uint32_t kth = wave_topk<NV>(key, E, k, lane, seli, selk_unused);
     float selv = 0.0f, sgv = 0.0f;
     const uint16_t *xrow = x + (size_t)t * H;
     if (EXACT) {
@@ -481,7 +388,6 @@ __device__ __forceinline__ void dispatch_wave(const int *__restrict__ s_idx, int
     ds.inv[i] = pos;
     ds.ptok[pos] = t;
   }
-  for (int i = lane; i < ds.n_cnt; i += 64) ds.cnt[i] = 0;
 }
 
 template <int NV>
@@ -497,6 +403,8 @@ __global__ __launch_bounds__(1024) void k_select_small(const float *__restrict__
   __shared__ int s_idx[SMALL_MT * 32];
   __shared__ uint32_t s_msk[1024];
   __shared__ int s_off[1024];
+  __shared__ uint64_t s_cand[SMALL_MT][64];
+  __shared__ uint64_t s_sel[SMALL_MT][16];
   const int t = threadIdx.x >> 6, lane = threadIdx.x & 63;
   if (t < T) {
     const float *ar = logits + (size_t)t * E;
@@ -508,7 +416,8 @@ __global__ __launch_bounds__(1024) void k_select_small(const float *__restrict__
       key[i] = e < E ? ordered_key(v) : 0u;
     }
     int seli;
-    wave_topk<NV>(key, E, k, lane, seli);
+    uint32_t selk;
+    wave_topk_fast<NV>(key, E, k, lane, seli, selk, s_cand[t], s_sel[t]);
     const float selv = lane < k ? ar[seli] : 0.0f;
     const float vmax = __shfl(selv, 0, 64);
     const float p = lane < k ? expf(selv - vmax) : 0.0f;

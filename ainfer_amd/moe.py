@@ -84,7 +84,9 @@ class MoeLayer:
             raise L.MoeError("invalid shape or token count for workspace")
         ws = torch.empty(n + 256, dtype=torch.uint8, device=self.device)
         off = (-ws.data_ptr()) % 256
-        return ws[off:off + n]
+        ws = ws[off:off + n]
+        L.check(L.lib().ainfer_moe_workspace_init(C.byref(self.shape), _ptr(ws), n, _stream(None)))
+        return ws
 
     def forward(self, x, y, ws, stream=None):
         T = x.shape[0]

@@ -6,8 +6,8 @@ microseconds per token (H2048, 512 experts, top-10, I512, + shared expert,
 INT4 g128 fp16 scales).  `details` adds c1 at 1 and 4 tokens and the c2
 prefill (4096 tokens, Zipf(1.1) routing) in tokens/s and % of bf16 MFMA peak.
 
-`roofline.traffic` (HBM bytes per launch of the gate/up kernel) is read from
-the committed rocprofv3 PMC summary profiles/k_expert_gate_up_c1_T16_traffic.md
+`roofline.traffic` (HBM bytes per launch of the decode expert kernel) is read
+from the committed rocprofv3 PMC summary profiles/k_experts_decode_c1_T16_traffic.md
 (FETCH_SIZE + WRITE_SIZE, scaled by the same counters on a copy of known
 size, made with --calib-copy); null when that file is absent.
 
@@ -46,16 +46,18 @@ def unique_experts(layer, x, ws):
     return int(torch.unique(idx).numel())
 
 
-def gateup_bytes(cfg, U):
-    """INT4 nibbles + fp16 scales of gate and up for U routed experts and the
-    shared expert, plus the bf16 tokens read."""
-    per = lambda I: 2 * (cfg.hidden * I // 2 + cfg.hidden * I // 128 * 2)
-    return U * per(cfg.inter) + (per(cfg.shared_inter) if cfg.shared_inter else 0)
+def experts_bytes(cfg, U, T):
+    """Algorithmic bytes of the decode expert kernel (k_experts_decode): INT4
+    nibbles + fp16 scales of gate, up and down for U routed experts and the
+    shared expert, plus the bf16 tokens read and the bf16 outputs written."""
+    per = lambda I: 3 * (cfg.hidden * I // 2 + cfg.hidden * I // 128 * 2)
+    w = U * per(cfg.inter) + (per(cfg.shared_inter) if cfg.shared_inter else 0)
+    return w + 2 * T * cfg.hidden * 2
 
 
 def measured_traffic(T):
     """HBM bytes per gate/up launch from the committed PMC summary, or None."""
-    f = ROOT / "profiles" / f"k_expert_gate_up_c1_T{T}_traffic.md"
+    f = ROOT / "profiles" / f"k_experts_decode_c1_T{T}_traffic.md"
     if not f.exists():
         return None
     for line in f.read_text().splitlines():
@@ -195,16 +197,18 @@ def main():
         log(f"[bench] c1 decode T={T}")
         ms, st, U = run_decode(layers, c1, T, args.steps, args.warmup, 64, stream)
         nbytes = algorithmic_bytes(c1, T, round(U))
-        gu_us = st["gate_up"]
-        gu_gbs = gateup_bytes(c1, U) / (gu_us * 1e-6) / 1e9 if gu_us > 0 else 0.0
+        # T <= 16: two kernels; the profile's stage 2 is the routing kernel and
+        # stage 5 the expert kernel (gate/up + down + combine)
+        ex_us, route_us = st["down"], st["topk"]
+        ex_bytes = experts_bytes(c1, U, T)
+        ex_gbs = ex_bytes / (ex_us * 1e-6) / 1e9 if ex_us > 0 else 0.0
         decode[T] = {
             "us_per_step": ms * 1e3, "us_per_token": ms * 1e3 / T,
             "unique_experts": U, "alg_bytes": nbytes,
             "layer_hbm_gbs": nbytes / (ms * 1e-3) / 1e9,
             "layer_hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
-            "stage_us": {k: round(v, 3) for k, v in st.items()},
-            "gate_up_gbs": gu_gbs,
-            "gate_up_alg_bytes": gateup_bytes(c1, U),
+            "route_us": round(route_us, 3), "experts_us": round(ex_us, 3),
+            "experts_gbs": ex_gbs, "experts_alg_bytes": ex_bytes,
         }
         log(f"[bench]   {json.dumps(decode[T])}")
 
@@ -266,12 +270,12 @@ def main():
                                "(sigmoid gate), INT4 g128 fp16 scales",
                    "layer_copies": args.layers, "global_batch": Th,
                    "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "achieved": round(d1["gate_up_gbs"], 1),
+        "roofline": {"bound": "hbm", "achieved": round(d1["experts_gbs"], 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(d1["gate_up_gbs"] / HBM_PEAK_GBS, 4),
+                     "frac": round(d1["experts_gbs"] / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(Th),
-                     "kernel": "k_expert<fp16, gate/up> (dominant decode kernel)",
-                     "alg_bytes_per_launch": round(d1["gate_up_alg_bytes"])},
+                     "kernel": "k_experts_decode (gate/up + down + combine; dominant decode kernel)",
+                     "alg_bytes_per_launch": round(d1["experts_alg_bytes"])},
         "cpu_baseline": cpu,
         "details": {
             f"layer_hbm_frac_T{Th}": round(d1["layer_hbm_frac"], 4),

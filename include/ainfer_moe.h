@@ -119,6 +119,15 @@ int ainfer_moe_validate(const ainfer_moe_shape *shape);
 size_t ainfer_moe_workspace_bytes(const ainfer_moe_shape *shape,
                                   int32_t max_tokens);
 
+/* Zero the workspace's synchronisation words (a few KB at its start).  Call
+ * once after allocating a workspace, before its first forward call (a
+ * workspace allocated zero-filled needs no call).  The decode path (T <= 16)
+ * hands work between workgroups through counters there and every call leaves
+ * them zero again.  Calls that use one workspace must not overlap.
+ * Replaces the init-time arena set-up of decode_l0.cpp:220-295 for this
+ * layer's scratch. */
+int ainfer_moe_workspace_init(const ainfer_moe_shape *shape, void *workspace,
+                              size_t workspace_bytes, void *stream);
 /* The whole layer: y[T][H] (bf16) = MoE(x[T][H] bf16).
  * Replaces the reference MLP sub-sequence decode_l0.cpp:663-674
  * (xq -> gemvE gate -> gemvE up -> SiluMul -> xq -> gemvE down -> res) with
@@ -180,7 +189,9 @@ int ainfer_moe_fill(int32_t kind, uint64_t seed, float std_, size_t n,
 /* ---- per-stage timing (the AINFER_PROFILE instrumentation of
  * tools/decode/decode_l0.cpp:705,714-725,870-884, with device events) -----
  * While enabled, forward/block_forward record a HIP event on the caller's
- * stream before and after every kernel.  ainfer_moe_profile_read()
+ * stream before and after every kernel.  For T <= 16 the layer is two kernels:
+ * stage 2 is the routing kernel (logits, top-k, weights, dispatch) and stage
+ * 5 the expert kernel (gate/up, down and combine); stages 1, 3, 4 and 6 read 0.  ainfer_moe_profile_read()
  * waits for them and returns, per stage, the mean device time in
  * microseconds over the calls since enable, and the call count.  Stages:
  * 0 rmsnorm, 1 router, 2 top-k (+ dispatch when T <= 64), 3 dispatch,
