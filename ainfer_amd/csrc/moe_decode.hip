@@ -65,6 +65,9 @@ constexpr int SPIN_MAX = 1 << 20;
 #ifndef DEC_WAVES_PER_SIMD
 #define DEC_WAVES_PER_SIMD 6  // register budget of the expert kernel (<= 80 VGPRs)
 #endif
+#ifndef DEC_NW_MIN
+#define DEC_NW_MIN 4  // waves per expert workgroup (at least)
+#endif
 #ifndef DEC_COH
 #define DEC_COH true
 #endif
@@ -445,7 +448,7 @@ int decode_geometry(const ainfer_moe_shape &s, DecodeGeom *g) {
     return 0;
   g->wk_dn = wk;
   g->nw = g->wk_gu > g->wk_dn ? g->wk_gu : g->wk_dn;
-  if (g->nw < 4) g->nw = 4;
+  if (g->nw < DEC_NW_MIN) g->nw = DEC_NW_MIN;
   if (g->nw % g->wk_gu || g->nw % g->wk_dn || g->nw > 16) return 0;
   g->wr_gu = g->nw / g->wk_gu;
   g->wr_dn = g->nw / g->wk_dn;

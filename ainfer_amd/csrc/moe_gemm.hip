@@ -24,6 +24,8 @@
 // hit distinct bank groups (B: chunk q at q ^ bswz(r)).  Scales and the group sums sum_{k in g} a
 // (for x from k_select, for act from this kernel's MODE 0 epilogue) are
 // copied to LDS once per block.
+#include <type_traits>
+
 #include "moe_common.h"
 #include "moe_internal.h"
 
@@ -112,7 +114,10 @@ __global__ __launch_bounds__(128 * WN) void k_expert_gemm(GemmArgs a) {
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
-  const int wm = wave & 1, wn = wave >> 1;  // 2 token waves x WN row waves
+  // 2 token waves x WN row waves; wave w runs on SIMD w % 4, so each SIMD
+  // hosts waves of both token halves (a tile of <= 64 tokens keeps every
+  // SIMD busy)
+  const int wn = wave % WN, wm = wave / WN;
   const int m16 = lane & 15, q = lane >> 4;
 
   // ---- per-thread DMA sources: A_DMA A slots and B_DMA B slots per stage ---
@@ -153,12 +158,16 @@ __global__ __launch_bounds__(128 * WN) void k_expert_gemm(GemmArgs a) {
   }
   auto issue = [&](int g) {  // DMA of group g into stage g % STAGES
     const uint32_t base = lds0 + (uint32_t)(g % STAGES) * STAGE;
+#ifndef GEMM_EXP_NOADMA
 #pragma unroll
     for (int i = 0; i < Gm::A_DMA; ++i)
       dma16(asrc[i] + g * 256, base + (uint32_t)((i * NW + wave) * 1024));
+#endif
+#ifndef GEMM_EXP_NOBDMA
 #pragma unroll
     for (int i = 0; i < Gm::B_DMA; ++i)
       dma16(bsrc[i] + g * 64, base + A_STAGE + (uint32_t)((i * NW + wave) * 1024));
+#endif
   };
 
   // ---- prologue: group 0 in flight; tables to LDS ---------------------------
@@ -240,11 +249,15 @@ __global__ __launch_bounds__(128 * WN) void k_expert_gemm(GemmArgs a) {
     brow[ns] = MODE == 0 ? (ns < 2 ? wn * 32 + ns * 16 : COLS + wn * 32 + (ns - 2) * 16) + m16
                          : wn * 64 + ns * 16 + m16;
 
+  // The main loop, for NMS of this wave's 4 token subtiles (16 tokens each):
+  // subtiles past the tile's token count cost no MFMA or A read.
   f32x4 tot[4][4];
 #pragma unroll
   for (int ms = 0; ms < 4; ++ms)
 #pragma unroll
     for (int ns = 0; ns < 4; ++ns) tot[ms][ns] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto main_loop = [&](auto nms_c) {
+    constexpr int NMS = decltype(nms_c)::value;
   uint32_t magic;
   asm volatile("v_mov_b32 %0, 0x43004300" : "=v"(magic));
 
@@ -267,7 +280,7 @@ __global__ __launch_bounds__(128 * WN) void k_expert_gemm(GemmArgs a) {
     const uint8_t *sb = sa + A_STAGE;
     f32x4 c0[4];
 #pragma unroll
-    for (int ms = 0; ms < 4; ++ms) c0[ms] = *(const f32x4 *)(xs_lds + g * BM + wm * 64 + ms * 16 + 4 * q);
+    for (int ms = 0; ms < NMS; ++ms) c0[ms] = *(const f32x4 *)(xs_lds + g * BM + wm * 64 + ms * 16 + 4 * q);
     u32x4 bx[4];
     float sg[4];
 #pragma unroll
@@ -279,7 +292,7 @@ __global__ __launch_bounds__(128 * WN) void k_expert_gemm(GemmArgs a) {
 #pragma unroll
       for (int ns = 0; ns < 4; ++ns)
 #pragma unroll
-        for (int ms = 0; ms < 4; ++ms) tot[ms][ns] += sprev[ns] * acc[ms][ns];
+        for (int ms = 0; ms < NMS; ++ms) tot[ms][ns] += sprev[ns] * acc[ms][ns];
     }
     const uint8_t *arow = sa + (wm * 64 + m16) * 256;
 #pragma unroll
@@ -287,15 +300,19 @@ __global__ __launch_bounds__(128 * WN) void k_expert_gemm(GemmArgs a) {
       u32x4 af[4], bf[4];
       const int chunk = ((4 * q + j) ^ m16) << 4;
 #pragma unroll
-      for (int ms = 0; ms < 4; ++ms) af[ms] = *(const u32x4 *)(arow + ms * 16 * 256 + chunk);
+      for (int ms = 0; ms < NMS; ++ms) af[ms] = *(const u32x4 *)(arow + ms * 16 * 256 + chunk);
 #pragma unroll
       for (int ns = 0; ns < 4; ++ns) bf[ns] = nib_slice3(bx[ns], j, magic);
       // the first k-slice accumulates onto c0 directly (no copies of c0)
 #pragma unroll
-      for (int ms = 0; ms < 4; ++ms)
+      for (int ms = 0; ms < NMS; ++ms)
 #pragma unroll
         for (int ns = 0; ns < 4; ++ns)
+#ifdef GEMM_EXP_NOMFMA
+          acc[ms][ns] = (j == 0 ? c0[ms] : acc[ms][ns]) + (float)(af[ms][0] ^ bf[ns][1]);
+#else
           acc[ms][ns] = mfma_bf16_16x16x32(af[ms], bf[ns], j == 0 ? c0[ms] : acc[ms][ns]);
+#endif
     }
 #pragma unroll
     for (int ns = 0; ns < 4; ++ns) sprev[ns] = sg[ns];
@@ -303,7 +320,16 @@ __global__ __launch_bounds__(128 * WN) void k_expert_gemm(GemmArgs a) {
 #pragma unroll
   for (int ns = 0; ns < 4; ++ns)
 #pragma unroll
-    for (int ms = 0; ms < 4; ++ms) tot[ms][ns] += sprev[ns] * acc[ms][ns];
+    for (int ms = 0; ms < NMS; ++ms) tot[ms][ns] += sprev[ns] * acc[ms][ns];
+  };
+  // token subtiles of this wave holding tokens of the tile (wave-uniform)
+  const int nms = __builtin_amdgcn_readfirstlane(max(0, min(4, (mcnt - wm * 64 + 15) >> 4)));
+  if (nms > 2)
+    main_loop(std::integral_constant<int, 4>());
+  else if (nms > 0)
+    main_loop(std::integral_constant<int, 2>());
+  else
+    main_loop(std::integral_constant<int, 0>());
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   block_barrier();  // every wave's last read of the ring precedes the staging below
 
