@@ -68,8 +68,11 @@ constexpr int SPIN_MAX = 1 << 20;
 #ifndef DEC_NW_MIN
 #define DEC_NW_MIN 4  // waves per expert workgroup (at least)
 #endif
-#ifndef DEC_COH
-#define DEC_COH true
+#ifndef DEC_RG_GU
+#define DEC_RG_GU 1  // 16-row groups per wave, gate/up items (16 x 2 rows x H)
+#endif
+#ifndef DEC_RG_DN
+#define DEC_RG_DN 2  // 16-row groups per wave, down items
 #endif
 #ifndef DEC_PERSIST
 #define DEC_PERSIST 0     // 1: at most the resident workgroups, looping over items
@@ -358,7 +361,7 @@ __global__ __launch_bounds__(1024, DEC_WAVES_PER_SIMD) void k_experts_decode(Exp
     __syncthreads();
     if (is_gu) {
       // x (MFMA order) comes from the routing kernel: plain, cacheable loads
-      expert_lds_item<SD, KBW_GU, RG_GU, DEC_MT, 0, DEC_COH, NoWait, false>(a.gu, a.gu.tiles[tile],
+      expert_lds_item<SD, KBW_GU, RG_GU, DEC_MT, 0, true, NoWait, false>(a.gu, a.gu.tiles[tile],
                                                                           slab, lds);
       if (threadIdx.x >= 64) DEC_NEXT;
       // wave 0: its act stores, then the arrival
@@ -372,7 +375,7 @@ __global__ __launch_bounds__(1024, DEC_WAVES_PER_SIMD) void k_experts_decode(Exp
     // the down weights are requested before the wait for the tile's act rows
     const int32_t *gdone = &gu_done[tile * SY_STRIDE];
     int32_t *err = a.sync + SY_ERR;
-    expert_lds_item<SD, KBW_DN, RG_DN, DEC_MT, 1, DEC_COH>(a.dn, td, slab, lds, [=]() {
+    expert_lds_item<SD, KBW_DN, RG_DN, DEC_MT, 1, true>(a.dn, td, slab, lds, [=]() {
       block_wait_geq(gdone, sg, err);
       DTRACE_AT(1, item, 1);
     });
@@ -453,11 +456,15 @@ int decode_geometry(const ainfer_moe_shape &s, DecodeGeom *g) {
   g->wr_gu = g->nw / g->wk_gu;
   g->wr_dn = g->nw / g->wk_dn;
   const int Ngu = s.inter > s.shared_inter ? s.inter : s.shared_inter;
-  g->slabs_gu = (Ngu + 16 * RG_GATE_UP * g->wr_gu - 1) / (16 * RG_GATE_UP * g->wr_gu);
-  g->slabs_dn = (s.hidden + 16 * RG_DOWN * g->wr_dn - 1) / (16 * RG_DOWN * g->wr_dn);
+  g->slabs_gu = (Ngu + 16 * DEC_RG_GU * g->wr_gu - 1) / (16 * DEC_RG_GU * g->wr_gu);
+  g->slabs_dn = (s.hidden + 16 * DEC_RG_DN * g->wr_dn - 1) / (16 * DEC_RG_DN * g->wr_dn);
   // A staging only: the K-split partials reuse it (expert_lds_item, COH)
-  const size_t lds_gu = (size_t)g->nw * DEC_MT * 4 * 256 + (DEC_COH ? 0 : 2ull * g->nw * RG_GATE_UP * 1024);
-  const size_t lds_dn = (size_t)g->nw * DEC_MT * 2 * 256 + (DEC_COH ? 0 : 2ull * g->nw * RG_DOWN * 1024);
+  auto item_lds = [&](int kbw, int rg, int halves) {
+    const size_t aw = (size_t)DEC_MT * kbw * 256, part = (size_t)halves * rg * 1024;
+    return (size_t)g->nw * (aw + (aw >= part ? 0 : part));
+  };
+  const size_t lds_gu = item_lds(4, DEC_RG_GU, 2);
+  const size_t lds_dn = item_lds(2, DEC_RG_DN, 1);
   g->lds = lds_gu > lds_dn ? lds_gu : lds_dn;
   if (g->lds > 64 * 1024) return 0;
   return 1;
@@ -540,8 +547,8 @@ hipError_t launch_experts_decode(int scale_dtype, const DecodeGeom &g, ExpertArg
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return hipErrorInvalidDevice;
   auto kern = scale_dtype == AINFER_SCALE_FP16
-                  ? k_experts_decode<AINFER_SCALE_FP16, 4, RG_GATE_UP, 2, RG_DOWN>
-                  : k_experts_decode<AINFER_SCALE_BF16, 4, RG_GATE_UP, 2, RG_DOWN>;
+                  ? k_experts_decode<AINFER_SCALE_FP16, 4, DEC_RG_GU, 2, DEC_RG_DN>
+                  : k_experts_decode<AINFER_SCALE_BF16, 4, DEC_RG_GU, 2, DEC_RG_DN>;
   int resident = 0;
   for (int i = 0; i < n_cache; ++i)
     if (cache[i].dev == dev && cache[i].sd == scale_dtype && cache[i].threads == threads &&

@@ -195,9 +195,12 @@ __device__ __forceinline__ void expert_lds_item(const ExpertArgs &a, int4 t, int
   // COH: each wave's partials overwrite its own A region (its A reads have
   // completed: the MFMAs consumed them), and wave 0 alone finishes the item
   // while the other waves exit.
-  static_assert(!COH || AW >= (MODE == 0 ? 2 : 1) * RG * 1024, "partials fit the A region");
+  // (when a wave's partials do not fit its A region they go past all A
+  // regions: PART bytes per wave)
+  constexpr int PART = (MODE == 0 ? 2 : 1) * RG * 1024;
   auto part = [&](int w, int half) -> float * {
-    if (COH) return (float *)(lds + w * AW) + half * RG * 256;
+    if (COH)
+      return (float *)(AW >= PART ? lds + w * AW : lds + nw * AW + w * PART) + half * RG * 256;
     return red + (half * nw + w) * RG * 256;
   };
 #pragma unroll
