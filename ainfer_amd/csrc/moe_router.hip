@@ -206,9 +206,14 @@ __global__ __launch_bounds__(256) void k_select(const float *__restrict__ approx
   // candidate lists (fast path only)
   __shared__ int cl[SEL_WAVES][EXACT ? 1 : 1024];
   __shared__ float cv[SEL_WAVES][EXACT ? 1 : 1024];
+  __shared__ uint64_t s_cand[SEL_WAVES][64];
+  __shared__ uint64_t s_sel[SEL_WAVES][16];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int t = blockIdx.x * SEL_WAVES + wave;
   if (t < T) {
+    // the MFMA-order copy of x (and its group sums) does not depend on the
+    // routing: written first, its latency hides under the selection
+    if (xperm) write_xperm(x + (size_t)t * H, xperm, xsum, t, H, lane);
     const float *ar = approx + (size_t)t * E;
     // ---- k-th largest approximate logit -------------------------------
     uint32_t key[NV];
@@ -221,8 +226,9 @@ __global__ __launch_bounds__(256) void k_select(const float *__restrict__ approx
       if (!EXACT) wn = fmaxf(wn, e < E ? wnorm[min(e, E - 1)] : 0.0f);
     }
     int seli;
-    uint32_t selk_unused;
-    const uint32_t kth = wave_topk<NV>(key, E, k, lane, seli, selk_unused);
+    uint32_t selk;
+    wave_topk_fast<NV>(key, E, k, lane, seli, selk, s_cand[wave], s_sel[wave]);
+    const uint32_t kth = (uint32_t)__shfl((int)selk, k - 1, 64);
     float selv = 0.0f, sgv = 0.0f;
     const uint16_t *xrow = x + (size_t)t * H;
     if (EXACT) {
@@ -284,6 +290,23 @@ __global__ __launch_bounds__(256) void k_select(const float *__restrict__ approx
       }
       __builtin_amdgcn_wave_barrier();
       // ---- top-k among candidates (value desc, expert asc) ----------------
+      if (nc <= 64 && k <= 16) {
+        // rank of each candidate = candidates above it (unique composite keys)
+        auto comp = [&](int i) {
+          return ((uint64_t)ordered_key(cv[wave][i]) << 32) | (uint32_t)~(uint32_t)cl[wave][i];
+        };
+        const uint64_t mine = lane < nc ? comp(lane) : 0ull;
+        int rk = 0;
+        for (int j = 0; j < nc; ++j) rk += comp(j) > mine ? 1 : 0;
+        if (lane < nc && rk < k) s_sel[wave][rk] = ((uint64_t)(uint32_t)lane << 32) | (uint32_t)cl[wave][lane];
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        if (lane < k) {
+          const uint64_t pk = s_sel[wave][lane];
+          seli = (int)(uint32_t)pk;
+          selv = cv[wave][(int)(pk >> 32)];
+        }
+      } else {
       uint32_t tmask = 0;  // taken bits per lane slot (nc <= 1024: 16 slots)
       for (int j = 0; j < k; ++j) {
         uint32_t bk = 0;
@@ -303,6 +326,7 @@ __global__ __launch_bounds__(256) void k_select(const float *__restrict__ approx
           selv = cv[wave][ws];
         }
       }
+      }
       if (gw) sgv = canon_dot<CH>(xc, gw, lane, nch);
     }
     const float vmax = __shfl(selv, 0, 64);
@@ -317,7 +341,6 @@ __global__ __launch_bounds__(256) void k_select(const float *__restrict__ approx
     float g = 1.0f;
     if (gw) g = 1.0f / (1.0f + expf(-sgv));
     if (lane == 0) sgate[t] = g;
-    if (xperm) write_xperm(xrow, xperm, xsum, t, H, lane);
   }
   if (!fused) return;
   // ---- the last block runs the dispatch ---------------------------------
