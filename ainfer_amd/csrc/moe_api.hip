@@ -234,10 +234,24 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
                                 at<uint16_t>(ws, L.xperm), T, H, E, k, has_shared, &d, sync, st));
     pc->end(2);
     ExpertArgs gu = expert_args(s, w, L, ws, d, T, 0), dn = expert_args(s, w, L, ws, d, T, 1);
-    HIP_TRY(launch_experts_decode(s->scale_dtype, dg, gu, dn, at<float>(ws, L.w),
-                                  at<float>(ws, L.sg), d.inv, resid, y, sync,
-                                  max_tiles_bound(*s, T, DEC_MT),
-                                  max_tiles_bound(*s, DECODE_MAX_T, DEC_MT), st));
+    if (T <= FUSED_EXPERTS_MAX_T) {
+      // latency-bound: gate/up, down and combine in one launch
+      HIP_TRY(launch_experts_decode(s->scale_dtype, dg, gu, dn, at<float>(ws, L.w),
+                                    at<float>(ws, L.sg), d.inv, resid, y, sync,
+                                    max_tiles_bound(*s, T, DEC_MT),
+                                    max_tiles_bound(*s, DECODE_MAX_T, DEC_MT), st));
+    } else {
+      // bandwidth-bound: three launches whose items hold no waits
+      const int mtb = max_tiles_bound(*s, T, DEC_MT);
+      HIP_TRY(launch_expert_stream(0, s->scale_dtype, gu, mtb, 4, RG_GATE_UP, DEC_MT, st));
+      pc->end(4);
+      HIP_TRY(launch_expert_stream(1, s->scale_dtype, dn, mtb, 2, RG_DOWN, DEC_MT, st));
+      pc->end(5);
+      HIP_TRY(launch_combine(at<uint16_t>(ws, L.o), d.inv, at<float>(ws, L.w), at<float>(ws, L.sg),
+                             has_shared, resid, y, T, k, H, st));
+      pc->end(6);
+      return AINFER_OK;
+    }
     pc->end(5);
     return AINFER_OK;
   }

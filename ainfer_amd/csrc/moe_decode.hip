@@ -74,14 +74,10 @@ constexpr int SPIN_MAX = 1 << 20;
 #ifndef DEC_RG_DN
 #define DEC_RG_DN 2  // 16-row groups per wave, down items
 #endif
-#ifndef DEC_PERSIST
-#define DEC_PERSIST 0     // 1: at most the resident workgroups, looping over items
+#ifndef DEC_SPLIT
+#define DEC_SPLIT 0  // 1: gate/up in a launch of its own before the down items
 #endif
-#if DEC_PERSIST
-#define DEC_NEXT continue
-#else
 #define DEC_NEXT return
-#endif
 
 __device__ __forceinline__ bool spin_until_geq(const int32_t *p, int target) {
   for (int it = 0; it < SPIN_MAX; ++it) {
@@ -331,7 +327,10 @@ struct ExpertsDecodeArgs {
 // only ever waits for gate/up items of lower index, which are held by
 // resident workgroups, so the waits end.  (One item per workgroup instead
 // would be bound by the workgroup dispatch rate, about 150 per us.)
-template <int SD, int KBW_GU, int RG_GU, int KBW_DN, int RG_DN>
+// SPLIT: the gate/up items ran in an earlier launch (k_expert_lds): this
+// launch holds only the down items, which need no wait and read act with
+// plain (cacheable) loads.
+template <int SD, int KBW_GU, int RG_GU, int KBW_DN, int RG_DN, bool SPLIT>
 __global__ __launch_bounds__(1024, DEC_WAVES_PER_SIMD) void k_experts_decode(ExpertsDecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   // one counter per 256-byte line: same-line atomics and polls serialise
@@ -339,14 +338,10 @@ __global__ __launch_bounds__(1024, DEC_WAVES_PER_SIMD) void k_experts_decode(Exp
           *cnt = dn_done + a.cap * SY_STRIDE;
   const int lane = threadIdx.x & 63;
   const int sg = a.gu.n_slabs, sd = a.dn.n_slabs;
-  const int n_gu = a.max_tiles * sg, n_items = n_gu + a.max_tiles * sd;
+  const int n_gu = a.max_tiles * sg;
   const int n_tiles = *a.gu.n_tiles;
-#if DEC_PERSIST
-  for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
-#else
   {
-    const int item = blockIdx.x;
-#endif
+    const int item = blockIdx.x + (SPLIT ? n_gu : 0);
     // ---- item -> (kind, tile, slab): all gate/up items (tile-major,
     // slab-minor), then all down items ---------------------------------------
     const int is_gu = item < n_gu;
@@ -359,9 +354,9 @@ __global__ __launch_bounds__(1024, DEC_WAVES_PER_SIMD) void k_experts_decode(Exp
 #endif
     // the previous item's partials (read by wave 0) are no longer needed
     __syncthreads();
-    if (is_gu) {
+    if (!SPLIT && is_gu) {
       // x (MFMA order) comes from the routing kernel: plain, cacheable loads
-      expert_lds_item<SD, KBW_GU, RG_GU, DEC_MT, 0, true, NoWait, false>(a.gu, a.gu.tiles[tile],
+      expert_lds_item<SD, KBW_GU, RG_GU, DEC_MT, 0, true, false>(a.gu, a.gu.tiles[tile],
                                                                           slab, lds);
       if (threadIdx.x >= 64) DEC_NEXT;
       // wave 0: its act stores, then the arrival
@@ -375,8 +370,8 @@ __global__ __launch_bounds__(1024, DEC_WAVES_PER_SIMD) void k_experts_decode(Exp
     // the down weights are requested before the wait for the tile's act rows
     const int32_t *gdone = &gu_done[tile * SY_STRIDE];
     int32_t *err = a.sync + SY_ERR;
-    expert_lds_item<SD, KBW_DN, RG_DN, DEC_MT, 1, true>(a.dn, td, slab, lds, [=]() {
-      block_wait_geq(gdone, sg, err);
+    expert_lds_item<SD, KBW_DN, RG_DN, DEC_MT, 1, true, !SPLIT>(a.dn, td, slab, lds, [=]() {
+      if (!SPLIT) block_wait_geq(gdone, sg, err);
       DTRACE_AT(1, item, 1);
     });
     if (threadIdx.x >= 64) DEC_NEXT;
@@ -384,7 +379,7 @@ __global__ __launch_bounds__(1024, DEC_WAVES_PER_SIMD) void k_experts_decode(Exp
     // ---- wave 0: publish o; count this tile's down items and each token's
     // arrivals on this row slab --------------------------------------------
     wait_stores();
-    if (lane == 0 && atomicAdd(&dn_done[tile * SY_STRIDE], 1) == sd - 1) {
+    if (!SPLIT && lane == 0 && atomicAdd(&dn_done[tile * SY_STRIDE], 1) == sd - 1) {
       gu_done[tile * SY_STRIDE] = 0;  // all of the tile's down items have passed their wait
       dn_done[tile * SY_STRIDE] = 0;
     }
@@ -535,38 +530,21 @@ hipError_t launch_experts_decode(int scale_dtype, const DecodeGeom &g, ExpertArg
   const long grid = (long)max_tiles * (g.slabs_gu + g.slabs_dn);
   if (grid > 0x7FFFFFFF) return hipErrorInvalidValue;
   const int threads = g.nw * 64;
-  // resident workgroups = occupancy per CU x CUs, for this device, kernel,
-  // workgroup size and LDS size (a few configurations are cached)
-  struct Res {
-    int dev, sd, threads;
-    size_t lds;
-    int n;
-  };
-  static Res cache[16];
-  static int n_cache = 0;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return hipErrorInvalidDevice;
-  auto kern = scale_dtype == AINFER_SCALE_FP16
-                  ? k_experts_decode<AINFER_SCALE_FP16, 4, DEC_RG_GU, 2, DEC_RG_DN>
-                  : k_experts_decode<AINFER_SCALE_BF16, 4, DEC_RG_GU, 2, DEC_RG_DN>;
-  int resident = 0;
-  for (int i = 0; i < n_cache; ++i)
-    if (cache[i].dev == dev && cache[i].sd == scale_dtype && cache[i].threads == threads &&
-        cache[i].lds == g.lds)
-      resident = cache[i].n;
-  if (resident == 0) {
-    int per_cu = 0, cus = 0;
-    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, threads, g.lds);
+  if (DEC_SPLIT) {
+    // gate/up in its own launch, then the down items with the combine
+    hipError_t e = launch_expert_stream(0, scale_dtype, gu, max_tiles, 4, DEC_RG_GU, DEC_MT, s);
     if (e != hipSuccess) return e;
-    e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    if (e != hipSuccess) return e;
-    if (per_cu < 1 || cus < 1) return hipErrorInvalidConfiguration;
-    resident = per_cu * cus;
-    cache[n_cache % 16] = Res{dev, scale_dtype, threads, g.lds, resident};
-    ++n_cache;
+    const long gd = (long)max_tiles * g.slabs_dn;
+    if (scale_dtype == AINFER_SCALE_FP16)
+      k_experts_decode<AINFER_SCALE_FP16, 4, DEC_RG_GU, 2, DEC_RG_DN, true><<<(unsigned)gd, threads, g.lds, s>>>(a);
+    else
+      k_experts_decode<AINFER_SCALE_BF16, 4, DEC_RG_GU, 2, DEC_RG_DN, true><<<(unsigned)gd, threads, g.lds, s>>>(a);
+    return hipGetLastError();
   }
-  const long wgs = (DEC_PERSIST && grid > resident) ? resident : grid;
-  kern<<<(unsigned)wgs, threads, g.lds, s>>>(a);
+  if (scale_dtype == AINFER_SCALE_FP16)
+    k_experts_decode<AINFER_SCALE_FP16, 4, DEC_RG_GU, 2, DEC_RG_DN, false><<<(unsigned)grid, threads, g.lds, s>>>(a);
+  else
+    k_experts_decode<AINFER_SCALE_BF16, 4, DEC_RG_GU, 2, DEC_RG_DN, false><<<(unsigned)grid, threads, g.lds, s>>>(a);
   return hipGetLastError();
 }
 

@@ -182,7 +182,7 @@ __global__ __launch_bounds__(1024) void k_expert_lds(ExpertArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int tile_id = blockIdx.x / a.n_slabs, slab = blockIdx.x % a.n_slabs;
   if (tile_id >= *a.n_tiles) return;
-  expert_lds_item<SD, KBW, RG, MT, MODE>(a, a.tiles[tile_id], slab, lds);
+  expert_lds_item<SD, KBW, RG, MT, MODE, false, false, true>(a, a.tiles[tile_id], slab, lds);
 }
 
 }  // namespace
@@ -252,7 +252,11 @@ hipError_t launch_expert_stream(int mode, int scale_dtype, ExpertArgs a, int max
   a.n_slabs = (Nmax + 16 * rg * a.WR - 1) / (16 * rg * a.WR);
   const int threads = a.WK * a.WR * 64;
   size_t lds = sizeof(float) * 2 * (size_t)a.WK * a.WR * rg * 256;
-  if (mt == DEC_MT) lds += (size_t)a.WK * a.WR * DEC_MT * kbw * 256;  // A staging
+  if (mt == DEC_MT) {
+    // A staging; the K-split partials reuse it when they fit (expert_lds_item, ALIAS)
+    const size_t aw = (size_t)DEC_MT * kbw * 256, part = (size_t)(mode == 0 ? 2 : 1) * rg * 1024;
+    lds = (size_t)a.WK * a.WR * (aw + (aw >= part ? 0 : part));
+  }
   if (lds > 160 * 1024) return hipErrorInvalidValue;
   const long grid = (long)max_tiles * a.n_slabs;
   if (grid > 0x7FFFFFFF) return hipErrorInvalidValue;

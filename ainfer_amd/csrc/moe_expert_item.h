@@ -74,8 +74,8 @@ struct NoWait {
 // LDS it needs is nw * MT * KBW * 256 bytes.
 // wait(): called by every thread after the weight loads are issued and
 // before the A rows are read (the weights never depend on earlier work).
-template <int SD, int KBW, int RG, int MT, int MODE, bool COH = false, typename Wait = NoWait,
-          bool COH_IN = COH>
+template <int SD, int KBW, int RG, int MT, int MODE, bool COH = false, bool COH_IN = COH,
+          bool ALIAS = COH, typename Wait = NoWait>
 __device__ __forceinline__ void expert_lds_item(const ExpertArgs &a, int4 t, int slab,
                                                 uint8_t *lds, Wait wait = Wait()) {
   constexpr int AROW = KBW * 256;  // bytes of one token row in this wave's k-range
@@ -199,7 +199,7 @@ __device__ __forceinline__ void expert_lds_item(const ExpertArgs &a, int4 t, int
   // regions: PART bytes per wave)
   constexpr int PART = (MODE == 0 ? 2 : 1) * RG * 1024;
   auto part = [&](int w, int half) -> float * {
-    if (COH)
+    if (ALIAS)
       return (float *)(AW >= PART ? lds + w * AW : lds + nw * AW + w * PART) + half * RG * 256;
     return red + (half * nw + w) * RG * 256;
   };
@@ -211,10 +211,10 @@ __device__ __forceinline__ void expert_lds_item(const ExpertArgs &a, int4 t, int
       if (MODE == 0) part(wave, 1)[g * 256 + (4 * q + r) * 16 + m] = tot1[g][r];
     }
   __syncthreads();
-  if (COH && wave != 0) return;
+  if (ALIAS && wave != 0) return;
   // tokens < mcnt <= MT only
-  const int nthr = COH ? 64 : nw * 64;
-  for (int idx = COH ? lane : (int)threadIdx.x; idx < a.WR * RG * 16 * MT; idx += nthr) {
+  const int nthr = ALIAS ? 64 : nw * 64;
+  for (int idx = ALIAS ? lane : (int)threadIdx.x; idx < a.WR * RG * 16 * MT; idx += nthr) {
     const int rgrp = idx / (16 * MT), cell = idx % (16 * MT);  // rgrp = wr * RG + g
     const int rwr = rgrp / RG, g = rgrp % RG;
     const int tm = cell >> 4, tn = cell & 15;

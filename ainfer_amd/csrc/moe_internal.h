@@ -128,6 +128,10 @@ constexpr int FUSED_DISPATCH_MAX_T = 64;
 
 // ---- decode layer in two launches (moe_decode.hip), T <= DECODE_MAX_T ----
 constexpr int DECODE_MAX_T = EXACT_ROUTER_MAX_T;
+// up to this many tokens the expert stages run fused in one launch
+// (k_experts_decode); above it as gate/up, down and combine launches (the
+// fused items' handoffs cost more than the two launches they save)
+constexpr int FUSED_EXPERTS_MAX_T = 2;
 // sync region (int32 words at the start of the workspace, zero between calls)
 // Counters sit SY_STRIDE words (256 bytes) apart.
 enum { SY_STRIDE = 64, SY_ROUTER_DONE = 0, SY_SELECT = SY_STRIDE, SY_ERR = 2 * SY_STRIDE,

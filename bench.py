@@ -6,8 +6,8 @@ microseconds per token (H2048, 512 experts, top-10, I512, + shared expert,
 INT4 g128 fp16 scales).  `details` adds c1 at 1 and 4 tokens and the c2
 prefill (4096 tokens, Zipf(1.1) routing) in tokens/s and % of bf16 MFMA peak.
 
-`roofline.traffic` (HBM bytes per launch of the decode expert kernel) is read
-from the committed rocprofv3 PMC summary profiles/k_experts_decode_c1_T16_traffic.md
+`roofline.traffic` (HBM bytes per launch of the dominant decode kernel) is read
+from the committed rocprofv3 PMC summary profiles/<kernel>_c1_T16_traffic.md
 (FETCH_SIZE + WRITE_SIZE, scaled by the same counters on a copy of known
 size, made with --calib-copy); null when that file is absent.
 
@@ -46,6 +46,13 @@ def unique_experts(layer, x, ws):
     return int(torch.unique(idx).numel())
 
 
+def gateup_bytes(cfg, U):
+    """INT4 nibbles + fp16 scales of gate and up for U routed experts and the
+    shared expert (the gate/up kernel's weight bytes)."""
+    per = lambda I: 2 * (cfg.hidden * I // 2 + cfg.hidden * I // 128 * 2)
+    return U * per(cfg.inter) + (per(cfg.shared_inter) if cfg.shared_inter else 0)
+
+
 def experts_bytes(cfg, U, T):
     """Algorithmic bytes of the decode expert kernel (k_experts_decode): INT4
     nibbles + fp16 scales of gate, up and down for U routed experts and the
@@ -55,9 +62,9 @@ def experts_bytes(cfg, U, T):
     return w + 2 * T * cfg.hidden * 2
 
 
-def measured_traffic(T):
-    """HBM bytes per gate/up launch from the committed PMC summary, or None."""
-    f = ROOT / "profiles" / f"k_experts_decode_c1_T{T}_traffic.md"
+def measured_traffic(kernel, T):
+    """HBM bytes per launch of `kernel` from the committed PMC summary, or None."""
+    f = ROOT / "profiles" / f"{kernel}_c1_T{T}_traffic.md"
     if not f.exists():
         return None
     for line in f.read_text().splitlines():
@@ -197,11 +204,19 @@ def main():
         log(f"[bench] c1 decode T={T}")
         ms, st, U = run_decode(layers, c1, T, args.steps, args.warmup, 64, stream)
         nbytes = algorithmic_bytes(c1, T, round(U))
-        # T <= 16: two kernels; the profile's stage 2 is the routing kernel and
-        # stage 5 the expert kernel (gate/up + down + combine)
-        ex_us, route_us = st["down"], st["topk"]
+        # T <= 16: stage 2 is the routing kernel; the expert stages are one
+        # fused kernel (stage 5, T <= 2) or gate/up, down and combine
+        route_us = st["topk"]
+        ex_us = st["gate_up"] + st["down"] + st["combine"]
         ex_bytes = experts_bytes(c1, U, T)
         ex_gbs = ex_bytes / (ex_us * 1e-6) / 1e9 if ex_us > 0 else 0.0
+        if st["gate_up"] > 0:   # dominant kernel: gate/up
+            dom = ("k_expert_gate_up", "k_expert_lds<fp16, gate/up> (dominant decode kernel)",
+                   gateup_bytes(c1, U), st["gate_up"])
+        else:                   # dominant kernel: the fused expert kernel
+            dom = ("k_experts_decode",
+                   "k_experts_decode (gate/up + down + combine; dominant decode kernel)",
+                   ex_bytes, ex_us)
         decode[T] = {
             "us_per_step": ms * 1e3, "us_per_token": ms * 1e3 / T,
             "unique_experts": U, "alg_bytes": nbytes,
@@ -209,6 +224,9 @@ def main():
             "layer_hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
             "route_us": round(route_us, 3), "experts_us": round(ex_us, 3),
             "experts_gbs": ex_gbs, "experts_alg_bytes": ex_bytes,
+            "stage_us": {k: round(v, 3) for k, v in st.items() if v > 0},
+            "dominant": {"file": dom[0], "kernel": dom[1], "alg_bytes": dom[2],
+                         "us": round(dom[3], 3), "gbs": dom[2] / (dom[3] * 1e-6) / 1e9 if dom[3] else 0},
         }
         log(f"[bench]   {json.dumps(decode[T])}")
 
@@ -270,12 +288,12 @@ def main():
                                "(sigmoid gate), INT4 g128 fp16 scales",
                    "layer_copies": args.layers, "global_batch": Th,
                    "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "achieved": round(d1["experts_gbs"], 1),
+        "roofline": {"bound": "hbm", "achieved": round(d1["dominant"]["gbs"], 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(d1["experts_gbs"] / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic(Th),
-                     "kernel": "k_experts_decode (gate/up + down + combine; dominant decode kernel)",
-                     "alg_bytes_per_launch": round(d1["experts_alg_bytes"])},
+                     "frac": round(d1["dominant"]["gbs"] / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(d1["dominant"]["file"], Th),
+                     "kernel": d1["dominant"]["kernel"],
+                     "alg_bytes_per_launch": round(d1["dominant"]["alg_bytes"])},
         "cpu_baseline": cpu,
         "details": {
             f"layer_hbm_frac_T{Th}": round(d1["layer_hbm_frac"], 4),

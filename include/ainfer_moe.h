@@ -189,9 +189,10 @@ int ainfer_moe_fill(int32_t kind, uint64_t seed, float std_, size_t n,
 /* ---- per-stage timing (the AINFER_PROFILE instrumentation of
  * tools/decode/decode_l0.cpp:705,714-725,870-884, with device events) -----
  * While enabled, forward/block_forward record a HIP event on the caller's
- * stream before and after every kernel.  For T <= 16 the layer is two kernels:
- * stage 2 is the routing kernel (logits, top-k, weights, dispatch) and stage
- * 5 the expert kernel (gate/up, down and combine); stages 1, 3, 4 and 6 read 0.  ainfer_moe_profile_read()
+ * stream before and after every kernel.  For T <= 16 stage 2 is the routing
+ * kernel (logits, top-k, weights, dispatch) and stages 1 and 3 read 0; for
+ * T <= 2 stage 5 is the fused expert kernel (gate/up, down and combine) and
+ * stages 4 and 6 read 0.  ainfer_moe_profile_read()
  * waits for them and returns, per stage, the mean device time in
  * microseconds over the calls since enable, and the call count.  Stages:
  * 0 rmsnorm, 1 router, 2 top-k (+ dispatch when T <= 64), 3 dispatch,
