@@ -8,7 +8,7 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "libainfer_moe.so"
 
 OK = 0
-ERR_SHAPE, ERR_NULL, ERR_WORKSPACE, ERR_TOKENS, ERR_HIP, ERR_ARG = -1, -2, -3, -4, -5, -6
+ERR_SHAPE, ERR_NULL, ERR_WORKSPACE, ERR_TOKENS, ERR_HIP, ERR_ARG, ERR_SYNC = -1, -2, -3, -4, -5, -6, -7
 SCALE_BF16, SCALE_FP16 = 0, 1
 NORM_PLAIN, NORM_ONE_PLUS = 0, 1
 FILL_BYTES, FILL_BF16_NORMAL, FILL_FP16_ABSNORMAL, FILL_BF16_ABSNORMAL = 0, 1, 2, 3
@@ -17,7 +17,7 @@ MAX_TOKENS = 65536
 # every symbol include/ainfer_moe.h declares
 EXPORTS = (
     "ainfer_moe_strerror", "ainfer_moe_validate", "ainfer_moe_workspace_bytes",
-    "ainfer_moe_workspace_init",
+    "ainfer_moe_workspace_init", "ainfer_moe_workspace_check",
     "ainfer_moe_forward", "ainfer_moe_block_forward", "ainfer_moe_route",
     "ainfer_moe_dispatch", "ainfer_moe_rmsnorm", "ainfer_moe_fill",
     "ainfer_moe_profile_enable", "ainfer_moe_profile_read",
@@ -61,6 +61,7 @@ def lib():
         L.ainfer_moe_workspace_bytes.restype = SZ
         L.ainfer_moe_workspace_bytes.argtypes = [sp, I32]
         L.ainfer_moe_workspace_init.argtypes = [sp, P, SZ, P]
+        L.ainfer_moe_workspace_check.argtypes = [sp, P, SZ, P]
         L.ainfer_moe_forward.argtypes = [sp, wp, P, P, I32, P, SZ, P]
         L.ainfer_moe_block_forward.argtypes = [sp, wp, P, I32, F, P, P, I32, P, SZ, P]
         L.ainfer_moe_route.argtypes = [sp, wp, P, I32, P, P, P, P, P, SZ, P]

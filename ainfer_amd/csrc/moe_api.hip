@@ -3,6 +3,8 @@
 // down -> combine.  Host code; every device buffer comes from the caller.
 #include <string.h>
 
+#include <vector>
+
 #include "moe_common.h"
 #include "moe_internal.h"
 
@@ -27,7 +29,7 @@ void prof_flush_slot(int s) {
   for (int i = 0; i <= NSTAGE; ++i) {
     if (!g_prof.used[s][i]) continue;
     if (prev >= 0) {
-      hipEventSynchronize(g_prof.ev[s][i]);
+      (void)hipEventSynchronize(g_prof.ev[s][i]);
       float ms = 0.f;
       if (hipEventElapsedTime(&ms, g_prof.ev[s][prev], g_prof.ev[s][i]) == hipSuccess) {
         g_prof.sum_us[i - 1] += ms * 1000.0;
@@ -58,13 +60,13 @@ struct ProfCall {
     if (s >= 0) rec(stage + 1);
   }
   void rec(int i) {
-    hipEventRecord(g_prof.ev[s][i], st);
+    (void)hipEventRecord(g_prof.ev[s][i], st);
     g_prof.used[s][i] = true;
   }
 };
 
 struct Layout {
-  size_t sync, sync_words, logits, sg_logit, idx, w, sg, xperm, chunk_counts, rank, counts, offsets, perm, inv,
+  size_t sync, sync_words, slots, logits, sg_logit, idx, w, sg, xperm, chunk_counts, rank, counts, offsets, perm, inv,
       ptok, tiles, n_tiles, ticket, act, act_s, o, h, wnorm, xsum, asum, asum_s, total;
 };
 
@@ -95,8 +97,9 @@ Layout layout_of(const ainfer_moe_shape &s, int Tm) {
   {
     DecodeGeom g;
     const int slabs = decode_geometry(s, &g) ? g.slabs_dn : 0;
-    L.sync_words = SY_TILES + SY_STRIDE * (2 * (size_t)max_tiles_bound(s, DECODE_MAX_T, DEC_MT) +
-                                           (size_t)DECODE_MAX_T * slabs);
+    L.slots = SY_TILES + SY_STRIDE * (2 * (size_t)max_tiles_bound(s, DECODE_MAX_T, DEC_MT) +
+                                      (size_t)DECODE_MAX_T * slabs);  // in words
+    L.sync_words = L.slots + (size_t)DECODE_MAX_T * (E + 1);
     L.sync = take(L.sync_words * 4);
   }
   L.logits = take(T * E * 4);
@@ -231,7 +234,8 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
     HIP_TRY(launch_route_decode(x, w->router_w, w->router_bias, w->shared_gate_w,
                                 at<float>(ws, L.logits), at<float>(ws, L.sg_logit),
                                 at<int32_t>(ws, L.idx), at<float>(ws, L.w), at<float>(ws, L.sg),
-                                at<uint16_t>(ws, L.xperm), T, H, E, k, has_shared, &d, sync, st));
+                                at<uint16_t>(ws, L.xperm), T, H, E, k, has_shared, &d, sync,
+                                (uint32_t *)(sync + L.slots), st));
     pc->end(2);
     ExpertArgs gu = expert_args(s, w, L, ws, d, T, 0), dn = expert_args(s, w, L, ws, d, T, 1);
     if (T <= FUSED_EXPERTS_MAX_T) {
@@ -382,6 +386,7 @@ const char *ainfer_moe_strerror(int status) {
   case AINFER_ERR_TOKENS: return "token count out of range";
   case AINFER_ERR_HIP: return "HIP runtime error";
   case AINFER_ERR_ARG: return "argument out of range";
+  case AINFER_ERR_SYNC: return "a device-side wait ran out (workspace synchronisation words)";
   default: return "unknown status";
   }
 }
@@ -418,6 +423,22 @@ int ainfer_moe_workspace_init(const ainfer_moe_shape *s, void *ws, size_t ws_byt
   if ((rc = check_ws(s, 0, ws, ws_bytes))) return rc;
   const Layout L = layout_of(*s, 0);
   HIP_TRY(launch_zero_i32(at<int32_t>(ws, L.sync), (int)L.sync_words, (hipStream_t)stream));
+  return AINFER_OK;
+}
+
+int ainfer_moe_workspace_check(const ainfer_moe_shape *s, const void *ws, size_t ws_bytes,
+                               void *stream) {
+  int rc = ainfer_moe_validate(s);
+  if (rc) return rc;
+  if ((rc = check_ws(s, 0, const_cast<void *>(ws), ws_bytes))) return rc;
+  const Layout L = layout_of(*s, 0);
+  std::vector<int32_t> h(L.sync_words);
+  HIP_TRY(hipStreamSynchronize((hipStream_t)stream));
+  HIP_TRY(hipMemcpy(h.data(), at<int32_t>(const_cast<void *>(ws), L.sync), L.sync_words * 4,
+                    hipMemcpyDeviceToHost));
+  if (h[SY_ERR]) return AINFER_ERR_SYNC;
+  for (size_t i = 0; i < h.size(); ++i)
+    if (h[i]) return AINFER_ERR_WORKSPACE;
   return AINFER_OK;
 }
 
@@ -477,7 +498,8 @@ int ainfer_moe_route(const ainfer_moe_shape *s, const ainfer_moe_weights *w, con
                                 logits ? logits : at<float>(ws, L.logits),
                                 at<float>(ws, L.sg_logit), topk_idx, topk_w, shared_gate, nullptr,
                                 T, s->hidden, s->n_experts, s->top_k, s->shared_inter > 0,
-                                nullptr, at<int32_t>(ws, L.sync), st));
+                                nullptr, at<int32_t>(ws, L.sync),
+                                at<uint32_t>(ws, L.sync) + L.slots, st));
     return AINFER_OK;
   }
   if (T <= EXACT_ROUTER_MAX_T) {

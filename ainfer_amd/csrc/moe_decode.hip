@@ -9,12 +9,16 @@
 // handed over by sc1 stores and loads instead of fences (moe_common.h):
 //
 //  k_route_decode   workgroups [0, NR): canonical router logits, one
-//                   (RD_R rows x RD_TT tokens) unit per wave, one arrival per
-//                   workgroup on router_done; the last workgroup (one wave
-//                   per token) writes x in MFMA order, waits for
-//                   router_done == NR, takes the exact top-k, the weights and
-//                   the shared gate, and builds the dispatch (tiles of at
-//                   most DEC_MT tokens) from LDS.
+//                   (RD_R rows x RD_TT tokens) unit per wave, each stored
+//                   with an sc1 store as ~bits into a key slot of the sync
+//                   region (never 0: ~bits == 0 only for one NaN pattern no
+//                   bf16 product or sum yields); the last workgroup (one wave
+//                   per token) writes x in MFMA order, polls its token's slots
+//                   until none is 0, clears them, takes the exact top-k, the
+//                   weights and the shared gate, and builds the dispatch
+//                   (tiles of at most DEC_MT tokens) from LDS.  A slot that is
+//                   its own ready flag saves the store wait, barrier and
+//                   counter round trip of an arrival.
 //  k_experts_decode one workgroup per item: first every gate/up + SiLU item
 //                   (tile-major, slab-minor), one arrival each on
 //                   gu_done[tile]; then every down item, which requests its
@@ -29,7 +33,7 @@
 // Waits are bounded (SPIN_MAX polls); one that runs out sets the error word
 // of the sync region and carries on.
 //
-// Every counter is reset by its last user (router_done by the selection
+// Every counter is reset by its last user (the logit slots by the selection
 // workgroup, gu_done/dn_done by a tile's last down item, a (token, slab)
 // counter by its last arrival), so the sync region is zero again when a call
 // ends.  It must be zero before the first call (ainfer_moe_workspace_init).
@@ -61,6 +65,7 @@ namespace {
 constexpr int RD_WAVES = 16;  // waves per k_route_decode workgroup
 constexpr int RD_R = 2;      // router rows per wave
 constexpr int RD_TT = 4;     // tokens per router pass
+constexpr int RD_NB = 2;     // 8-element chunks per lane whose loads are issued together
 constexpr int SPIN_MAX = 1 << 20;
 #ifndef DEC_WAVES_PER_SIMD
 #define DEC_WAVES_PER_SIMD 6  // register budget of the expert kernel (<= 80 VGPRs)
@@ -77,7 +82,6 @@ constexpr int SPIN_MAX = 1 << 20;
 #ifndef DEC_SPLIT
 #define DEC_SPLIT 0  // 1: gate/up in a launch of its own before the down items
 #endif
-#define DEC_NEXT return
 
 __device__ __forceinline__ bool spin_until_geq(const int32_t *p, int target) {
   for (int it = 0; it < SPIN_MAX; ++it) {
@@ -92,17 +96,6 @@ __device__ __forceinline__ bool spin_until_geq(const int32_t *p, int target) {
 __device__ __forceinline__ void block_wait_geq(const int32_t *p, int target, int32_t *err) {
   if (threadIdx.x == 0 && !spin_until_geq(p, target)) atomicOr(err, 1);
   __syncthreads();
-}
-
-// Workgroup-wide: every wave waits for its sc1 stores, then one arrival.
-// Returns the counter's previous value in every thread.
-__device__ __forceinline__ int block_arrive(int32_t *p) {
-  __shared__ int old;
-  wait_stores();
-  __syncthreads();
-  if (threadIdx.x == 0) old = atomicAdd(p, 1);
-  __syncthreads();
-  return old;
 }
 
 // A uniform 16-byte load through the scalar cache (the compiler cannot
@@ -124,6 +117,7 @@ struct RouteDecodeArgs {
   uint16_t *xperm;
   DispatchOut ds;
   int32_t *sync;
+  uint32_t *slots;  // [DECODE_MAX_T][E + 1] ~bits of the logits (sync region)
   int T, H, E, k, has_shared, NR;
 };
 
@@ -134,7 +128,7 @@ __device__ __forceinline__ void dispatch_decode(const int32_t *__restrict__ idx,
                                                 int E, int has_shared, const DispatchOut &ds) {
   __shared__ uint32_t msk[1024];
   __shared__ int offl[1024];
-  __shared__ int wsum_c[RD_WAVES], wsum_t[RD_WAVES];
+  __shared__ int wsum[RD_WAVES];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   constexpr int NT = RD_WAVES * 64;
   for (int e = tid; e < E; e += NT) msk[e] = 0u;
@@ -149,30 +143,19 @@ __device__ __forceinline__ void dispatch_decode(const int32_t *__restrict__ idx,
     c_loc += c;
     t_loc += (c + DEC_MT - 1) / DEC_MT;
   }
-  int ci = c_loc, ti = t_loc;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int a = __shfl_up(ci, d, 64), b = __shfl_up(ti, d, 64);
-    if (lane >= d) {
-      ci += a;
-      ti += b;
-    }
-  }
-  if (lane == 63) {
-    wsum_c[wv] = ci;
-    wsum_t[wv] = ti;
-  }
+  // one scan of (tiles << 16 | tokens): both stay below 2^16 (T * k entries)
+  const int packed = wave_scan_incl((t_loc << 16) | c_loc);
+  if (lane == 63) wsum[wv] = packed;
   __syncthreads();
-  int cb = 0, tb0 = 0, ctot = 0, ttot = 0;
+  int base = 0, tot = 0;
 #pragma unroll
   for (int w = 0; w < RD_WAVES; ++w) {
-    if (w < wv) {
-      cb += wsum_c[w];
-      tb0 += wsum_t[w];
-    }
-    ctot += wsum_c[w];
-    ttot += wsum_t[w];
+    const int v = wsum[w];
+    base += w < wv ? v : 0;
+    tot += v;
   }
+  const int cb = base & 0xFFFF, tb0 = base >> 16, ctot = tot & 0xFFFF, ttot = tot >> 16;
+  const int ci = packed & 0xFFFF, ti = packed >> 16;
   int o = cb + ci - c_loc, tb = tb0 + ti - t_loc;
   for (int e = e0; e < e1; ++e) {
     const int c = __popc(msk[e]);
@@ -200,12 +183,11 @@ __device__ __forceinline__ void dispatch_decode(const int32_t *__restrict__ idx,
 
 template <int NV>
 __global__ __launch_bounds__(RD_WAVES * 64) void k_route_decode(RouteDecodeArgs a) {
-  __shared__ uint64_t s_cand[RD_WAVES][64];
+  __shared__ uint64_t s_cand[RD_WAVES][68];
   __shared__ uint64_t s_sel[RD_WAVES][16];
   __shared__ int s_idx[RD_WAVES * 32];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int T = a.T, H = a.H, E = a.E, k = a.k;
-  int32_t *router_done = a.sync + SY_ROUTER_DONE;
   DTRACE(0, 0);
   if ((int)blockIdx.x < a.NR) {
     // ---- canonical logits of RD_R rows x RD_TT tokens per wave: lane l
@@ -228,26 +210,38 @@ __global__ __launch_bounds__(RD_WAVES * 64) void k_route_decode(RouteDecodeArgs 
       for (int i = 0; i < RD_R; ++i)
 #pragma unroll
         for (int j = 0; j < RD_TT; ++j) acc[i][j] = 0.0f;
-      for (int c = lane; c < nch; c += 64) {
-        u32x4 wv[RD_R], xv[RD_TT];
+      // RD_NB chunks' loads in flight at once; the sums still run over
+      // chunks l, l + 64, ... in order
+      for (int cb = lane; cb < nch; cb += 64 * RD_NB) {
+        u32x4 wv[RD_NB][RD_R], xv[RD_NB][RD_TT];
 #pragma unroll
-        for (int i = 0; i < RD_R; ++i) wv[i] = *(const u32x4 *)(wr[i] + (size_t)c * 8);
+        for (int b = 0; b < RD_NB; ++b) {
+          const int c = min(cb + 64 * b, nch - 1);
 #pragma unroll
-        for (int j = 0; j < RD_TT; ++j)
-          xv[j] = *(const u32x4 *)(a.x + (size_t)min(t0 + j, T - 1) * H + (size_t)c * 8);
+          for (int i = 0; i < RD_R; ++i) wv[b][i] = *(const u32x4 *)(wr[i] + (size_t)c * 8);
 #pragma unroll
-        for (int i = 0; i < RD_R; ++i)
+          for (int j = 0; j < RD_TT; ++j)
+            xv[b][j] = *(const u32x4 *)(a.x + (size_t)min(t0 + j, T - 1) * H + (size_t)c * 8);
+        }
 #pragma unroll
-          for (int j = 0; j < RD_TT; ++j) {
-            float s = acc[i][j];
+        for (int b = 0; b < RD_NB; ++b) {
+          // past the row end: computed on a clamped chunk and discarded, so
+          // no load depends on a branch
+          const bool in = cb + 64 * b < nch;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              s = __builtin_fmaf(__uint_as_float(xv[j][q] << 16), __uint_as_float(wv[i][q] << 16), s);
-              s = __builtin_fmaf(__uint_as_float(xv[j][q] & 0xFFFF0000u),
-                                 __uint_as_float(wv[i][q] & 0xFFFF0000u), s);
+          for (int i = 0; i < RD_R; ++i)
+#pragma unroll
+            for (int j = 0; j < RD_TT; ++j) {
+              float s = acc[i][j];
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                s = __builtin_fmaf(__uint_as_float(xv[b][j][q] << 16), __uint_as_float(wv[b][i][q] << 16), s);
+                s = __builtin_fmaf(__uint_as_float(xv[b][j][q] & 0xFFFF0000u),
+                                   __uint_as_float(wv[b][i][q] & 0xFFFF0000u), s);
+              }
+              acc[i][j] = in ? s : acc[i][j];
             }
-            acc[i][j] = s;
-          }
+        }
       }
 #pragma unroll
       for (int m = 32; m >= 1; m >>= 1)
@@ -262,42 +256,50 @@ __global__ __launch_bounds__(RD_WAVES * 64) void k_route_decode(RouteDecodeArgs 
           for (int j = 0; j < RD_TT; ++j) {
             const int r = rbase + i, t = t0 + j;
             if (r >= nrows || t >= T) continue;
-            if (r < E)
-              st_dev(a.logits + (size_t)t * E + r, a.bias ? acc[i][j] + a.bias[r] : acc[i][j]);
-            else
-              st_dev(a.sgl + t, acc[i][j]);
+            const float v = r < E && a.bias ? acc[i][j] + a.bias[r] : acc[i][j];
+            st_dev(a.slots + (size_t)t * (E + 1) + r, ~__float_as_uint(v));
           }
       }
     }
     DTRACE(0, 1);
-    block_arrive(router_done);
-    DTRACE(0, 3);
     return;
   }
   // ---- the selection workgroup: one wave per token (T <= RD_WAVES) --------
   const int t = wave;
   // the MFMA-order copy of x does not depend on the routing
   if (t < T && a.xperm) write_xperm(a.x + (size_t)t * H, a.xperm, nullptr, t, H, lane);
-  block_wait_geq(router_done, a.NR, a.sync + SY_ERR);
   DTRACE(0, 1);
+  uint32_t raw[NV], graw = 0u;
   if (t < T) {
-    const float *ar = a.logits + (size_t)t * E;
+    uint32_t *sl = a.slots + (size_t)t * (E + 1);
+    // poll the token's slots until every one is written (bounded)
+    for (int it = 0;; ++it) {
+#pragma unroll
+      for (int i = 0; i < NV; ++i) raw[i] = ld_dev(sl + min(lane + 64 * i, E - 1));
+      graw = ld_dev(sl + E);  // the shared gate's slot (stays 0 without one)
+      uint32_t nz = graw | (a.gw ? 0u : 1u);
+#pragma unroll
+      for (int i = 0; i < NV; ++i) nz = min(nz, raw[i]);
+      if (__all(nz != 0u)) break;
+      if (it == SPIN_MAX) {
+        if (lane == 0) atomicOr(a.sync + SY_ERR, 1);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    DTRACE(0, 4);
     uint32_t key[NV];
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const int e = lane + 64 * i;
-      const float v = ld_dev(ar + min(e, E - 1));
-      key[i] = e < E ? ordered_key(v) : 0u;
-    }
-    const float sgl = a.gw ? ld_dev(a.sgl + t) : 0.0f;
+    for (int i = 0; i < NV; ++i) key[i] = lane + 64 * i < E ? ordered_key(__uint_as_float(~raw[i])) : 0u;
+    const float sgl = __uint_as_float(~graw);
     int seli;
     uint32_t selk;
     wave_topk_fast<NV>(key, E, k, lane, seli, selk, s_cand[wave], s_sel[wave]);
     const float selv = lane < k ? key_to_float(selk) : 0.0f;
-    const float vmax = __shfl(selv, 0, 64);
+    const float vmax = __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(selv)));
     const float p = lane < k ? expf(selv - vmax) : 0.0f;
-    float sum = 0.0f;
-    for (int j = 0; j < k; ++j) sum += __shfl(p, j, 64);
+    float sum = 0.0f;  // in pick order, as the oracle
+    for (int j = 0; j < k; ++j) sum += __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(p), j));
     if (lane < k) {
       a.idx[(size_t)t * k + lane] = seli;
       a.w[(size_t)t * k + lane] = p / sum;
@@ -307,9 +309,25 @@ __global__ __launch_bounds__(RD_WAVES * 64) void k_route_decode(RouteDecodeArgs 
   }
   DTRACE(0, 2);
   __syncthreads();
-  if (threadIdx.x == 0) *router_done = 0;  // this workgroup was its only waiter
   if (a.ds.tiles) dispatch_decode(s_idx, T, k, E, a.has_shared, a.ds);
   DTRACE(0, 3);
+  // off the critical path: the logits output, and the slots cleared for
+  // the next call
+  if (t < T) {
+    uint32_t *sl = a.slots + (size_t)t * (E + 1);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int e = lane + 64 * i;
+      if (e < E) {
+        st_dev(sl + e, 0u);
+        a.logits[(size_t)t * E + e] = __uint_as_float(~raw[i]);
+      }
+    }
+    if (a.gw && lane == 0) {
+      st_dev(sl + E, 0u);
+      a.sgl[t] = __uint_as_float(~graw);
+    }
+  }
 }
 
 struct ExpertsDecodeArgs {
@@ -322,11 +340,8 @@ struct ExpertsDecodeArgs {
   int max_tiles, cap;  // grid tiles; capacity of the per-tile counter arrays
 };
 
-// Persistent: gridDim.x workgroups (all resident: the launcher sizes the
-// grid by the occupancy) take items it, it + gridDim.x, ...  A workgroup
-// only ever waits for gate/up items of lower index, which are held by
-// resident workgroups, so the waits end.  (One item per workgroup instead
-// would be bound by the workgroup dispatch rate, about 150 per us.)
+// One item per workgroup.  A down item only ever waits for gate/up items of
+// lower index, which the dispatcher has started, so the waits end.
 // SPLIT: the gate/up items ran in an earlier launch (k_expert_lds): this
 // launch holds only the down items, which need no wait and read act with
 // plain (cacheable) loads.
@@ -347,7 +362,7 @@ __global__ __launch_bounds__(1024, DEC_WAVES_PER_SIMD) void k_experts_decode(Exp
     const int is_gu = item < n_gu;
     const int r = is_gu ? item : item - n_gu, ns = is_gu ? sg : sd;
     const int tile = r / ns, slab = r % ns;
-    if (tile >= n_tiles) DEC_NEXT;
+    if (tile >= n_tiles) return;
     DTRACE_AT(1, item, 0);
 #ifdef AINFER_DECODE_TRACE
     if (threadIdx.x == 0) g_dtrace[1][item][4] = is_gu;
@@ -358,13 +373,13 @@ __global__ __launch_bounds__(1024, DEC_WAVES_PER_SIMD) void k_experts_decode(Exp
       // x (MFMA order) comes from the routing kernel: plain, cacheable loads
       expert_lds_item<SD, KBW_GU, RG_GU, DEC_MT, 0, true, false>(a.gu, a.gu.tiles[tile],
                                                                           slab, lds);
-      if (threadIdx.x >= 64) DEC_NEXT;
+      if (threadIdx.x >= 64) return;
       // wave 0: its act stores, then the arrival
       DTRACE_AT(1, item, 2);
       wait_stores();
       if (lane == 0) atomicAdd(&gu_done[tile * SY_STRIDE], 1);
       DTRACE_AT(1, item, 3);
-      DEC_NEXT;
+      return;
     }
     const int4 td = sload_int4(a.dn.tiles + tile);
     // the down weights are requested before the wait for the tile's act rows
@@ -374,7 +389,7 @@ __global__ __launch_bounds__(1024, DEC_WAVES_PER_SIMD) void k_experts_decode(Exp
       if (!SPLIT) block_wait_geq(gdone, sg, err);
       DTRACE_AT(1, item, 1);
     });
-    if (threadIdx.x >= 64) DEC_NEXT;
+    if (threadIdx.x >= 64) return;
     DTRACE_AT(1, item, 2);
     // ---- wave 0: publish o; count this tile's down items and each token's
     // arrivals on this row slab --------------------------------------------
@@ -398,7 +413,7 @@ __global__ __launch_bounds__(1024, DEC_WAVES_PER_SIMD) void k_experts_decode(Exp
       }
     }
     DTRACE_AT(1, item, 3);
-    if (__ballot(tok >= 0) == 0ull) DEC_NEXT;
+    if (__ballot(tok >= 0) == 0ull) return;
     // ---- combine of the completed (token, slab) pairs: slot order, as
     // k_combine -------------------------------------------------------------
     const __amdgpu_buffer_rsrc_t orr = make_rsrc(a.dn.o, 0x7FFFFFFFu);
@@ -468,7 +483,8 @@ int decode_geometry(const ainfer_moe_shape &s, DecodeGeom *g) {
 hipError_t launch_route_decode(const void *x, const void *rw, const float *bias, const void *gw,
                                float *logits, float *sgl, int32_t *idx, float *w, float *sg,
                                void *xperm, int T, int H, int E, int k, int has_shared,
-                               const DispatchOut *ds, int32_t *sync, hipStream_t s) {
+                               const DispatchOut *ds, int32_t *sync, uint32_t *slots,
+                               hipStream_t s) {
   if (T <= 0) return hipSuccess;
   if (T > DECODE_MAX_T || T > RD_WAVES || E > 1024) return hipErrorInvalidValue;
   RouteDecodeArgs a;
@@ -485,6 +501,7 @@ hipError_t launch_route_decode(const void *x, const void *rw, const float *bias,
   a.xperm = (uint16_t *)xperm;
   if (ds) a.ds = *ds;
   a.sync = sync;
+  a.slots = slots;
   a.T = T;
   a.H = H;
   a.E = E;

@@ -132,10 +132,11 @@ constexpr int DECODE_MAX_T = EXACT_ROUTER_MAX_T;
 // (k_experts_decode); above it as gate/up, down and combine launches (the
 // fused items' handoffs cost more than the two launches they save)
 constexpr int FUSED_EXPERTS_MAX_T = 2;
-// sync region (int32 words at the start of the workspace, zero between calls)
-// Counters sit SY_STRIDE words (256 bytes) apart.
-enum { SY_STRIDE = 64, SY_ROUTER_DONE = 0, SY_SELECT = SY_STRIDE, SY_ERR = 2 * SY_STRIDE,
-       SY_TILES = 3 * SY_STRIDE };
+// sync region (int32 words at the start of the workspace, zero between calls):
+// the error word, the per-tile and per-(token, slab) counters of the fused
+// expert kernel, then the routing kernel's logit slots.  Counters sit
+// SY_STRIDE words (256 bytes) apart.
+enum { SY_STRIDE = 64, SY_ERR = 0, SY_TILES = SY_STRIDE };
 struct DecodeGeom {
   int nw;                  // waves per expert workgroup
   int wk_gu, wr_gu, wk_dn, wr_dn;
@@ -149,7 +150,8 @@ int decode_geometry(const ainfer_moe_shape &s, DecodeGeom *g);
 hipError_t launch_route_decode(const void *x, const void *rw, const float *bias, const void *gw,
                                float *logits, float *sgl, int32_t *idx, float *w, float *sg,
                                void *xperm, int T, int H, int E, int k, int has_shared,
-                               const DispatchOut *ds, int32_t *sync, hipStream_t s);
+                               const DispatchOut *ds, int32_t *sync, uint32_t *slots,
+                               hipStream_t s);
 // gate/up + SiLU, down and the combine (y = sum_j w_j o_j + g_s o_s (+ resid))
 hipError_t launch_experts_decode(int scale_dtype, const DecodeGeom &g, ExpertArgs gu,
                                  ExpertArgs dn, const float *w, const float *sg,

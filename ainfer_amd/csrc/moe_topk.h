@@ -88,7 +88,7 @@ __device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a >
 //     r < k is pick r.
 // More than 64 candidates (many equal logits), an absent tau or k > 16 take
 // the round-by-round path above.  Lane j < k returns pick j in seli and its
-// key in selk.  cand and sel are wave-private LDS arrays (64 and 16 entries).
+// key in selk.  cand and sel are wave-private LDS arrays (68 and 16 entries).
 template <int NV>
 __device__ __forceinline__ void wave_topk_fast(const uint32_t (&key)[NV], int E, int k, int lane,
                                                int &seli, uint32_t &selk, uint64_t *cand,
@@ -132,7 +132,14 @@ __device__ __forceinline__ void wave_topk_fast(const uint32_t (&key)[NV], int E,
   __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
   const uint64_t mine = lane < nc ? cand[lane] : 0ull;
   int rk = 0;
-  for (int j = 0; j < nc; ++j) rk += cand[j] > mine ? 1 : 0;
+  // four broadcast reads in flight per step; entries past nc are ignored
+  for (int j0 = 0; j0 < nc; j0 += 4) {
+    uint64_t v[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v[q] = cand[j0 + q];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) rk += (j0 + q < nc && v[q] > mine) ? 1 : 0;
+  }
   if (lane < nc && rk < k) sel[rk] = mine;
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");

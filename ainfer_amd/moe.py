@@ -88,6 +88,11 @@ class MoeLayer:
         L.check(L.lib().ainfer_moe_workspace_init(C.byref(self.shape), _ptr(ws), n, _stream(None)))
         return ws
 
+    def workspace_check(self, ws, stream=None) -> int:
+        """Status of the workspace's synchronisation words (OK when all zero)."""
+        return L.lib().ainfer_moe_workspace_check(C.byref(self.shape), _ptr(ws), ws.numel(),
+                                                  _stream(stream))
+
     def forward(self, x, y, ws, stream=None):
         T = x.shape[0]
         return L.check(L.lib().ainfer_moe_forward(

@@ -63,7 +63,8 @@ enum {
   AINFER_ERR_WORKSPACE = -3,  /* workspace too small or misaligned          */
   AINFER_ERR_TOKENS = -4,     /* T < 0 or above the supported maximum       */
   AINFER_ERR_HIP = -5,        /* a HIP runtime call failed                  */
-  AINFER_ERR_ARG = -6         /* another argument is out of range           */
+  AINFER_ERR_ARG = -6,        /* another argument is out of range           */
+  AINFER_ERR_SYNC = -7        /* a device-side wait ran out (decode path)   */
 };
 
 enum { AINFER_SCALE_BF16 = 0, AINFER_SCALE_FP16 = 1 };
@@ -128,6 +129,15 @@ size_t ainfer_moe_workspace_bytes(const ainfer_moe_shape *shape,
  * layer's scratch. */
 int ainfer_moe_workspace_init(const ainfer_moe_shape *shape, void *workspace,
                               size_t workspace_bytes, void *stream);
+/* Synchronise the stream and read the workspace's synchronisation words
+ * back: AINFER_OK when they are all zero, AINFER_ERR_SYNC when a bounded
+ * device-side wait ran out (its result is then not to be trusted; re-init
+ * the workspace), AINFER_ERR_WORKSPACE when other words are left non-zero
+ * (overlapping calls on one workspace).  A diagnostic, not for the hot loop;
+ * it has no counterpart in the reference, whose waits are host fences
+ * (decode_l0.cpp:484-493). */
+int ainfer_moe_workspace_check(const ainfer_moe_shape *shape, const void *workspace,
+                               size_t workspace_bytes, void *stream);
 /* The whole layer: y[T][H] (bf16) = MoE(x[T][H] bf16).
  * Replaces the reference MLP sub-sequence decode_l0.cpp:663-674
  * (xq -> gemvE gate -> gemvE up -> SiluMul -> xq -> gemvE down -> res) with

@@ -168,6 +168,26 @@ def test_forward_parity(torch, oracle, name, T):
     assert torch.equal(y.view(torch.int16), y2.view(torch.int16))
 
 
+def test_decode_sync_words_return_to_zero(torch, oracle):
+    """Every decode call leaves the workspace's counters and logit slots zero
+    and no bounded wait runs out, over all decode token counts in a row."""
+    from ainfer_amd import _lib as L
+    from ainfer_amd.moe import make_input
+    layer = get_layer(torch, "c1")
+    ws = layer.workspace(16)
+    assert layer.workspace_check(ws) == L.OK
+    y = torch.empty(16, layer.cfg.hidden, dtype=torch.bfloat16, device="cuda")
+    for rep in range(3):
+        for T in range(1, 17):
+            layer.forward(make_input(layer.cfg, T, tag=200 + T), y[:T], ws)
+    rc = layer.workspace_check(ws)
+    assert rc == L.OK, L.lib().ainfer_moe_strerror(rc).decode()
+    # the route-only entry shares the logit slots
+    x = make_input(layer.cfg, 16, tag=9)
+    layer.route(x, ws, want_logits=True)
+    assert layer.workspace_check(ws) == L.OK
+
+
 def test_prefill_zipf_parity_on_token_sample(torch, oracle):
     """c2 at full size (T = 4096): tokens are independent given routing, so
     the oracle recomputes a sample of rows; the whole output is checked for
