@@ -11,6 +11,7 @@ OK = 0
 ERR_SHAPE, ERR_NULL, ERR_WORKSPACE, ERR_TOKENS, ERR_HIP, ERR_ARG, ERR_SYNC = -1, -2, -3, -4, -5, -6, -7
 SCALE_BF16, SCALE_FP16 = 0, 1
 NORM_PLAIN, NORM_ONE_PLUS = 0, 1
+ACT_F32, ACT_BF16 = 0, 1
 FILL_BYTES, FILL_BF16_NORMAL, FILL_FP16_ABSNORMAL, FILL_BF16_ABSNORMAL = 0, 1, 2, 3
 MAX_TOKENS = 65536
 
@@ -20,6 +21,7 @@ EXPORTS = (
     "ainfer_moe_workspace_init", "ainfer_moe_workspace_check",
     "ainfer_moe_forward", "ainfer_moe_block_forward", "ainfer_moe_route",
     "ainfer_moe_dispatch", "ainfer_moe_rmsnorm", "ainfer_moe_fill",
+    "ainfer_moe_act_quant_i8", "ainfer_moe_int4_gemv_i8",
     "ainfer_moe_profile_enable", "ainfer_moe_profile_read",
 )
 N_STAGES = 7
@@ -68,6 +70,8 @@ def lib():
         L.ainfer_moe_dispatch.argtypes = [sp, P, I32, P, P, P, P, P, SZ, P]
         L.ainfer_moe_rmsnorm.argtypes = [P, P, I32, F, P, I32, I32, P]
         L.ainfer_moe_fill.argtypes = [I32, C.c_uint64, F, SZ, P, P]
+        L.ainfer_moe_act_quant_i8.argtypes = [P, I32, I32, I32, P, P, P]
+        L.ainfer_moe_int4_gemv_i8.argtypes = [P, P, I32, P, P, I32, I32, I32, P, P]
         L.ainfer_moe_profile_enable.argtypes = [I32]
         L.ainfer_moe_profile_read.argtypes = [C.POINTER(C.c_float), I32, C.POINTER(I32)]
         for name in EXPORTS:

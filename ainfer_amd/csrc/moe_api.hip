@@ -554,6 +554,33 @@ int ainfer_moe_rmsnorm(const void *x, const void *w, int32_t norm_mode, float ep
   return AINFER_OK;
 }
 
+int ainfer_moe_act_quant_i8(const void *x, int32_t x_dtype, int32_t T, int32_t K, int8_t *q,
+                            float *sq, void *stream) {
+  if (T < 0 || T > AINFER_MOE_MAX_TOKENS) return AINFER_ERR_TOKENS;
+  if (K <= 0 || K % 128) return AINFER_ERR_SHAPE;
+  if (x_dtype != AINFER_ACT_F32 && x_dtype != AINFER_ACT_BF16) return AINFER_ERR_ARG;
+  if (T == 0) return AINFER_OK;
+  if (!x || !q || !sq) return AINFER_ERR_NULL;
+  if ((uintptr_t)x % 8 || (uintptr_t)q % 2 || (uintptr_t)sq % 4) return AINFER_ERR_ARG;
+  HIP_TRY(launch_act_quant_i8(x, x_dtype, T, K, q, sq, (hipStream_t)stream));
+  return AINFER_OK;
+}
+
+int ainfer_moe_int4_gemv_i8(const uint8_t *packed, const void *scales, int32_t scale_dtype,
+                            const int8_t *q, const float *sq, int32_t M, int32_t K, int32_t T,
+                            float *y, void *stream) {
+  if (T < 0 || T > AINFER_MOE_MAX_TOKENS) return AINFER_ERR_TOKENS;
+  if (M <= 0 || K <= 0 || K % 128) return AINFER_ERR_SHAPE;
+  if (scale_dtype != AINFER_SCALE_BF16 && scale_dtype != AINFER_SCALE_FP16) return AINFER_ERR_ARG;
+  if (T == 0) return AINFER_OK;
+  if (!packed || !scales || !q || !sq || !y) return AINFER_ERR_NULL;
+  if ((uintptr_t)packed % 16 || (uintptr_t)q % 16 || (uintptr_t)scales % 2 ||
+      (uintptr_t)sq % 4 || (uintptr_t)y % 4)
+    return AINFER_ERR_ARG;
+  HIP_TRY(launch_int4_gemv_i8(packed, scales, scale_dtype, q, sq, M, K, T, y, (hipStream_t)stream));
+  return AINFER_OK;
+}
+
 int ainfer_moe_profile_enable(int32_t enable) {
   if (enable && !g_prof.created) {
     for (int i = 0; i < PROF_SLOTS; ++i)

@@ -143,6 +143,11 @@ struct DecodeGeom {
   int slabs_gu, slabs_dn;  // row slabs per tile
   size_t lds;              // dynamic LDS bytes
 };
+// W4A8 GEMV numerics (moe_w4a8.hip)
+hipError_t launch_act_quant_i8(const void *x, int x_dtype, int T, int K, int8_t *q, float *sq,
+                               hipStream_t s);
+hipError_t launch_int4_gemv_i8(const uint8_t *P, const void *S, int scale_dtype, const int8_t *xq,
+                               const float *sq, int M, int K, int T, float *y, hipStream_t s);
 // 0 when the shape has no decode geometry (the staged path is used then)
 int decode_geometry(const ainfer_moe_shape &s, DecodeGeom *g);
 // router logits + top-k + weights + shared gate + x in MFMA order, and the

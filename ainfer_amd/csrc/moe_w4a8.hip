@@ -1,0 +1,164 @@
+// moe_w4a8.hip - the reference's production GEMV numerics (W4A8) on gfx950:
+// per-group-128 int8 activation quantisation and the INT4 x int8 GEMV.
+//
+// Reference arithmetic (restated, not translated):
+//  - ScalesMax + Quantize (tools/cmdlist/kernels.cpp:551-579): per group of
+//    128, SQ = max|x| / 127 (0 -> 1), q = trunc(x/SQ +- 0.5) clamped to
+//    [-127, 127];
+//  - Int4Gemv (tools/cmdlist/kernels.cpp:148-201): per row m,
+//    y = sum over groups g in order of float(gs) * s_w[m][g] * SQ[g], with
+//    gs the exact int32 dot of the group's nibbles and int8 activations.
+//
+// gfx950 form: a wave owns 16 rows x 16 tokens and walks the groups in
+// order.  One group is one 16-byte load per lane (row l%16, k-quarter l/16)
+// and two v_mfma_i32_16x16x64_i8: the nibbles' even and odd halves, each
+// widened to bytes q+8 in [0, 15] by one xor and one and.  The activation
+// bytes are permuted with v_perm_b32 into the same k order, so A and B agree
+// on every k.  gs = D(q+8) - 8 * D(ones), exact in int32, and the float
+// rescale runs in group order with no contraction, so each y is
+// bit-identical to the reference formula.
+#include "moe_common.h"
+#include "moe_internal.h"
+
+namespace {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// one wave per (token, group of 128): two elements per lane
+template <typename XT>
+__global__ __launch_bounds__(256) void k_act_quant_i8(const XT *__restrict__ x, int T, int K,
+                                                      int8_t *__restrict__ q,
+                                                      float *__restrict__ sq) {
+  const int G = K / 128;
+  const int item = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (item >= T * G) return;
+  const int t = item / G, g = item % G;
+  const size_t base = (size_t)t * K + (size_t)g * 128 + 2 * lane;
+  float v[2];
+  if constexpr (sizeof(XT) == 4) {
+    const float2 p = *(const float2 *)(x + base);
+    v[0] = p.x;
+    v[1] = p.y;
+  } else {
+    const uint32_t p = *(const uint32_t *)(x + base);
+    v[0] = __uint_as_float(p << 16);
+    v[1] = __uint_as_float(p & 0xFFFF0000u);
+  }
+  // the reference's running max (a > m ? a : m from 0, so NaNs drop out);
+  // max is exact, so the lane-tree order does not matter
+  float m = 0.0f;
+  for (int i = 0; i < 2; ++i) {
+    const float a = fabsf(v[i]);
+    m = a > m ? a : m;
+  }
+  m = __uint_as_float(wave_max_u32(__float_as_uint(m)));
+  float s = m / 127.0f;
+  s = s == 0.0f ? 1.0f : s;
+  int8_t out[2];
+  for (int i = 0; i < 2; ++i) {
+    const float r = v[i] / s;
+    int qi = (int)(r >= 0.0f ? r + 0.5f : r - 0.5f);
+    qi = qi < -127 ? -127 : (qi > 127 ? 127 : qi);
+    out[i] = (int8_t)qi;
+  }
+  *(uint16_t *)(q + base) = (uint16_t)((uint8_t)out[0] | ((uint16_t)(uint8_t)out[1] << 8));
+  if (lane == 0) sq[(size_t)t * G + g] = s;
+}
+
+__device__ __forceinline__ i32x4 mfma_i8(i32x4 a, i32x4 b, i32x4 c) {
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+// grid (ceil(M / 64), ceil(T / 16)), 256 threads: wave w owns rows
+// [64 * bx + 16 * w, +16) and tokens [16 * by, +16).  y is [T][M] fp32.
+template <int SD>
+__global__ __launch_bounds__(256) void k_int4_gemv_i8(const uint8_t *__restrict__ P,
+                                                      const uint16_t *__restrict__ S,
+                                                      const int8_t *__restrict__ xq,
+                                                      const float *__restrict__ sq, int M,
+                                                      int K, int T, float *__restrict__ y) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int m0 = blockIdx.x * 64 + wave * 16;
+  if (m0 >= M) return;
+  const int t0 = blockIdx.y * 16;
+  const int G = K / 128, qd = lane >> 4, c = lane & 15;
+  // A operand: row m0 + c; B operand and D column: token t0 + c
+  const uint8_t *wp = P + (size_t)min(m0 + c, M - 1) * (K / 2) + qd * 16;
+  const int tb = min(t0 + c, T - 1);
+  const int8_t *xp = xq + (size_t)tb * K + qd * 32;
+  const float *sqp = sq + (size_t)tb * G;
+  // D rows of this lane: m0 + 4 * qd + i
+  const uint16_t *sp[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) sp[i] = S + (size_t)min(m0 + 4 * qd + i, M - 1) * G;
+  const i32x4 ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
+  const i32x4 zero = {0, 0, 0, 0};
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 4
+  for (int g = 0; g < G; ++g) {
+    const u32x4 w = __builtin_nontemporal_load((const u32x4 *)(wp + (size_t)g * 64));
+    const u32x4 xa = *(const u32x4 *)(xp + (size_t)g * 128);
+    const u32x4 xb = *(const u32x4 *)(xp + (size_t)g * 128 + 16);
+    float sc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sc[i] = scale_to_f32<SD>(sp[i][g]);
+    const float sqg = sqp[g];
+    i32x4 a0, a1, b0, b1;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t u = w[j] ^ 0x88888888u;  // nibble q -> q + 8
+      a0[j] = (int)(u & 0x0F0F0F0Fu);         // k = 8j + {0, 2, 4, 6}
+      a1[j] = (int)((u >> 4) & 0x0F0F0F0Fu);  // k = 8j + {1, 3, 5, 7}
+    }
+    b0[0] = (int)__builtin_amdgcn_perm(xa[1], xa[0], 0x06040200u);
+    b0[1] = (int)__builtin_amdgcn_perm(xa[3], xa[2], 0x06040200u);
+    b0[2] = (int)__builtin_amdgcn_perm(xb[1], xb[0], 0x06040200u);
+    b0[3] = (int)__builtin_amdgcn_perm(xb[3], xb[2], 0x06040200u);
+    b1[0] = (int)__builtin_amdgcn_perm(xa[1], xa[0], 0x07050301u);
+    b1[1] = (int)__builtin_amdgcn_perm(xa[3], xa[2], 0x07050301u);
+    b1[2] = (int)__builtin_amdgcn_perm(xb[1], xb[0], 0x07050301u);
+    b1[3] = (int)__builtin_amdgcn_perm(xb[3], xb[2], 0x07050301u);
+    i32x4 d = mfma_i8(a0, b0, zero);
+    d = mfma_i8(a1, b1, d);
+    i32x4 sx = mfma_i8(ones, b0, zero);
+    sx = mfma_i8(ones, b1, sx);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma clang fp contract(off)
+      const int gs = d[i] - 8 * sx[i];
+      acc[i] = acc[i] + (float)gs * sc[i] * sqg;  // the reference's statement, unfused
+    }
+  }
+  const int t = t0 + c;
+  if (t >= T) return;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int m = m0 + 4 * qd + i;
+    if (m < M) y[(size_t)t * M + m] = acc[i];
+  }
+}
+
+}  // namespace
+
+hipError_t launch_act_quant_i8(const void *x, int x_dtype, int T, int K, int8_t *q, float *sq,
+                               hipStream_t s) {
+  const int items = T * (K / 128);
+  const unsigned grid = (items + 3) / 4;
+  if (x_dtype == AINFER_ACT_F32)
+    k_act_quant_i8<float><<<grid, 256, 0, s>>>((const float *)x, T, K, q, sq);
+  else
+    k_act_quant_i8<uint16_t><<<grid, 256, 0, s>>>((const uint16_t *)x, T, K, q, sq);
+  return hipGetLastError();
+}
+
+hipError_t launch_int4_gemv_i8(const uint8_t *P, const void *S, int scale_dtype, const int8_t *xq,
+                               const float *sq, int M, int K, int T, float *y, hipStream_t s) {
+  const dim3 grid((M + 63) / 64, (T + 15) / 16);
+  if (scale_dtype == AINFER_SCALE_FP16)
+    k_int4_gemv_i8<AINFER_SCALE_FP16>
+        <<<grid, 256, 0, s>>>(P, (const uint16_t *)S, xq, sq, M, K, T, y);
+  else
+    k_int4_gemv_i8<AINFER_SCALE_BF16>
+        <<<grid, 256, 0, s>>>(P, (const uint16_t *)S, xq, sq, M, K, T, y);
+  return hipGetLastError();
+}

@@ -182,6 +182,36 @@ int ainfer_moe_dispatch(const ainfer_moe_shape *shape,
 int ainfer_moe_rmsnorm(const void *x, const void *w, int32_t norm_mode,
                        float eps, void *y, int32_t T, int32_t H, void *stream);
 
+/* ---- W4A8: the reference's production GEMV numerics ---------------------
+ * Activations quantised per group of 128 to int8, INT4 weights, int32 group
+ * dots, fp32 rescale in group order.  These two entries are the operator
+ * surface of the reference's decode GEMV stage; the MoE layer entries above
+ * keep bf16 activations (W4A16). */
+enum { AINFER_ACT_F32 = 0, AINFER_ACT_BF16 = 1 };
+
+/* Per-group int8 quantisation of x[T][K] (fp32 or bf16, K % 128 == 0):
+ * sq[t][g] = max|x| / 127 over the group (1 when that is 0) and
+ * q[t][k] = (int)(x/sq + 0.5) for x/sq >= 0, (int)(x/sq - 0.5) otherwise,
+ * clamped to [-127, 127] (round half away from zero).  NaN inputs give
+ * unspecified codes.  x 8-byte aligned, q 2-byte aligned.
+ * Replaces ScalesMax + Quantize, tools/cmdlist/kernels.cpp:551-579
+ * (launched per vector by decode_l0.cpp:505-515). */
+int ainfer_moe_act_quant_i8(const void *x, int32_t x_dtype, int32_t T, int32_t K,
+                            int8_t *q, float *sq, void *stream);
+
+/* INT4 x int8 GEMV: y[t][m] (fp32) = sum over g = 0..K/128-1, in order, of
+ * float(gs) * s[m][g] * sq[t][g], gs = sum_j w[m][128g+j] * q[t][128g+j]
+ * exact in int32; products and sums rounded to fp32 one at a time (no fused
+ * multiply-add), so y is bit-identical to that formula.  packed [M][K/2]
+ * (low nibble = even k), scales [M][K/128] (AINFER_SCALE_BF16 as the
+ * reference, or FP16), q [T][K], sq [T][K/128].  packed, q 16-byte aligned.
+ * Replaces Int4Gemv(float* Y, const u8* P, const u16* S, const i8* XQ,
+ * const float* SQ, int K), tools/cmdlist/kernels.cpp:148-201, bound by
+ * decode_l0.cpp:494-504 (one launch per token there; T tokens here). */
+int ainfer_moe_int4_gemv_i8(const uint8_t *packed, const void *scales,
+                            int32_t scale_dtype, const int8_t *q, const float *sq,
+                            int32_t M, int32_t K, int32_t T, float *y, void *stream);
+
 /* ---- synthetic data (counter-based, bit-identical to the CPU oracle) --- */
 enum {
   AINFER_FILL_BYTES = 0,      /* uniform random bytes (packed int4 weights)  */

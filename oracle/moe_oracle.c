@@ -161,6 +161,101 @@ void mo_quantize_int4(const float *w, int rows, int K, uint8_t *packed,
 /* ------------------------------------------------------------------------ */
 /* pointwise                                                                 */
 /* ------------------------------------------------------------------------ */
+/* W4A8: the reference's production GEMV numerics                           */
+/* ------------------------------------------------------------------------ */
+/* ScalesMax + Quantize, tools/cmdlist/kernels.cpp:551-579 (host form
+ * tools/cmdlist/gemv_replay.cpp:193-204): per group of 128, m = running max
+ * of |x| (a > m ? a : m from 0), sq = m / 127 (0 -> 1), q = (int)(v + 0.5)
+ * for v = x/sq >= 0 else (int)(v - 0.5), clamped to [-127, 127].  x is fp32
+ * (x_bf16 NULL) or bf16. */
+void mo_act_quant_i8(const float *x, const uint16_t *x_bf16, int T, int K, int8_t *q,
+                     float *sq) {
+  int G = K / 128;
+  for (int t = 0; t < T; ++t)
+    for (int g = 0; g < G; ++g) {
+      size_t b = (size_t)t * K + (size_t)g * 128;
+      float v[128];
+      for (int j = 0; j < 128; ++j) v[j] = x ? x[b + j] : mo_bf16_to_f32(x_bf16[b + j]);
+      float m = 0.f;
+      for (int j = 0; j < 128; ++j) {
+        float a = fabsf(v[j]);
+        m = a > m ? a : m;
+      }
+      float s = m / 127.0f;
+      if (s == 0.f) s = 1.0f;
+      sq[(size_t)t * G + g] = s;
+      for (int j = 0; j < 128; ++j) {
+        float r = v[j] / s;
+        int qi = (int)(r >= 0 ? r + 0.5f : r - 0.5f);
+        q[b + j] = (int8_t)(qi < -127 ? -127 : (qi > 127 ? 127 : qi));
+      }
+    }
+}
+
+/* The reference GEMV test's own inputs, tools/cmdlist/gemv_replay.cpp:158-192
+ * (the test generator, restated): one 64-bit LCG stream; weights drawn row
+ * by row, group by group, quantised with scale amax/7 (0 -> 1, stored as
+ * bf16, the unrounded fp32 scale used for the division) and lrint (half to
+ * even) clamped to [-8, 7]; then n_vec activation vectors of K draws x 50. */
+void mo_ref_gemv_inputs(int M, int K, int n_vec, uint8_t *packed, uint16_t *scales_bf16,
+                        float *x) {
+  uint64_t s = 0x9E3779B9ull;
+  const float unit = 0.02f / 32768.0f;
+#define MO_RND() (s = s * 6364136223846793005ull + 1442695040888963407ull, \
+                  (float)((int)((s >> 33) & 0xFFFF) - 32768) * unit)
+  int G = K / 128;
+  memset(packed, 0, (size_t)M * K / 2);
+  for (int m = 0; m < M; ++m)
+    for (int g = 0; g < G; ++g) {
+      float w[128], amax = 0.f;
+      for (int j = 0; j < 128; ++j) {
+        w[j] = MO_RND();
+        amax = fmaxf(amax, fabsf(w[j]));
+      }
+      float sc = amax == 0.f ? 1.0f : amax / 7.0f;
+      scales_bf16[(size_t)m * G + g] = mo_f32_to_bf16(sc);
+      for (int j = 0; j < 128; ++j) {
+        int q = (int)lrintf(w[j] / sc);
+        q = q < -8 ? -8 : (q > 7 ? 7 : q);
+        size_t idx = (size_t)m * K + (size_t)g * 128 + j;
+        if (j & 1)
+          packed[idx / 2] |= (uint8_t)((q & 0xF) << 4);
+        else
+          packed[idx / 2] = (uint8_t)(q & 0xF);
+      }
+    }
+  for (size_t i = 0; i < (size_t)n_vec * K; ++i) x[i] = MO_RND() * 50.0f;
+#undef MO_RND
+}
+
+/* Int4Gemv, tools/cmdlist/kernels.cpp:148-201 (host mirror
+ * tools/cmdlist/gemv_replay.cpp:205-221): y[t][m] = sum over groups in
+ * order of (float)gs * sc * sq[t][g], gs the int32 dot of the group's
+ * nibbles (low nibble = even k, nibble >= 8 -> -16) and int8 activations.
+ * Built with -ffp-contract=off, so each product and sum rounds to fp32. */
+void mo_int4_gemv_i8(const uint8_t *packed, const void *scales, int scale_dtype,
+                     const int8_t *q, const float *sq, int M, int K, int T, float *y) {
+  int G = K / 128;
+  for (int t = 0; t < T; ++t)
+    for (int m = 0; m < M; ++m) {
+      float acc = 0.f;
+      for (int g = 0; g < G; ++g) {
+        float sc = scale_at(scales, scale_dtype, (size_t)m * G + g);
+        int gs = 0;
+        for (int j = 0; j < 128; ++j) {
+          size_t k = (size_t)g * 128 + j;
+          uint8_t b = packed[((size_t)m * K + k) >> 1];
+          int nib = (k & 1) ? (b >> 4) : (b & 0xF);
+          if (nib >= 8) nib -= 16;
+          gs += nib * (int)q[(size_t)t * K + k];
+        }
+        acc += (float)gs * sc * sq[(size_t)t * G + g];
+      }
+      y[(size_t)t * M + m] = acc;
+    }
+}
+
+/* ------------------------------------------------------------------------ */
 /* SiluMul, tools/cmdlist/kernels.cpp:29-37 (z = g/(1+exp(-g)) * u), as the
  * fp64 CPU form of tools/forward/fwd_oracle.py:307. */
 void mo_silu_mul(const double *g, const double *u, double *out, int n) {

@@ -28,6 +28,13 @@
  *   mo_forward          dense fp64 recomputation on tiny shapes (all
  *                       experts evaluated, combine by explicit weights)
  *   mo_fill             closed-form moments; byte-level golden values
+ *   mo_act_quant_i8     numpy float32 restatement; hand-derived golden
+ *                       (zero group -> scale 1, exact halves away from 0,
+ *                       the group max -> +-127)
+ *   mo_int4_gemv_i8     group dots against an int64 numpy matmul of the
+ *                       unpacked nibbles; the float32 group-order rescale
+ *                       restated in numpy (bit-exact); fp64 dequantised dot
+ *                       within the fp32 rounding bound
  */
 #ifndef MOE_ORACLE_H
 #define MOE_ORACLE_H
@@ -56,6 +63,14 @@ void mo_dequant_int4(const uint8_t *packed, const void *scales, int scale_dtype,
                      int rows, int K, float *out);
 void mo_quantize_int4(const float *w, int rows, int K, uint8_t *packed,
                       uint16_t *scales_bf16);
+
+/* W4A8 GEMV numerics */
+void mo_act_quant_i8(const float *x, const uint16_t *x_bf16, int T, int K, int8_t *q,
+                     float *sq);
+void mo_int4_gemv_i8(const uint8_t *packed, const void *scales, int scale_dtype,
+                     const int8_t *q, const float *sq, int M, int K, int T, float *y);
+void mo_ref_gemv_inputs(int M, int K, int n_vec, uint8_t *packed, uint16_t *scales_bf16,
+                        float *x);
 
 /* pointwise */
 void mo_silu_mul(const double *g, const double *u, double *out, int n);

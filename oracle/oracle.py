@@ -72,6 +72,9 @@ def lib():
         L.mo_forward.argtypes = [P, P, P, I, P, P, I]
         L.mo_block_forward.argtypes = [P, P, P, I, F, P, P, I, I]
         L.mo_forward_dense.argtypes = [P, P, P, I, P, P, P, P]
+        L.mo_act_quant_i8.argtypes = [P, P, I, I, P, P]
+        L.mo_int4_gemv_i8.argtypes = [P, P, I, P, P, I, I, I, P]
+        L.mo_ref_gemv_inputs.argtypes = [I, I, I, P, P, P]
         _lib = L
     return _lib
 
@@ -240,6 +243,39 @@ def quantize(w):
     scales = np.zeros(rows * K // 128, np.uint16)
     lib().mo_quantize_int4(ptr(w), rows, K, ptr(packed), ptr(scales))
     return packed, scales
+
+
+def act_quant_i8(x: np.ndarray):
+    """x [T][K] float32 or bf16 bits (uint16) -> (q int8 [T][K], sq float32 [T][K/128])."""
+    T, K = x.shape
+    q = np.empty((T, K), np.int8)
+    sq = np.empty((T, K // 128), np.float32)
+    if x.dtype == np.uint16:
+        lib().mo_act_quant_i8(None, ptr(np.ascontiguousarray(x)), T, K, ptr(q), ptr(sq))
+    else:
+        lib().mo_act_quant_i8(ptr(np.ascontiguousarray(x, np.float32)), None, T, K, ptr(q), ptr(sq))
+    return q, sq
+
+
+def int4_gemv_i8(packed, scales, scale_dtype, q, sq, M, K):
+    """y [T][M] float32 of the reference's Int4Gemv arithmetic."""
+    T = q.shape[0]
+    y = np.empty((T, M), np.float32)
+    lib().mo_int4_gemv_i8(ptr(np.ascontiguousarray(packed, np.uint8)),
+                          ptr(np.ascontiguousarray(scales, np.uint16)), scale_dtype,
+                          ptr(np.ascontiguousarray(q, np.int8)),
+                          ptr(np.ascontiguousarray(sq, np.float32)), M, K, T, ptr(y))
+    return y
+
+
+def ref_gemv_inputs(M, K, n_vec):
+    """The reference GEMV test's inputs (gemv_replay.cpp:158-192 generator):
+    packed [M][K/2], bf16 scales [M][K/128], x [n_vec][K] float32."""
+    packed = np.empty(M * K // 2, np.uint8)
+    scales = np.empty(M * K // 128, np.uint16)
+    x = np.empty((n_vec, K), np.float32)
+    lib().mo_ref_gemv_inputs(M, K, n_vec, ptr(packed), ptr(scales), ptr(x))
+    return packed, scales, x
 
 
 _ref = None

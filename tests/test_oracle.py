@@ -248,3 +248,116 @@ def test_block_forward_is_norm_then_moe_plus_residual(oracle):
     y = hl.forward(h, T)
     want = oracle.f32_to_bf16(oracle.bf16_to_f32(r) + y)
     assert np.array_equal(out, want)
+
+
+# ------------------------------------------------------------ W4A8 GEMV ----
+def _np_act_quant(x):
+    """ScalesMax + Quantize (kernels.cpp:551-579) restated in numpy float32."""
+    x = x.astype(np.float32)
+    T, K = x.shape
+    g = x.reshape(T, K // 128, 128)
+    m = np.abs(g).max(axis=2)
+    s = (m / np.float32(127.0)).astype(np.float32)
+    s[s == 0] = np.float32(1.0)
+    r = (g / s[..., None]).astype(np.float32)
+    v = np.where(r >= 0, r + np.float32(0.5), r - np.float32(0.5)).astype(np.float32)
+    q = np.clip(np.trunc(v), -127, 127).astype(np.int8)
+    return q.reshape(T, K), s
+
+
+def _unpack(packed, M, K):
+    b = np.asarray(packed, np.uint8).reshape(M, K // 2)
+    n = np.empty((M, K), np.int64)
+    n[:, 0::2] = b & 0xF
+    n[:, 1::2] = b >> 4
+    return np.where(n >= 8, n - 16, n)
+
+
+def _np_gemv_i8(packed, scales_f32, q, sq, M, K):
+    """Int4Gemv: int64 group dots by matmul, then the float32 group-order
+    rescale one rounding at a time."""
+    G = K // 128
+    w = _unpack(packed, M, K).reshape(M, G, 128)
+    T = q.shape[0]
+    xq = q.astype(np.int64).reshape(T, G, 128)
+    gs = np.einsum("mgj,tgj->tmg", w, xq)                      # exact
+    acc = np.zeros((T, M), np.float32)
+    sc = scales_f32.reshape(M, G).astype(np.float32)
+    for g in range(G):
+        term = (gs[:, :, g].astype(np.float32) * sc[None, :, g]).astype(np.float32)
+        term = (term * sq[:, g][:, None]).astype(np.float32)
+        acc = (acc + term).astype(np.float32)
+    return acc, gs
+
+
+def test_act_quant_hand_golden(oracle):
+    x = np.zeros((2, 256), np.float32)
+    # group 0: max 254 -> scale exactly 2; halves go away from zero
+    x[0, :8] = [254, 127, -127, 1, -1, 0.5 * 2, -0.5 * 2, 3]
+    # group 1 of row 0 and row 1 group 0: all zero -> scale 1, codes 0
+    x[1, 128:131] = [-7, 7, 0.25]
+    q, sq = oracle.act_quant_i8(x)
+    assert sq[0, 0] == 2.0 and sq[0, 1] == 1.0 and sq[1, 0] == 1.0
+    assert list(q[0, :8]) == [127, 64, -64, 1, -1, 1, -1, 2]
+    assert not q[0, 8:].any() and not q[1, :128].any()
+    assert sq[1, 1] == np.float32(7) / np.float32(127)
+    assert list(q[1, 128:131]) == [-127, 127, 5]   # 0.25 / (7/127) = 4.5357 -> 5
+
+
+def test_act_quant_matches_numpy_restatement(oracle):
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal((7, 1024)) * rng.choice([1e-3, 1, 50, 3e4], (7, 1))).astype(np.float32)
+    x[3, 256:384] = 0
+    q, sq = oracle.act_quant_i8(x)
+    q2, sq2 = _np_act_quant(x)
+    assert np.array_equal(sq, sq2) and np.array_equal(q, q2)
+    # bf16 input form = fp32 form on the widened values
+    xb = oracle.f32_to_bf16(x)
+    qb, sqb = oracle.act_quant_i8(xb)
+    qw, sqw = oracle.act_quant_i8(oracle.bf16_to_f32(xb))
+    assert np.array_equal(qb, qw) and np.array_equal(sqb, sqw)
+
+
+@pytest.mark.parametrize("sdt", [0, 1])
+def test_int4_gemv_i8_matches_numpy_and_fp64(oracle, sdt):
+    rng = np.random.default_rng(11 + sdt)
+    M, K, T = 48, 512, 3
+    packed = rng.integers(0, 256, M * K // 2, dtype=np.uint8)
+    sf = np.abs(rng.standard_normal(M * K // 128) * 0.02).astype(np.float32)
+    scales = oracle.f32_to_bf16(sf) if sdt == 0 else sf.astype(np.float16).view(np.uint16)
+    sc_f32 = oracle.bf16_to_f32(scales) if sdt == 0 else scales.view(np.float16).astype(np.float32)
+    x = (rng.standard_normal((T, K)) * 3).astype(np.float32)
+    q, sq = oracle.act_quant_i8(x)
+    y = oracle.int4_gemv_i8(packed, scales, sdt, q, sq, M, K)
+    want, gs = _np_gemv_i8(packed, sc_f32, q, sq, M, K)
+    assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
+    # closed form: the fp64 dot of the dequantised weights with q*sq
+    wdq = oracle.dequant(packed, scales, sdt, M, K).astype(np.float64)
+    xdq = (q.astype(np.float64).reshape(T, K // 128, 128) * sq[..., None]).reshape(T, K)
+    ref = xdq @ wdq.T
+    bound = 1e-6 * np.abs(wdq) @ np.abs(xdq).T + 1e-30
+    assert (np.abs(y - ref) <= 8 * K // 128 * bound.T.max() + 1e-6 * np.abs(ref)).all()
+
+
+def test_ref_gemv_inputs_follow_the_reference_quantiser(oracle):
+    """The reference GEMV test's generator (gemv_replay.cpp:158-192): codes in
+    [-8, 7], each group's largest |w| mapped to +-7, bf16 scales of amax/7."""
+    M, K = 8, 256
+    packed, scales, x = oracle.ref_gemv_inputs(M, K, 2)
+    w = _unpack(packed, M, K).reshape(M, K // 128, 128)
+    assert w.min() >= -8 and w.max() <= 7
+    assert (np.abs(w).max(axis=2) == 7).all()
+    sc = oracle.bf16_to_f32(scales)
+    assert (sc > 0).all() and (sc <= np.float32(0.02 / 7 * 1.01)).all()
+    assert np.abs(x).max() <= 1.0 + 1e-6 and x.std() > 0.3
+    # the first group recomputed from the LCG in Python integers
+    st, draws = 0x9E3779B9, []
+    unit = np.float32(np.float32(0.02) / np.float32(32768.0))
+    for _ in range(128):
+        st = (st * 6364136223846793005 + 1442695040888963407) % (1 << 64)
+        draws.append(np.float32(((st >> 33) & 0xFFFF) - 32768) * unit)
+    wf = np.array(draws, np.float32)
+    sc0 = np.float32(np.abs(wf).max() / np.float32(7.0))
+    assert scales[0] == oracle.f32_to_bf16(np.array([sc0]))[0]
+    q0 = np.clip(np.rint((wf / sc0).astype(np.float32)), -8, 7).astype(np.int64)
+    assert np.array_equal(w[0, 0], q0)
