@@ -9,14 +9,15 @@
 //    y = sum over groups g in order of float(gs) * s_w[m][g] * SQ[g], with
 //    gs the exact int32 dot of the group's nibbles and int8 activations.
 //
-// gfx950 form: a wave owns 16 rows x 16 tokens and walks the groups in
-// order.  One group is one 16-byte load per lane (row l%16, k-quarter l/16)
+// gfx950 form: a block owns 16 rows x 16 tokens, its waves split the
+// groups.  One group is one 16-byte load per lane (row l%16, k-quarter l/16)
 // and two v_mfma_i32_16x16x64_i8: the nibbles' even and odd halves, each
 // widened to bytes q+8 in [0, 15] by one xor and one and.  The activation
 // bytes are permuted with v_perm_b32 into the same k order, so A and B agree
-// on every k.  gs = D(q+8) - 8 * D(ones), exact in int32, and the float
-// rescale runs in group order with no contraction, so each y is
-// bit-identical to the reference formula.
+// on every k.  gs = D(q+8) - 8 * D(ones), exact in int32; each group's term
+// float(gs) * s * sq is rounded as the reference rounds it, and the terms
+// are added in group order with no contraction, so each y is bit-identical
+// to the reference formula.
 #include "moe_common.h"
 #include "moe_internal.h"
 
@@ -69,18 +70,27 @@ __device__ __forceinline__ i32x4 mfma_i8(i32x4 a, i32x4 b, i32x4 c) {
   return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 }
 
-// grid (ceil(M / 64), ceil(T / 16)), 256 threads: wave w owns rows
-// [64 * bx + 16 * w, +16) and tokens [16 * by, +16).  y is [T][M] fp32.
+#ifndef GV_WAVES
+#define GV_WAVES 4  // waves per GEMV block, split over the groups
+#endif
+#ifndef GV_GPW
+#define GV_GPW 2  // groups per wave per pass, loads issued together
+#endif
+constexpr int GV_CHUNK = GV_WAVES * GV_GPW;  // groups whose terms one LDS pass holds
+static_assert(GV_WAVES >= 4, "the ordered sum uses one thread per (row, token) of a 16 x 16 tile");
+
+// grid (ceil(M / 16), ceil(T / 16)), GV_WAVES waves: the block owns rows
+// [16 * bx, +16) and tokens [16 * by, +16).  Wave w computes the terms
+// float(gs) * s * sq of groups w, w + GV_WAVES, ... of each chunk into LDS;
+// then 256 threads, one per (row, token), add them in group order.  y is
+// [T][M] fp32.
 template <int SD>
-__global__ __launch_bounds__(256) void k_int4_gemv_i8(const uint8_t *__restrict__ P,
-                                                      const uint16_t *__restrict__ S,
-                                                      const int8_t *__restrict__ xq,
-                                                      const float *__restrict__ sq, int M,
-                                                      int K, int T, float *__restrict__ y) {
+__global__ __launch_bounds__(GV_WAVES * 64) void k_int4_gemv_i8(
+    const uint8_t *__restrict__ P, const uint16_t *__restrict__ S, const int8_t *__restrict__ xq,
+    const float *__restrict__ sq, int M, int K, int T, float *__restrict__ y) {
+  __shared__ float term[GV_CHUNK][256];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int m0 = blockIdx.x * 64 + wave * 16;
-  if (m0 >= M) return;
-  const int t0 = blockIdx.y * 16;
+  const int m0 = blockIdx.x * 16, t0 = blockIdx.y * 16;
   const int G = K / 128, qd = lane >> 4, c = lane & 15;
   // A operand: row m0 + c; B operand and D column: token t0 + c
   const uint8_t *wp = P + (size_t)min(m0 + c, M - 1) * (K / 2) + qd * 16;
@@ -93,49 +103,72 @@ __global__ __launch_bounds__(256) void k_int4_gemv_i8(const uint8_t *__restrict_
   for (int i = 0; i < 4; ++i) sp[i] = S + (size_t)min(m0 + 4 * qd + i, M - 1) * G;
   const i32x4 ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
   const i32x4 zero = {0, 0, 0, 0};
-  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 4
-  for (int g = 0; g < G; ++g) {
-    const u32x4 w = __builtin_nontemporal_load((const u32x4 *)(wp + (size_t)g * 64));
-    const u32x4 xa = *(const u32x4 *)(xp + (size_t)g * 128);
-    const u32x4 xb = *(const u32x4 *)(xp + (size_t)g * 128 + 16);
-    float sc[4];
+  float acc = 0.0f;
+  for (int c0 = 0; c0 < G; c0 += GV_CHUNK) {
+    const int cn = min(GV_CHUNK, G - c0);
+    // every load of the pass first (clamped to the last group; the terms
+    // past the chunk are not stored)
+    u32x4 wv[GV_GPW], xav[GV_GPW], xbv[GV_GPW];
+    uint16_t scv[GV_GPW][4];
+    float sqv[GV_GPW];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) sc[i] = scale_to_f32<SD>(sp[i][g]);
-    const float sqg = sqp[g];
-    i32x4 a0, a1, b0, b1;
+    for (int jj = 0; jj < GV_GPW; ++jj) {
+      const int g = c0 + min(wave + jj * GV_WAVES, cn - 1);
+      wv[jj] = __builtin_nontemporal_load((const u32x4 *)(wp + (size_t)g * 64));
+      xav[jj] = *(const u32x4 *)(xp + (size_t)g * 128);
+      xbv[jj] = *(const u32x4 *)(xp + (size_t)g * 128 + 16);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t u = w[j] ^ 0x88888888u;  // nibble q -> q + 8
-      a0[j] = (int)(u & 0x0F0F0F0Fu);         // k = 8j + {0, 2, 4, 6}
-      a1[j] = (int)((u >> 4) & 0x0F0F0F0Fu);  // k = 8j + {1, 3, 5, 7}
+      for (int i = 0; i < 4; ++i) scv[jj][i] = sp[i][g];
+      sqv[jj] = sqp[g];
     }
-    b0[0] = (int)__builtin_amdgcn_perm(xa[1], xa[0], 0x06040200u);
-    b0[1] = (int)__builtin_amdgcn_perm(xa[3], xa[2], 0x06040200u);
-    b0[2] = (int)__builtin_amdgcn_perm(xb[1], xb[0], 0x06040200u);
-    b0[3] = (int)__builtin_amdgcn_perm(xb[3], xb[2], 0x06040200u);
-    b1[0] = (int)__builtin_amdgcn_perm(xa[1], xa[0], 0x07050301u);
-    b1[1] = (int)__builtin_amdgcn_perm(xa[3], xa[2], 0x07050301u);
-    b1[2] = (int)__builtin_amdgcn_perm(xb[1], xb[0], 0x07050301u);
-    b1[3] = (int)__builtin_amdgcn_perm(xb[3], xb[2], 0x07050301u);
-    i32x4 d = mfma_i8(a0, b0, zero);
-    d = mfma_i8(a1, b1, d);
-    i32x4 sx = mfma_i8(ones, b0, zero);
-    sx = mfma_i8(ones, b1, sx);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int jj = 0; jj < GV_GPW; ++jj) {
+      const int j = wave + jj * GV_WAVES;
+      const u32x4 w = wv[jj], xa = xav[jj], xb = xbv[jj];
+      float sc[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sc[i] = scale_to_f32<SD>(scv[jj][i]);
+      const float sqg = sqv[jj];
+      i32x4 a0, a1, b0, b1;
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const uint32_t u = w[jj] ^ 0x88888888u;  // nibble q -> q + 8
+        a0[jj] = (int)(u & 0x0F0F0F0Fu);         // k = 8jj + {0, 2, 4, 6}
+        a1[jj] = (int)((u >> 4) & 0x0F0F0F0Fu);  // k = 8jj + {1, 3, 5, 7}
+      }
+      b0[0] = (int)__builtin_amdgcn_perm(xa[1], xa[0], 0x06040200u);
+      b0[1] = (int)__builtin_amdgcn_perm(xa[3], xa[2], 0x06040200u);
+      b0[2] = (int)__builtin_amdgcn_perm(xb[1], xb[0], 0x06040200u);
+      b0[3] = (int)__builtin_amdgcn_perm(xb[3], xb[2], 0x06040200u);
+      b1[0] = (int)__builtin_amdgcn_perm(xa[1], xa[0], 0x07050301u);
+      b1[1] = (int)__builtin_amdgcn_perm(xa[3], xa[2], 0x07050301u);
+      b1[2] = (int)__builtin_amdgcn_perm(xb[1], xb[0], 0x07050301u);
+      b1[3] = (int)__builtin_amdgcn_perm(xb[3], xb[2], 0x07050301u);
+      i32x4 d = mfma_i8(a0, b0, zero);
+      d = mfma_i8(a1, b1, d);
+      i32x4 sx = mfma_i8(ones, b0, zero);
+      sx = mfma_i8(ones, b1, sx);
+      f32x4 tv;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
 #pragma clang fp contract(off)
-      const int gs = d[i] - 8 * sx[i];
-      acc[i] = acc[i] + (float)gs * sc[i] * sqg;  // the reference's statement, unfused
+        const int gs = d[i] - 8 * sx[i];
+        tv[i] = (float)gs * sc[i] * sqg;  // the reference's product, unfused
+      }
+      if (j < cn) *(f32x4 *)&term[j][lane * 4] = tv;
     }
+    __syncthreads();
+    {
+#pragma clang fp contract(off)
+      for (int j = 0; j < cn; ++j) acc = acc + term[j][threadIdx.x];  // group order
+    }
+    __syncthreads();
   }
-  const int t = t0 + c;
-  if (t >= T) return;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int m = m0 + 4 * qd + i;
-    if (m < M) y[(size_t)t * M + m] = acc[i];
-  }
+  // element e = lane' * 4 + i of the producing lane': row 4 * (lane' / 16) + i,
+  // token lane' % 16
+  const int lp = threadIdx.x >> 2, i = threadIdx.x & 3;
+  const int m = m0 + 4 * (lp >> 4) + i, t = t0 + (lp & 15);
+  if (m < M && t < T) y[(size_t)t * M + m] = acc;
 }
 
 }  // namespace
@@ -153,12 +186,12 @@ hipError_t launch_act_quant_i8(const void *x, int x_dtype, int T, int K, int8_t 
 
 hipError_t launch_int4_gemv_i8(const uint8_t *P, const void *S, int scale_dtype, const int8_t *xq,
                                const float *sq, int M, int K, int T, float *y, hipStream_t s) {
-  const dim3 grid((M + 63) / 64, (T + 15) / 16);
+  const dim3 grid((M + 15) / 16, (T + 15) / 16);
   if (scale_dtype == AINFER_SCALE_FP16)
     k_int4_gemv_i8<AINFER_SCALE_FP16>
-        <<<grid, 256, 0, s>>>(P, (const uint16_t *)S, xq, sq, M, K, T, y);
+        <<<grid, GV_WAVES * 64, 0, s>>>(P, (const uint16_t *)S, xq, sq, M, K, T, y);
   else
     k_int4_gemv_i8<AINFER_SCALE_BF16>
-        <<<grid, 256, 0, s>>>(P, (const uint16_t *)S, xq, sq, M, K, T, y);
+        <<<grid, GV_WAVES * 64, 0, s>>>(P, (const uint16_t *)S, xq, sq, M, K, T, y);
   return hipGetLastError();
 }

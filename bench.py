@@ -134,6 +134,55 @@ def run_prefill(layer, cfg, T, steps, warmup, stream):
     return ms, stages, U
 
 
+def run_gemv_w4a8(steps, copies=8, M=17408, K=5120):
+    """The reference's headline GEMV shape (tools/cmdlist/gemv_replay.cpp:57)
+    in its W4A8 numerics: activation quantisation + INT4 x int8 GEMV per
+    step, `copies` distinct weight matrices cycled so none stays in the MALL."""
+    import ctypes as C
+    import torch
+    from ainfer_amd import _lib as L
+    lib = L.lib()
+    p = lambda t: C.c_void_p(t.data_ptr())
+    G = K // 128
+    Ws, Ss = [], []
+    for i in range(copies):
+        w = torch.empty(M * K // 2, dtype=torch.uint8, device="cuda")
+        s = torch.empty(M * G, dtype=torch.int16, device="cuda")
+        L.check(lib.ainfer_moe_fill(L.FILL_BYTES, 77 + i, 0.0, w.numel(), p(w), None))
+        L.check(lib.ainfer_moe_fill(L.FILL_BF16_ABSNORMAL, 177 + i, 0.02, s.numel(), p(s), None))
+        Ws.append(w)
+        Ss.append(s)
+    x = torch.randn(1, K, device="cuda", dtype=torch.float32) * 50
+    q = torch.empty(1, K, dtype=torch.int8, device="cuda")
+    sq = torch.empty(1, G, dtype=torch.float32, device="cuda")
+    y = torch.empty(1, M, dtype=torch.float32, device="cuda")
+
+    def step(i, quant=True):
+        if quant:
+            L.check(lib.ainfer_moe_act_quant_i8(p(x), L.ACT_F32, 1, K, p(q), p(sq), None))
+        L.check(lib.ainfer_moe_int4_gemv_i8(p(Ws[i % copies]), p(Ss[i % copies]), L.SCALE_BF16,
+                                            p(q), p(sq), M, K, 1, p(y), None))
+    res = {}
+    for quant in (False, True):
+        for i in range(10):
+            step(i, quant)
+        torch.cuda.synchronize()
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for i in range(steps):
+            step(i, quant)
+        t1.record()
+        torch.cuda.synchronize()
+        res[quant] = t0.elapsed_time(t1) / steps * 1e3
+    nbytes = M * K // 2 + M * G * 2 + K + G * 4 + M * 4
+    return {"shape": f"M={M} K={K} T=1 (gemv_replay.cpp:57)", "gemv_us": round(res[False], 3),
+            "gemv_gbs": round(nbytes / (res[False] * 1e-6) / 1e9, 1),
+            "gemv_hbm_frac": round(nbytes / (res[False] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "quant_plus_gemv_us": round(res[True], 3), "alg_bytes": nbytes,
+            "reference_b60_replay_us": 283.0}
+
+
 def cpu_baseline(layer, cfg, T, budget_s):
     """The C oracle on host cores, bounded to about budget_s seconds."""
     import numpy as np
@@ -178,6 +227,7 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-gemv", action="store_true", help="skip the W4A8 GEMV line")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="finally copy MIB MiB device-to-device 5 times (PMC calibration)")
@@ -251,6 +301,12 @@ def main():
         log(f"[bench]   {json.dumps(prefill)}")
         layers = [MoeLayer(c1, layer=0)]
 
+    gemv = None
+    if not args.no_gemv:
+        log("[bench] W4A8 GEMV 17408x5120")
+        gemv = run_gemv_w4a8(args.steps)
+        log(f"[bench]   {json.dumps(gemv)}")
+
     if args.calib_copy > 0:
         n = args.calib_copy << 20
         src = torch.ones(n, dtype=torch.uint8, device="cuda")
@@ -261,7 +317,7 @@ def main():
         log(f"[bench] calibration copy: 5 x {n} bytes")
 
     if not decode:
-        print(json.dumps({"prefill_c2_T4096": prefill}), flush=True)
+        print(json.dumps({"prefill_c2_T4096": prefill, "gemv_w4a8": gemv}), flush=True)
         return
     Th = 16 if 16 in decode else max(decode)
     d1 = decode[Th]
@@ -300,6 +356,7 @@ def main():
             "decode": {str(T): {k: (round(v, 4) if isinstance(v, float) else v)
                                 for k, v in d.items()} for T, d in decode.items()},
             "prefill_c2_T4096": prefill,
+            "gemv_w4a8": gemv,
         },
     }
     print(json.dumps(out), flush=True)
