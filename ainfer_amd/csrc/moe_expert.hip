@@ -190,6 +190,9 @@ __global__ __launch_bounds__(1024) void k_expert_lds(ExpertArgs a) {
 // KBW k-groups per wave (the preferred count, raised until one row group
 // fits in 16 waves, lowered until it divides both K group counts), WK =
 // waves along K, WR = row groups per block.
+#ifndef EXPERT_WAVES
+#define EXPERT_WAVES 4  // waves per expert item (K-split x row groups)
+#endif
 bool expert_geometry(int mode, int H, int I, int Is, int pref_kbw, int *KBW, int *WK,
                      int *WR) {
   const int KBr = (mode == 0 ? H : I) / 128;
@@ -200,7 +203,7 @@ bool expert_geometry(int mode, int H, int I, int Is, int pref_kbw, int *KBW, int
   while (kbw > 1 && (KBr % kbw || KBs % kbw)) kbw /= 2;
   if ((KBmax + kbw - 1) / kbw > MAX_WAVES || KBr % kbw || KBs % kbw) return false;
   const int wk = KBmax / kbw;
-  int wr = 4 / wk;
+  int wr = EXPERT_WAVES / wk;
   if (wr < 1) wr = 1;
   *KBW = kbw;
   *WK = wk;

@@ -131,7 +131,9 @@ constexpr int DECODE_MAX_T = EXACT_ROUTER_MAX_T;
 // up to this many tokens the expert stages run fused in one launch
 // (k_experts_decode); above it as gate/up, down and combine launches (the
 // fused items' handoffs cost more than the two launches they save)
-constexpr int FUSED_EXPERTS_MAX_T = 2;
+#ifndef FUSED_EXPERTS_MAX_T
+#define FUSED_EXPERTS_MAX_T 2
+#endif
 // sync region (int32 words at the start of the workspace, zero between calls):
 // the error word, the per-tile and per-(token, slab) counters of the fused
 // expert kernel, then the routing kernel's logit slots.  Counters sit
