@@ -66,7 +66,7 @@ struct ProfCall {
 };
 
 struct Layout {
-  size_t sync, sync_words, slots, logits, sg_logit, idx, w, sg, xperm, chunk_counts, rank, counts, offsets, perm, inv,
+  size_t sync, sync_words, slots, tiles2, n_tiles2, logits, sg_logit, idx, w, sg, xperm, chunk_counts, rank, counts, offsets, perm, inv,
       ptok, tiles, n_tiles, ticket, act, act_s, o, h, wnorm, xsum, asum, asum_s, total;
 };
 
@@ -118,6 +118,8 @@ Layout layout_of(const ainfer_moe_shape &s, int Tm) {
   L.tiles = take((size_t)max_tiles_bound(s, (int)T, DEC_MT) * 16);  // >= every other bound
   L.n_tiles = take(4);
   L.ticket = take(4);
+  L.tiles2 = take((E * ((GEMM_SMALL_MAX + SMALL_MT - 1) / SMALL_MT) + 1) * 16);
+  L.n_tiles2 = take(4);
   L.act = take(T * k * s.inter * 2);
   L.act_s = take(T * (size_t)(s.shared_inter > 0 ? s.shared_inter : 1) * 2);
   L.o = take(T * (k + 1) * H * 2);
@@ -174,6 +176,9 @@ DispatchOut dispatch_out(const ainfer_moe_shape *s, const Layout &L, void *ws, i
   d.tiles = at<int4>(ws, L.tiles);
   d.n_tiles = at<int32_t>(ws, L.n_tiles);
   d.ticket = at<int32_t>(ws, L.ticket);
+  d.tiles2 = at<int4>(ws, L.tiles2);
+  d.n_tiles2 = at<int32_t>(ws, L.n_tiles2);
+  d.small_max = 0;
   return d;
 }
 
@@ -272,6 +277,10 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
                                at<uint16_t>(ws, L.xperm), gemm ? at<float>(ws, L.xsum) : nullptr,
                                T, H, E, k, has_shared, fused ? &d : nullptr, st));
   pc->end(2);
+  // prefill: experts with at most SMALL_MT tokens skip the GEMM (a 128-token
+  // tile costs about half a full one however few tokens it holds) for one
+  // 16-token tile of the streaming kernels, which read their weights once
+  if (gemm) d.small_max = GEMM_SMALL_MAX;
   if (!fused)
     HIP_TRY(launch_dispatch(at<int32_t>(ws, L.idx), T, k, E, mt, has_shared,
                             at<int32_t>(ws, L.chunk_counts), at<int32_t>(ws, L.rank), d, st));
@@ -304,6 +313,22 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
     g.act = at<uint16_t>(ws, L.act);
     g.act_s = at<uint16_t>(ws, L.act_s);
     HIP_TRY(launch_expert_gemm(0, s->scale_dtype, g, gtiles, st));
+    ExpertArgs sgu, sdn;
+    int small_bound = 0;
+    if (d.small_max > 0) {
+      DispatchOut d2 = d;
+      d2.tiles = d.tiles2;
+      d2.n_tiles = d.n_tiles2;
+      sgu = expert_args(s, w, L, ws, d2, T, 0);
+      sdn = expert_args(s, w, L, ws, d2, T, 1);
+      // tiles2 holds at most E * ceil(small_max / SMALL_MT) tiles, and at
+      // most one partial tile per expert beyond T * k / SMALL_MT full ones
+      const long b1 = (long)E * ((GEMM_SMALL_MAX + SMALL_MT - 1) / SMALL_MT);
+      const long b2 = (long)T * k / SMALL_MT + E;
+      small_bound = (int)(b1 < b2 ? b1 : b2);
+      HIP_TRY(launch_expert_stream(0, s->scale_dtype, sgu, small_bound, 4, RG_GATE_UP, SMALL_MT,
+                                   st));
+    }
     pc->end(4);
     g.w0 = w->w_down;
     g.s0 = (const uint16_t *)w->s_down;
@@ -317,6 +342,10 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
     g.a_shared = at<uint16_t>(ws, L.act_s);
     g.o = at<uint16_t>(ws, L.o);
     HIP_TRY(launch_expert_gemm(1, s->scale_dtype, g, gtiles, st));
+    if (d.small_max > 0) {
+      HIP_TRY(launch_expert_stream(1, s->scale_dtype, sdn, small_bound, 2, RG_DOWN, SMALL_MT,
+                                   st));
+    }
     pc->end(5);
     HIP_TRY(launch_combine(at<uint16_t>(ws, L.o), d.inv, at<float>(ws, L.w), at<float>(ws, L.sg),
                            has_shared, resid, y, T, k, H, st));

@@ -51,6 +51,10 @@ hipError_t launch_expert_gemm(int mode, int scale_dtype, GemmArgs a, int max_til
                               hipStream_t s);
 // token-tile height of the prefill GEMM and the T above which it is used
 constexpr int GEMM_MT = 128;
+// experts with at most this many tokens leave the prefill GEMM (0: none)
+#ifndef GEMM_SMALL_MAX
+#define GEMM_SMALL_MAX 32
+#endif
 #ifndef GEMM_WN
 #define GEMM_WN 4       // row waves per GEMM block (2 x GEMM_WN waves)
 #endif
@@ -69,6 +73,11 @@ struct DispatchOut {
   int4 *tiles;
   int32_t *n_tiles;
   int32_t *ticket;
+  // experts with 1..small_max tokens get SMALL_MT-token tiles in tiles2
+  // instead of tiles (small_max 0: no split)
+  int4 *tiles2;
+  int32_t *n_tiles2;
+  int small_max;
 };
 
 hipError_t launch_fill(int kind, uint64_t seed, float std_, size_t n, void *out,

@@ -249,13 +249,17 @@ __global__ __launch_bounds__(64) void k_dispatch_count(const int32_t *__restrict
 
 // blockDim = 1024 >= E.  Also emits the tile list: for each expert with
 // tokens, ceil(count / mt) tiles (expert, first row), experts ascending,
-// then ceil(T / mt) shared-expert tiles (expert id E) when has_shared.
+// then ceil(T / mt) shared-expert tiles (expert id E) when has_shared.  With
+// ds.small_max > 0, an expert with 1..small_max tokens instead gets
+// ceil(count / SMALL_MT) tiles in ds.tiles2 (experts ascending), counted in
+// ds.n_tiles2.
 __global__ __launch_bounds__(1024) void k_dispatch_scan(int32_t *__restrict__ chunk_counts,
                                                         int nchunks, int E, int T, int mt,
                                                         int has_shared,
                                                         DispatchOut ds) {
   __shared__ int32_t sc[1024];
   __shared__ int32_t st[1024];
+  __shared__ int32_t ss[1024];
   const int e = threadIdx.x;
   constexpr int CB = 16;  // chunk counts loaded together (independent loads)
   int total = 0;
@@ -269,21 +273,27 @@ __global__ __launch_bounds__(1024) void k_dispatch_scan(int32_t *__restrict__ ch
       for (int j = 0; j < CB; ++j) total += v[j];
     }
   }
-  int ntile = (e < E) ? (total + mt - 1) / mt : 0;
+  const bool small = ds.small_max > 0 && total > 0 && total <= ds.small_max;
+  int ntile = (e < E && !small) ? (total + mt - 1) / mt : 0;
   sc[e] = e < E ? total : 0;
   st[e] = ntile;
+  const int nsmall = small ? (total + SMALL_MT - 1) / SMALL_MT : 0;
+  ss[e] = nsmall;
   __syncthreads();
   // Hillis-Steele inclusive scans over 1024 entries (integers: exact)
   for (int off = 1; off < 1024; off <<= 1) {
     int a = e >= off ? sc[e - off] : 0;
     int b = e >= off ? st[e - off] : 0;
+    int c = e >= off ? ss[e - off] : 0;
     __syncthreads();
     sc[e] += a;
     st[e] += b;
+    ss[e] += c;
     __syncthreads();
   }
   int base = sc[e] - (e < E ? total : 0);
   int tbase = st[e] - ntile;
+  const int sbase = ss[e] - nsmall;
   if (e < E) {
     ds.counts[e] = total;
     ds.offsets[e] = base;
@@ -303,8 +313,11 @@ __global__ __launch_bounds__(1024) void k_dispatch_scan(int32_t *__restrict__ ch
     if (ds.tiles)
       for (int i = 0; i < ntile; ++i)
         ds.tiles[tbase + i] = make_int4(e, base + i * mt, min(mt, total - i * mt), 0);
+    for (int i = 0; i < nsmall; ++i)
+      ds.tiles2[sbase + i] = make_int4(e, base + i * SMALL_MT, min(SMALL_MT, total - i * SMALL_MT), 0);
   }
   if (e == 0) ds.offsets[E] = sc[1023];
+  if (e == 0 && ds.small_max > 0) *ds.n_tiles2 = ss[1023];
   __syncthreads();
   const int routed_tiles = st[1023];
   const int nsh = has_shared ? (T + mt - 1) / mt : 0;
