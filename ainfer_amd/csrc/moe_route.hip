@@ -360,19 +360,21 @@ hipError_t launch_dispatch(const int32_t *idx, int T, int k, int E, int mt, int 
 
 // ---------------------------------------------------------------------------
 // Combine: y[t] = sum_j w[t][j] * o[inv[t*k+j]] + g_s[t] * o[T*k + t]
-// (+ residual), in slot order with fp32 fma, bf16 out.  One thread per 4
-// columns.
+// (+ residual), in slot order with fp32 fma, bf16 out.  One thread per CPT
+// columns (8: 16-byte loads).
 // ---------------------------------------------------------------------------
+template <int CPT>
 __global__ __launch_bounds__(256) void k_combine(const uint16_t *__restrict__ o,
                                                  const int32_t *__restrict__ inv,
                                                  const float *__restrict__ w,
                                                  const float *__restrict__ sg, int has_shared,
                                                  const uint16_t *__restrict__ resid,
                                                  uint16_t *__restrict__ y, int T, int k, int H) {
-  const int per_tok = H >> 2;
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= T * per_tok) return;
-  const int t = i / per_tok, h0 = (i % per_tok) * 4;
+  typedef uint32_t vec_t __attribute__((ext_vector_type(CPT / 2)));
+  // grid (T, ceil(H / (CPT * blockDim.x))): the token is uniform, so its
+  // slots' positions and weights are scalar loads
+  const int t = blockIdx.x, h0 = (blockIdx.y * blockDim.x + threadIdx.x) * CPT;
+  if (h0 >= H) return;
   int pos[32];
   float wj[32];
 #pragma unroll
@@ -381,43 +383,57 @@ __global__ __launch_bounds__(256) void k_combine(const uint16_t *__restrict__ o,
       pos[j] = inv[(size_t)t * k + j];
       wj[j] = w[(size_t)t * k + j];
     }
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  float acc[CPT];
 #pragma unroll
-  for (int j = 0; j < 32; ++j)
-    if (j < k) {
-      const uint2 r = *(const uint2 *)(o + (size_t)pos[j] * H + h0);
-      const float v[4] = {__uint_as_float(r.x << 16), __uint_as_float(r.x & 0xFFFF0000u),
-                          __uint_as_float(r.y << 16), __uint_as_float(r.y & 0xFFFF0000u)};
+  for (int q = 0; q < CPT; ++q) acc[q] = 0.0f;
+  auto fma_row = [&](float g, const vec_t &rv) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) acc[q] = __builtin_fmaf(wj[j], v[q], acc[q]);
+    for (int q = 0; q < CPT / 2; ++q) {
+      acc[2 * q] = __builtin_fmaf(g, __uint_as_float(rv[q] << 16), acc[2 * q]);
+      acc[2 * q + 1] = __builtin_fmaf(g, __uint_as_float(rv[q] & 0xFFFF0000u), acc[2 * q + 1]);
     }
-  if (has_shared) {
-    const float g = sg[t];
-    const uint2 r = *(const uint2 *)(o + ((size_t)T * k + t) * H + h0);
-    const float v[4] = {__uint_as_float(r.x << 16), __uint_as_float(r.x & 0xFFFF0000u),
-                        __uint_as_float(r.y << 16), __uint_as_float(r.y & 0xFFFF0000u)};
+  };
+  // slots in batches of 8: the batch's loads first, then its fmas in slot order
+  constexpr int B = 8;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) acc[q] = __builtin_fmaf(g, v[q], acc[q]);
+  for (int j0 = 0; j0 < 32; j0 += B) {
+    if (j0 >= k) break;
+    vec_t r[B];
+#pragma unroll
+    for (int j = 0; j < B; ++j)
+      r[j] = __builtin_nontemporal_load((const vec_t *)(o + (size_t)pos[min(j0 + j, k - 1)] * H + h0));
+#pragma unroll
+    for (int j = 0; j < B; ++j)
+      if (j0 + j < k) fma_row(wj[j0 + j], r[j]);
   }
+  if (has_shared)
+    fma_row(sg[t], __builtin_nontemporal_load((const vec_t *)(o + ((size_t)T * k + t) * H + h0)));
   if (resid) {
-    const uint2 r = *(const uint2 *)(resid + (size_t)t * H + h0);
-    acc[0] += __uint_as_float(r.x << 16);
-    acc[1] += __uint_as_float(r.x & 0xFFFF0000u);
-    acc[2] += __uint_as_float(r.y << 16);
-    acc[3] += __uint_as_float(r.y & 0xFFFF0000u);
+    const vec_t rr = *(const vec_t *)(resid + (size_t)t * H + h0);
+#pragma unroll
+    for (int q = 0; q < CPT / 2; ++q) {
+      acc[2 * q] += __uint_as_float(rr[q] << 16);
+      acc[2 * q + 1] += __uint_as_float(rr[q] & 0xFFFF0000u);
+    }
   }
-  uint2 out;
-  out.x = (uint32_t)f32_to_bf16(acc[0]) | ((uint32_t)f32_to_bf16(acc[1]) << 16);
-  out.y = (uint32_t)f32_to_bf16(acc[2]) | ((uint32_t)f32_to_bf16(acc[3]) << 16);
-  *(uint2 *)(y + (size_t)t * H + h0) = out;
+  vec_t out;
+#pragma unroll
+  for (int q = 0; q < CPT / 2; ++q)
+    out[q] = (uint32_t)f32_to_bf16(acc[2 * q]) | ((uint32_t)f32_to_bf16(acc[2 * q + 1]) << 16);
+  *(vec_t *)(y + (size_t)t * H + h0) = out;
 }
 
 hipError_t launch_combine(const uint16_t *o, const int32_t *inv, const float *w, const float *sg,
                           int has_shared, const void *resid, void *y, int T, int k, int H,
                           hipStream_t s) {
   if (T == 0) return hipSuccess;
-  const int n = T * (H / 4);
-  k_combine<<<(n + 255) / 256, 256, 0, s>>>(o, inv, w, sg, has_shared, (const uint16_t *)resid,
-                                            (uint16_t *)y, T, k, H);
+  // few tokens: 64-thread blocks, so the layer's columns spread over more CUs
+  const int nt = T <= 64 ? 64 : 256;
+  if (H % 8 == 0)
+    k_combine<8><<<dim3(T, (H / 8 + nt - 1) / nt), nt, 0, s>>>(
+        o, inv, w, sg, has_shared, (const uint16_t *)resid, (uint16_t *)y, T, k, H);
+  else
+    k_combine<4><<<dim3(T, (H / 4 + nt - 1) / nt), nt, 0, s>>>(
+        o, inv, w, sg, has_shared, (const uint16_t *)resid, (uint16_t *)y, T, k, H);
   return hipGetLastError();
 }
