@@ -257,57 +257,60 @@ __global__ __launch_bounds__(1024) void k_dispatch_scan(int32_t *__restrict__ ch
                                                         int nchunks, int E, int T, int mt,
                                                         int has_shared,
                                                         DispatchOut ds) {
-  __shared__ int32_t sc[1024];
-  __shared__ int32_t st[1024];
-  __shared__ int32_t ss[1024];
-  const int e = threadIdx.x;
-  constexpr int CB = 16;  // chunk counts loaded together (independent loads)
+  __shared__ int32_t wsum[2][16];
+  const int e = threadIdx.x, lane = e & 63, wv = e >> 6;
+  constexpr int CB = 16;    // chunk counts loaded together (independent loads)
   int total = 0;
   if (e < E) {
     for (int c0 = 0; c0 < nchunks; c0 += CB) {
-      int v[CB];
+      int u[CB];
 #pragma unroll
       for (int j = 0; j < CB; ++j)
-        v[j] = c0 + j < nchunks ? chunk_counts[(size_t)(c0 + j) * E + e] : 0;
+        u[j] = c0 + j < nchunks ? chunk_counts[(size_t)(c0 + j) * E + e] : 0;
 #pragma unroll
-      for (int j = 0; j < CB; ++j) total += v[j];
+      for (int j = 0; j < CB; ++j) total += u[j];
     }
   }
   const bool small = ds.small_max > 0 && total > 0 && total <= ds.small_max;
-  int ntile = (e < E && !small) ? (total + mt - 1) / mt : 0;
-  sc[e] = e < E ? total : 0;
-  st[e] = ntile;
+  const int ntile = (ds.tiles && e < E && !small) ? (total + mt - 1) / mt : 0;
   const int nsmall = small ? (total + SMALL_MT - 1) / SMALL_MT : 0;
-  ss[e] = nsmall;
-  __syncthreads();
-  // Hillis-Steele inclusive scans over 1024 entries (integers: exact)
-  for (int off = 1; off < 1024; off <<= 1) {
-    int a = e >= off ? sc[e - off] : 0;
-    int b = e >= off ? st[e - off] : 0;
-    int c = e >= off ? ss[e - off] : 0;
-    __syncthreads();
-    sc[e] += a;
-    st[e] += b;
-    ss[e] += c;
-    __syncthreads();
+  // two block scans (integers: exact): token counts, and the big tile count
+  // (low 16 bits) with the small tile count (high bits).  Where tiles are
+  // written (T * k / mt + E tiles at most, mt = 16 only below 256 tokens)
+  // both counts stay below 2^15.
+  const int ic = wave_scan_incl(total);
+  const int it = wave_scan_incl(ntile | (nsmall << 16));
+  if (lane == 63) {
+    wsum[0][wv] = ic;
+    wsum[1][wv] = it;
   }
-  int base = sc[e] - (e < E ? total : 0);
-  int tbase = st[e] - ntile;
-  const int sbase = ss[e] - nsmall;
+  __syncthreads();
+  int bc = 0, bt = 0, tc = 0, tt = 0;
+#pragma unroll
+  for (int w = 0; w < 16; ++w) {
+    const int a0 = wsum[0][w], a1 = wsum[1][w];
+    bc += w < wv ? a0 : 0;
+    bt += w < wv ? a1 : 0;
+    tc += a0;
+    tt += a1;
+  }
+  const int base = bc + ic - total;
+  const int tb = bt + it - (ntile | (nsmall << 16));
+  const int tbase = tb & 0xFFFF, sbase = tb >> 16;
   if (e < E) {
     ds.counts[e] = total;
     ds.offsets[e] = base;
     // chunk_counts[c][e] becomes the first position of chunk c's tokens of e
     int run = base;
     for (int c0 = 0; c0 < nchunks; c0 += CB) {
-      int v[CB];
+      int u[CB];
 #pragma unroll
       for (int j = 0; j < CB; ++j)
-        v[j] = c0 + j < nchunks ? chunk_counts[(size_t)(c0 + j) * E + e] : 0;
+        u[j] = c0 + j < nchunks ? chunk_counts[(size_t)(c0 + j) * E + e] : 0;
 #pragma unroll
       for (int j = 0; j < CB; ++j) {
         if (c0 + j < nchunks) chunk_counts[(size_t)(c0 + j) * E + e] = run;
-        run += v[j];
+        run += u[j];
       }
     }
     if (ds.tiles)
@@ -316,10 +319,9 @@ __global__ __launch_bounds__(1024) void k_dispatch_scan(int32_t *__restrict__ ch
     for (int i = 0; i < nsmall; ++i)
       ds.tiles2[sbase + i] = make_int4(e, base + i * SMALL_MT, min(SMALL_MT, total - i * SMALL_MT), 0);
   }
-  if (e == 0) ds.offsets[E] = sc[1023];
-  if (e == 0 && ds.small_max > 0) *ds.n_tiles2 = ss[1023];
-  __syncthreads();
-  const int routed_tiles = st[1023];
+  if (e == 0) ds.offsets[E] = tc;
+  if (e == 0 && ds.small_max > 0) *ds.n_tiles2 = tt >> 16;
+  const int routed_tiles = tt & 0xFFFF;
   const int nsh = has_shared ? (T + mt - 1) / mt : 0;
   if (ds.tiles)
     for (int i = e; i < nsh; i += blockDim.x)
