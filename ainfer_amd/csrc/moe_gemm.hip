@@ -431,7 +431,11 @@ __global__ __launch_bounds__(128 * WN) void k_expert_gemm(GemmArgs a) {
 // blocks after the GEMM tiles compute ||w_e|| (used only as the bound of
 // the canonical refine).
 // ---------------------------------------------------------------------------
-constexpr int RG_BM = 64, RG_BN = 128, RG_BK = 64, RG_ST = 3;
+#ifndef RG_BM_
+#define RG_BM_ 64
+#endif
+constexpr int RG_BM = RG_BM_, RG_BN = 128, RG_BK = 64, RG_ST = 3;
+constexpr int RG_MS = RG_BM / 32;  // 16-token MFMA rows per wave
 constexpr int RG_A = RG_BM * RG_BK * 2, RG_B = RG_BN * RG_BK * 2;  // bytes per stage
 constexpr int RG_STAGE = RG_A + RG_B;
 constexpr int RG_DMA = RG_STAGE / (256 * 16);  // per thread per stage: 6
@@ -497,9 +501,9 @@ __global__ __launch_bounds__(256) void k_router_gemm(const uint16_t *__restrict_
   const int G = H / RG_BK;
   issue(0);
   if (G > 1) issue(1);
-  f32x4 acc[2][4];
+  f32x4 acc[RG_MS][4];
 #pragma unroll
-  for (int ms = 0; ms < 2; ++ms)
+  for (int ms = 0; ms < RG_MS; ++ms)
 #pragma unroll
     for (int ns = 0; ns < 4; ++ns) acc[ms][ns] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int g = 0; g < G; ++g) {
@@ -516,10 +520,10 @@ __global__ __launch_bounds__(256) void k_router_gemm(const uint16_t *__restrict_
     const uint8_t *sa = lds + (g % RG_ST) * RG_STAGE, *sb = sa + RG_A;
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2) {  // two 32-wide MFMA steps
-      u32x4 af[2], bf[4];
+      u32x4 af[RG_MS], bf[4];
 #pragma unroll
-      for (int ms = 0; ms < 2; ++ms) {
-        const int r = wm * 32 + ms * 16 + m16;
+      for (int ms = 0; ms < RG_MS; ++ms) {
+        const int r = wm * (RG_BM / 2) + ms * 16 + m16;
         af[ms] = *(const u32x4 *)(sa + r * 128 + (((4 * s2 + q) ^ (r & 7)) << 4));
       }
 #pragma unroll
@@ -528,7 +532,7 @@ __global__ __launch_bounds__(256) void k_router_gemm(const uint16_t *__restrict_
         bf[ns] = *(const u32x4 *)(sb + r * 128 + (((4 * s2 + q) ^ (r & 7)) << 4));
       }
 #pragma unroll
-      for (int ms = 0; ms < 2; ++ms)
+      for (int ms = 0; ms < RG_MS; ++ms)
 #pragma unroll
         for (int ns = 0; ns < 4; ++ns) acc[ms][ns] = mfma_bf16_16x16x32(af[ms], bf[ns], acc[ms][ns]);
     }
@@ -541,10 +545,10 @@ __global__ __launch_bounds__(256) void k_router_gemm(const uint16_t *__restrict_
     if (e >= E) continue;
     const float b = bias ? bias[e] : 0.0f;
 #pragma unroll
-    for (int ms = 0; ms < 2; ++ms)
+    for (int ms = 0; ms < RG_MS; ++ms)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int t = t0 + wm * 32 + ms * 16 + 4 * q + r;
+        const int t = t0 + wm * (RG_BM / 2) + ms * 16 + 4 * q + r;
         if (t < T) approx[(size_t)t * E + e] = bias ? acc[ms][ns][r] + b : acc[ms][ns][r];
       }
   }

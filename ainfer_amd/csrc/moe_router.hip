@@ -31,6 +31,17 @@
 #include "moe_topk.h"
 #include "moe_internal.h"
 
+#ifdef AINFER_DECODE_TRACE
+__device__ unsigned long long g_strace[4096][8];
+#define STRACE(I) \
+  if ((threadIdx.x & 63) == 0 && t < 4096) g_strace[t][I] = __builtin_amdgcn_s_memrealtime()
+extern "C" int ainfer_debug_strace(void *host) {
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_strace), sizeof(g_strace)) == hipSuccess ? 0 : -1;
+}
+#else
+#define STRACE(I)
+#endif
+
 namespace {
 
 // ---------------------------------------------------------------------------
@@ -185,6 +196,9 @@ __device__ __forceinline__ void canon_dot_batch(const u32x4 (&xc)[CH], const uin
 
 
 constexpr int SEL_WAVES = 4;
+#ifndef SEL_NB
+#define SEL_NB 4  // candidate rows whose loads are issued together
+#endif
 
 // EXACT: `approx` already holds the canonical logits (k_router_logits) and
 // `sgl` the canonical shared-gate logits; the refine is skipped.
@@ -213,7 +227,9 @@ __global__ __launch_bounds__(256) void k_select(const float *__restrict__ approx
   if (t < T) {
     // the MFMA-order copy of x (and its group sums) does not depend on the
     // routing: written first, its latency hides under the selection
+    STRACE(0);
     if (xperm) write_xperm(x + (size_t)t * H, xperm, xsum, t, H, lane);
+    STRACE(1);
     const float *ar = approx + (size_t)t * E;
     // ---- k-th largest approximate logit -------------------------------
     uint32_t key[NV];
@@ -228,6 +244,7 @@ __global__ __launch_bounds__(256) void k_select(const float *__restrict__ approx
     int seli;
     uint32_t selk;
     wave_topk_fast<NV>(key, E, k, lane, seli, selk, s_cand[wave], s_sel[wave]);
+    STRACE(2);
     const uint32_t kth = (uint32_t)__shfl((int)selk, k - 1, 64);
     float selv = 0.0f, sgv = 0.0f;
     const uint16_t *xrow = x + (size_t)t * H;
@@ -271,24 +288,26 @@ __global__ __launch_bounds__(256) void k_select(const float *__restrict__ approx
         nc += __popcll(b);
       }
       __builtin_amdgcn_wave_barrier();
+      STRACE(3);
       // ---- canonical logits of the candidates ------------------------------
       {
-        for (int c0 = 0; c0 < nc; c0 += 4) {
-          const uint16_t *rows[4];
-          int ee[4];
+        for (int c0 = 0; c0 < nc; c0 += SEL_NB) {
+          const uint16_t *rows[SEL_NB];
+          int ee[SEL_NB];
 #pragma unroll
-          for (int b = 0; b < 4; ++b) {
+          for (int b = 0; b < SEL_NB; ++b) {
             ee[b] = cl[wave][min(c0 + b, nc - 1)];
             rows[b] = rw + (size_t)ee[b] * H;
           }
-          float v[4];
-          canon_dot_batch<CH, 4>(xc, rows, lane, nch, v);
+          float v[SEL_NB];
+          canon_dot_batch<CH, SEL_NB>(xc, rows, lane, nch, v);
 #pragma unroll
-          for (int b = 0; b < 4; ++b)
+          for (int b = 0; b < SEL_NB; ++b)
             if (lane == 0 && c0 + b < nc) cv[wave][c0 + b] = bias ? v[b] + bias[ee[b]] : v[b];
         }
       }
       __builtin_amdgcn_wave_barrier();
+      STRACE(4);
       // ---- top-k among candidates (value desc, expert asc) ----------------
       if (nc <= 64 && k <= 16) {
         // rank of each candidate = candidates above it (unique composite keys)
@@ -327,7 +346,9 @@ __global__ __launch_bounds__(256) void k_select(const float *__restrict__ approx
         }
       }
       }
+      STRACE(5);
       if (gw) sgv = canon_dot<CH>(xc, gw, lane, nch);
+      STRACE(6);
     }
     const float vmax = __shfl(selv, 0, 64);
     const float p = lane < k ? expf(selv - vmax) : 0.0f;
@@ -341,6 +362,7 @@ __global__ __launch_bounds__(256) void k_select(const float *__restrict__ approx
     float g = 1.0f;
     if (gw) g = 1.0f / (1.0f + expf(-sgv));
     if (lane == 0) sgate[t] = g;
+    STRACE(7);
   }
   if (!fused) return;
   // ---- the last block runs the dispatch ---------------------------------
