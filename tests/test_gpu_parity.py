@@ -269,3 +269,27 @@ def test_zero_tokens_and_errors(torch, oracle):
     x = torch.zeros(8, layer.cfg.hidden, dtype=torch.bfloat16, device="cuda")
     with pytest.raises(L.MoeError):
         layer.forward(x, x.clone(), ws)       # workspace sized for 4 tokens
+
+
+@pytest.mark.parametrize("name,T", [("c1", 1), ("c1", 16), ("c1", 300), ("c3", 64)])
+def test_forward_parity_bf16_scales(torch, oracle, name, T):
+    """The reference's own scale dtype (bf16, binfer.py:76-91) through every
+    expert path: the fused decode kernel (T=1), the staged decode kernels
+    (T=16), the prefill GEMM with small-expert tiles (T=300) and the
+    16-token-tile kernels (c3, T=64)."""
+    from ainfer_amd import _lib as L
+    from ainfer_amd.moe import MoeLayer, make_input
+    from ainfer_amd.synthetic import CONFIGS
+    print(f"[case] forward bf16 scales {name} T={T}", flush=True)
+    _layers.clear()
+    torch.cuda.empty_cache()
+    layer = MoeLayer(CONFIGS[name], scale_dtype=L.SCALE_BF16)
+    x = make_input(layer.cfg, T, tag=500 + T)
+    ws = layer.workspace(T)
+    y = torch.full((T, layer.cfg.hidden), float("nan"), dtype=torch.bfloat16, device="cuda")
+    layer.forward(x, y, ws)
+    torch.cuda.synchronize()
+    assert not torch.isnan(y).any()
+    ref = host_copy(oracle, layer).forward(to_np(x), T)
+    check_close(to_np(y), ref, f"bf16 scales {name} T={T}")
+    del layer
