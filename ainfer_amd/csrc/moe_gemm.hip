@@ -158,36 +158,28 @@ __global__ __launch_bounds__(128 * WN) void k_expert_gemm(GemmArgs a) {
   }
   auto issue = [&](int g) {  // DMA of group g into stage g % STAGES
     const uint32_t base = lds0 + (uint32_t)(g % STAGES) * STAGE;
-#ifndef GEMM_EXP_NOADMA
 #pragma unroll
     for (int i = 0; i < Gm::A_DMA; ++i)
       dma16(asrc[i] + g * 256, base + (uint32_t)((i * NW + wave) * 1024));
-#endif
-#ifndef GEMM_EXP_NOBDMA
 #pragma unroll
     for (int i = 0; i < Gm::B_DMA; ++i)
       dma16(bsrc[i] + g * 64, base + A_STAGE + (uint32_t)((i * NW + wave) * 1024));
-#endif
   };
 
   // ---- prologue: group 0 in flight; tables to LDS ---------------------------
   issue(0);
   // Tables: every load is issued before the first use (unrolled, clamped
   // indices, no per-lane branches), so the block pays one latency, not one
-  // per element.  G <= 32.
+  // per element.  G <= 32.  Entry idx is (g = idx / rows, row = idx % rows):
+  // consecutive threads write consecutive LDS words (the global reads
+  // gather instead), so the LDS stores are free of bank conflicts.
   {
-    // idx / G through a float reciprocal: idx < 2^13 and G <= 32, so
-    // (idx + 0.5) / G is at least 1/64 away from an integer and the float
-    // product truncates to the exact quotient.
-    const float rG = 1.0f / (float)G;
-    auto divG = [&](int idx) { return (int)(((float)idx + 0.5f) * rG); };
     constexpr int SC_IT = BN * 32 / THREADS;
-    const int nsc = BN * G;
     uint16_t scv[SC_IT];
 #pragma unroll
     for (int i = 0; i < SC_IT; ++i) {
-      const int idx = min(tid + i * THREADS, nsc - 1);
-      const int r = divG(idx), g = idx - r * G;
+      const int idx = tid + i * THREADS;
+      const int r = idx % BN, g = min(idx / BN, G - 1);
       const uint16_t *sc;
       int row;
       if (MODE == 0) {
@@ -201,27 +193,26 @@ __global__ __launch_bounds__(128 * WN) void k_expert_gemm(GemmArgs a) {
       scv[i] = sc[(size_t)min(row, N - 1) * G + g];
     }
     constexpr int XS_IT = BM * 32 / THREADS;
-    const int nxs = BM * G;
     float xv[XS_IT];
     if (MODE == 0) {
       int tok[XS_IT];
 #pragma unroll
       for (int i = 0; i < XS_IT; ++i) {
-        const int row = min(divG(min(tid + i * THREADS, nxs - 1)), mcnt - 1);
+        const int row = min((tid + i * THREADS) % BM, mcnt - 1);
         tok[i] = shared ? pos0 + row : a.ptok[pos0 + row];
       }
 #pragma unroll
       for (int i = 0; i < XS_IT; ++i) {
-        const int idx = min(tid + i * THREADS, nxs - 1);
-        xv[i] = a.xsum[(size_t)tok[i] * G + (idx - divG(idx) * G)];
+        const int g = min((tid + i * THREADS) / BM, G - 1);
+        xv[i] = a.xsum[(size_t)tok[i] * G + g];
       }
     } else {
       // act partial sums: a.aslots per 128-wide group, added in order
       const float *asb = shared ? a.asum_s : a.asum;
 #pragma unroll
       for (int i = 0; i < XS_IT; ++i) {
-        const int idx = min(tid + i * THREADS, nxs - 1);
-        const int q0 = divG(idx), row = min(q0, mcnt - 1), g = idx - q0 * G;
+        const int idx = tid + i * THREADS;
+        const int row = min(idx % BM, mcnt - 1), g = min(idx / BM, G - 1);
         const float *as = asb + (size_t)(pos0 + row) * (a.aslots * G) + a.aslots * g;
         float v = as[0];
         for (int j = 1; j < a.aslots; ++j) v += as[j];
@@ -231,14 +222,12 @@ __global__ __launch_bounds__(128 * WN) void k_expert_gemm(GemmArgs a) {
 #pragma unroll
     for (int i = 0; i < SC_IT; ++i) {
       const int idx = tid + i * THREADS;
-      const int r = divG(idx);
-      if (idx < nsc) sc_lds[(idx - r * G) * BN + r] = scv[i];
+      if (idx < BN * G) sc_lds[idx] = scv[i];  // [g][r]
     }
 #pragma unroll
     for (int i = 0; i < XS_IT; ++i) {
       const int idx = tid + i * THREADS;
-      const int row = divG(idx);
-      if (idx < nxs) xs_lds[(idx - row * G) * BM + row] = row < mcnt ? -136.0f * xv[i] : 0.0f;
+      if (idx < BM * G) xs_lds[idx] = idx % BM < mcnt ? -136.0f * xv[i] : 0.0f;  // [g][row]
     }
   }
 
@@ -308,11 +297,7 @@ __global__ __launch_bounds__(128 * WN) void k_expert_gemm(GemmArgs a) {
       for (int ms = 0; ms < NMS; ++ms)
 #pragma unroll
         for (int ns = 0; ns < 4; ++ns)
-#ifdef GEMM_EXP_NOMFMA
-          acc[ms][ns] = (j == 0 ? c0[ms] : acc[ms][ns]) + (float)(af[ms][0] ^ bf[ns][1]);
-#else
           acc[ms][ns] = mfma_bf16_16x16x32(af[ms], bf[ns], j == 0 ? c0[ms] : acc[ms][ns]);
-#endif
     }
 #pragma unroll
     for (int ns = 0; ns < 4; ++ns) sprev[ns] = sg[ns];
@@ -345,19 +330,33 @@ __global__ __launch_bounds__(128 * WN) void k_expert_gemm(GemmArgs a) {
     for (int ms = 0; ms < 4; ++ms)
 #pragma unroll
       for (int r = 0; r < 4; ++r) rowsum[ms][r] = 0.0f;
+    // Columns k and k + 4 of a 32-column block are neighbours in MFMA order
+    // (perm32_pos), and live in lanes m16 and m16 ^ 4: the pair trades
+    // halves so that each lane stores whole dwords (lane bit 2 clear: rows
+    // r = 0, 1; set: rows 2, 3).  2-byte LDS stores cost several times a
+    // dword store.
+    const bool hi4 = (m16 & 4) != 0;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       // within a 32-aligned block of columns, MFMA order is block-local
-      const int p = perm32_pos(wn * 32 + h * 16 + m16);
+      const int p = perm32_pos(wn * 32 + h * 16 + (m16 & ~4));  // the pair's even position
 #pragma unroll
-      for (int ms = 0; ms < 4; ++ms)
+      for (int ms = 0; ms < 4; ++ms) {
+        uint32_t v[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int row = wm * 64 + ms * 16 + 4 * q + r;
-          const uint16_t v = f32_to_bf16(silu_mul(tot[ms][h][r], tot[ms][h + 2][r]));
-          rowsum[ms][r] += bf16_to_f32(v);
-          *(uint16_t *)(lds + row * OST + p * 2) = v;
+          v[r] = f32_to_bf16(silu_mul(tot[ms][h][r], tot[ms][h + 2][r]));
+          rowsum[ms][r] += bf16_to_f32((uint16_t)v[r]);
         }
+        const uint32_t send = hi4 ? (v[0] | (v[1] << 16)) : (v[2] | (v[3] << 16));
+        // lane ^ 4 inside each group of 32 lanes (ds_swizzle bit mode)
+        const uint32_t recv = (uint32_t)__builtin_amdgcn_ds_swizzle((int)send, 0x101F);
+        const int row0 = wm * 64 + ms * 16 + 4 * q + (hi4 ? 2 : 0);
+        const uint32_t d0 = hi4 ? ((recv & 0xFFFFu) | (v[2] << 16)) : (v[0] | (recv << 16));
+        const uint32_t d1 = hi4 ? ((recv >> 16) | (v[3] << 16)) : (v[1] | (recv & 0xFFFF0000u));
+        *(uint32_t *)(lds + row0 * OST + p * 2) = d0;
+        *(uint32_t *)(lds + (row0 + 1) * OST + p * 2) = d1;
+      }
     }
     // per-row sum over this wave's 32 columns: reduce over the 16 lanes m16
 #pragma unroll
@@ -397,16 +396,28 @@ __global__ __launch_bounds__(128 * WN) void k_expert_gemm(GemmArgs a) {
   } else {
     constexpr int OST = BN * 2 + 16;
     static_assert(BM * OST <= STAGES * STAGE, "staging exceeds the ring");
+    // Neighbouring columns live in lanes m16 and m16 ^ 1: the pair trades
+    // halves so that each lane stores whole dwords (even lane: rows r = 0,
+    // 1; odd lane: rows 2, 3).  With the 528-byte row stride the 32 lanes of
+    // one store hit 32 distinct banks.
+    const bool odd = (m16 & 1) != 0;
 #pragma unroll
     for (int ns = 0; ns < 4; ++ns) {
-      const int cl = wn * 64 + 16 * ns + m16;
+      const int cl = wn * 64 + 16 * ns + (m16 & ~1);
 #pragma unroll
-      for (int ms = 0; ms < 4; ++ms)
+      for (int ms = 0; ms < 4; ++ms) {
+        uint32_t v[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = wm * 64 + ms * 16 + 4 * q + r;
-          *(uint16_t *)(lds + row * OST + cl * 2) = f32_to_bf16(tot[ms][ns][r]);
-        }
+        for (int r = 0; r < 4; ++r) v[r] = f32_to_bf16(tot[ms][ns][r]);
+        const uint32_t send = odd ? (v[0] | (v[1] << 16)) : (v[2] | (v[3] << 16));
+        const uint32_t recv =
+            (uint32_t)__builtin_amdgcn_update_dpp(0, (int)send, 0xB1, 0xF, 0xF, false);  // lane ^ 1
+        const int row0 = wm * 64 + ms * 16 + 4 * q + (odd ? 2 : 0);
+        const uint32_t d0 = odd ? ((recv & 0xFFFFu) | (v[2] << 16)) : (v[0] | (recv << 16));
+        const uint32_t d1 = odd ? ((recv >> 16) | (v[3] << 16)) : (v[1] | (recv & 0xFFFF0000u));
+        *(uint32_t *)(lds + row0 * OST + cl * 2) = d0;
+        *(uint32_t *)(lds + (row0 + 1) * OST + cl * 2) = d1;
+      }
     }
     __syncthreads();
     constexpr int CPR = BN / 8;
