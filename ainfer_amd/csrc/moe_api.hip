@@ -423,9 +423,10 @@ const char *ainfer_moe_strerror(int status) {
 int ainfer_moe_validate(const ainfer_moe_shape *s) {
   if (!s) return AINFER_ERR_NULL;
   if (s->group != 128 || s->reserved != 0) return AINFER_ERR_SHAPE;
-  if (s->hidden < 128 || s->hidden % 128 || s->hidden > 8192) return AINFER_ERR_SHAPE;
-  if (s->inter < 128 || s->inter % 128 || s->inter > 8192) return AINFER_ERR_SHAPE;
-  if (s->shared_inter < 0 || s->shared_inter % 128 || s->shared_inter > 8192)
+  // K of every expert product <= 4096 (the prefill GEMM's tables hold 32 groups)
+  if (s->hidden < 128 || s->hidden % 128 || s->hidden > 4096) return AINFER_ERR_SHAPE;
+  if (s->inter < 128 || s->inter % 128 || s->inter > 4096) return AINFER_ERR_SHAPE;
+  if (s->shared_inter < 0 || s->shared_inter % 128 || s->shared_inter > 4096)
     return AINFER_ERR_SHAPE;
   if (s->n_experts < 1 || s->n_experts > 1024) return AINFER_ERR_SHAPE;
   if (s->top_k < 1 || s->top_k > 32 || s->top_k > s->n_experts) return AINFER_ERR_SHAPE;

@@ -293,3 +293,45 @@ def test_forward_parity_bf16_scales(torch, oracle, name, T):
     ref = host_copy(oracle, layer).forward(to_np(x), T)
     check_close(to_np(y), ref, f"bf16 scales {name} T={T}")
     del layer
+
+
+# shapes at the validation limits: E = 1024 experts, k = 32 (above the fast
+# top-k's 16), no shared expert; H = I = 128 (one k-group); H = I = 4096
+EDGE = {
+    "wide": dict(hidden=1024, n_experts=1024, top_k=32, inter=128, shared_inter=0),
+    "narrow": dict(hidden=128, n_experts=8, top_k=8, inter=128, shared_inter=128),
+    "deep": dict(hidden=4096, n_experts=16, top_k=2, inter=4096, shared_inter=4096),
+}
+
+
+EDGE_CASES = [(e, T) for e in ("wide", "narrow") for T in (1, 5, 16, 40, 300)] + \
+    [("deep", T) for T in (1, 5, 16, 40)]
+
+
+@pytest.mark.parametrize("edge,T", EDGE_CASES)
+def test_forward_parity_at_shape_limits(torch, oracle, edge, T):
+    """Route (bit-exact top-k and permutation) and forward parity on shapes
+    at the validation limits, through every T regime (decode kernels,
+    16-token tiles, prefill GEMM)."""
+    import dataclasses
+    from ainfer_amd.moe import MoeLayer, make_input
+    from ainfer_amd.synthetic import CONFIGS
+    print(f"[case] edge {edge} T={T}", flush=True)
+    cfg = dataclasses.replace(CONFIGS["c1"], name=f"edge_{edge}", **EDGE[edge])
+    _layers.clear()
+    torch.cuda.empty_cache()
+    layer = MoeLayer(cfg)
+    x = make_input(cfg, T, tag=900 + T)
+    ws = layer.workspace(T)
+    hl = host_copy(oracle, layer)
+    idx, w, sg, lg = layer.route(x, ws, want_logits=True)
+    torch.cuda.synchronize()
+    r_idx, r_w, r_sg, r_lg = hl.route(to_np(x), T)
+    assert np.array_equal(to_np(lg).view(np.uint32), r_lg.view(np.uint32)), "logits"
+    assert np.array_equal(to_np(idx), r_idx), "top-k"
+    y = torch.full((T, cfg.hidden), float("nan"), dtype=torch.bfloat16, device="cuda")
+    layer.forward(x, y, ws)
+    torch.cuda.synchronize()
+    assert not torch.isnan(y).any()
+    check_close(to_np(y), hl.forward(to_np(x), T), f"edge {edge} T={T}")
+    del layer
