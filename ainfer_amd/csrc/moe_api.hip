@@ -222,6 +222,18 @@ ExpertArgs expert_args(const ainfer_moe_shape *s, const ainfer_moe_weights *w, c
   return a;
 }
 
+#ifndef SGU_KBW
+#define SGU_KBW 4
+#endif
+#ifndef SGU_RG
+#define SGU_RG RG_GATE_UP
+#endif
+#ifndef SDN_KBW
+#define SDN_KBW 2
+#endif
+#ifndef SDN_RG
+#define SDN_RG RG_DOWN
+#endif
 int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const void *x,
                const void *resid, void *y, int T, void *ws, hipStream_t st,
                ProfCall *pc) {
@@ -326,7 +338,7 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
       const long b1 = (long)E * ((GEMM_SMALL_MAX + SMALL_MT - 1) / SMALL_MT);
       const long b2 = (long)T * k / SMALL_MT + E;
       small_bound = (int)(b1 < b2 ? b1 : b2);
-      HIP_TRY(launch_expert_stream(0, s->scale_dtype, sgu, small_bound, 4, RG_GATE_UP, SMALL_MT,
+      HIP_TRY(launch_expert_stream(0, s->scale_dtype, sgu, small_bound, SGU_KBW, SGU_RG, SMALL_MT,
                                    st));
     }
     pc->end(4);
@@ -343,7 +355,7 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
     g.o = at<uint16_t>(ws, L.o);
     HIP_TRY(launch_expert_gemm(1, s->scale_dtype, g, gtiles, st));
     if (d.small_max > 0) {
-      HIP_TRY(launch_expert_stream(1, s->scale_dtype, sdn, small_bound, 2, RG_DOWN, SMALL_MT,
+      HIP_TRY(launch_expert_stream(1, s->scale_dtype, sdn, small_bound, SDN_KBW, SDN_RG, SMALL_MT,
                                    st));
     }
     pc->end(5);
