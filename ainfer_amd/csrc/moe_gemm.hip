@@ -7,23 +7,25 @@
 // Restates the reference's INT4 GEMM (ChunkGemm, tools/cmdlist/kernels.cpp:
 // 691-785; gemmMT4, tools/prefill/prefill.cpp:46-129) for bf16 MFMA.
 //
-// Block tile: 128 tokens (one expert tile of the dispatch) x 128 weight rows
-// (MODE 0: 64 gate rows + the matching 64 up rows; MODE 1: 128 down rows),
-// K in 128-wide groups.  4 waves as 2 (tokens) x 2 (rows); a wave owns
-// 64 x 64 = 4 x 4 tiles of v_mfma_f32_16x16x32_bf16.
+// Block tile: 128 tokens (one expert tile of the dispatch) x 64 * GEMM_WN
+// weight rows (GEMM_WN = 4: MODE 0 takes 128 gate rows and the matching 128
+// up rows, MODE 1 256 down rows), K in 128-wide groups.  2 x GEMM_WN waves
+// as 2 (tokens) x GEMM_WN (rows); a wave owns 64 x 64 = 4 x 4 tiles of
+// v_mfma_f32_16x16x32_bf16.  Token subtiles past the tile's count skip
+// their MFMAs and A reads.
 //
-// Data movement: a 3-stage LDS ring per block.  Each stage holds one group
-// of the token rows (128 x 256 B, already in MFMA order) and of the raw INT4
-// weight rows (128 x 64 B).  Both arrive by global->LDS DMA
-// (global_load_lds_dwordx4: lane i of a wave lands at M0 + 16 i), two groups
-// ahead of the math, with no staging registers.  The DMA is issued from
-// inline asm and its completion tracked with explicit vmcnt waits, so the
-// compiler's conservative waits do not serialise the ring.  Rows are XOR-
-// swizzled in 16-byte chunks (A: chunk c of row r at c ^ (r & 15)) so that
-// the 16 lanes reading 16 rows at one column
-// hit distinct bank groups (B: chunk q at q ^ bswz(r)).  Scales and the group sums sum_{k in g} a
-// (for x from k_select, for act from this kernel's MODE 0 epilogue) are
-// copied to LDS once per block.
+// Data movement: a 2-stage LDS ring per block, one barrier per group.  Each
+// stage holds one group of the token rows (128 x 256 B, already in MFMA
+// order) and of the raw INT4 weight rows (64 B each).  Both arrive by
+// global->LDS DMA (global_load_lds_dwordx4: lane i of a wave lands at
+// M0 + 16 i), one group ahead of the math, with no staging registers.  The
+// DMA is issued from inline asm and its completion tracked with explicit
+// vmcnt waits, so the compiler's conservative waits do not serialise the
+// ring.  Rows are swizzled in 16-byte chunks (A: chunk c of row r at
+// c ^ aswz(r); B: chunk q at q ^ bswz(r)) so that the lanes reading 16 rows
+// at one column hit distinct bank groups.  Scales and the group sums
+// sum_{k in g} a (for x from k_select, for act from this kernel's MODE 0
+// epilogue) are copied to LDS once per block.
 #include <type_traits>
 
 #include "moe_common.h"
@@ -66,6 +68,13 @@ __device__ __forceinline__ void block_barrier() {
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
 }
+
+// A chunk swizzle: logical 16-byte chunk c of token row r sits at
+// c ^ aswz(r), the 2-bit halves of r & 15 swapped.  The 16 rows that one
+// fragment read touches at one logical chunk then spread over all 8
+// 16-byte bank groups in each pair of k-quarter lanes (measured: 77% fewer
+// LDS bank-conflict cycles than c ^ r).
+__device__ __forceinline__ int aswz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 
 // B chunk swizzle: 2-bit function of the row such that 8 consecutive rows
 // (32 banks x 4 B) and 16 consecutive rows (64 banks) both land the 16-byte
@@ -126,7 +135,7 @@ __global__ __launch_bounds__(128 * WN) void k_expert_gemm(GemmArgs a) {
 #pragma unroll
   for (int i = 0; i < Gm::A_DMA; ++i) {
     const int s = (i * NW + wave) * 64 + lane;
-    const int r = s >> 4, c = (s & 15) ^ (r & 15);
+    const int r = s >> 4, c = (s & 15) ^ aswz(r);
     const int rr = min(r, mcnt - 1);
     const uint16_t *row;
     if (MODE == 0) {
@@ -287,7 +296,7 @@ __global__ __launch_bounds__(128 * WN) void k_expert_gemm(GemmArgs a) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       u32x4 af[4], bf[4];
-      const int chunk = ((4 * q + j) ^ m16) << 4;
+      const int chunk = ((4 * q + j) ^ aswz(m16)) << 4;
 #pragma unroll
       for (int ms = 0; ms < NMS; ++ms) af[ms] = *(const u32x4 *)(arow + ms * 16 * 256 + chunk);
 #pragma unroll
