@@ -9,7 +9,7 @@
 // handed over by sc1 stores and loads instead of fences (moe_common.h):
 //
 //  k_route_decode   workgroups [0, NR): canonical router logits, one
-//                   (RD_R rows x RD_TT tokens) unit per wave, each stored
+//                   (one row x 1 or 2 tokens) unit per wave, each stored
 //                   with an sc1 store as ~bits into a key slot of the sync
 //                   region (never 0: ~bits == 0 only for one NaN pattern no
 //                   bf16 product or sum yields); the last workgroup (one wave
@@ -41,6 +41,8 @@
 // Debug builds with -DAINFER_DECODE_TRACE record per-workgroup timestamps.
 #include <string.h>
 
+#include <type_traits>
+
 #include "moe_common.h"
 #include "moe_expert_item.h"
 #include "moe_internal.h"
@@ -63,9 +65,13 @@ extern "C" int ainfer_debug_trace(void *host) {
 namespace {
 
 constexpr int RD_WAVES = 16;  // waves per k_route_decode workgroup
-constexpr int RD_R = 2;      // router rows per wave
-constexpr int RD_TT = 4;     // tokens per router pass
-constexpr int RD_NB = 2;     // 8-element chunks per lane whose loads are issued together
+// Router units: one router row x TT tokens per wave (TT = 1 up to
+// RD_TT1_MAX tokens, else 2: more, shorter units shorten the routing at few
+// tokens; measured at T = 1, 4, 16 against 2 rows x 4 tokens: -2.9, -3.4,
+// -0.5 us per layer).
+constexpr int RD_R = 1;       // router rows per wave
+constexpr int RD_TT1_MAX = 4;
+constexpr int RD_NB = 2;      // 8-element chunks per lane whose loads are issued together
 constexpr int SPIN_MAX = 1 << 20;
 #ifndef DEC_WAVES_PER_SIMD
 #define DEC_WAVES_PER_SIMD 6  // register budget of the expert kernel (<= 80 VGPRs)
@@ -181,7 +187,7 @@ __device__ __forceinline__ void dispatch_decode(const int32_t *__restrict__ idx,
   }
 }
 
-template <int NV>
+template <int NV, int RD_TT>
 __global__ __launch_bounds__(RD_WAVES * 64) void k_route_decode(RouteDecodeArgs a) {
   __shared__ uint64_t s_cand[RD_WAVES][68];
   __shared__ uint64_t s_sel[RD_WAVES][16];
@@ -508,15 +514,23 @@ hipError_t launch_route_decode(const void *x, const void *rw, const float *bias,
   a.k = k;
   a.has_shared = has_shared;
   const int nrows = E + (gw ? 1 : 0);
-  const int units = (nrows + RD_R - 1) / RD_R * ((T + RD_TT - 1) / RD_TT);
+  const int tt = T <= RD_TT1_MAX ? 1 : 2;
+  const int units = (nrows + RD_R - 1) / RD_R * ((T + tt - 1) / tt);
   a.NR = (units + RD_WAVES - 1) / RD_WAVES;
   const unsigned grid = a.NR + 1;
   const int nv = (E + 63) / 64;
-  if (nv <= 1) k_route_decode<1><<<grid, RD_WAVES * 64, 0, s>>>(a);
-  else if (nv <= 2) k_route_decode<2><<<grid, RD_WAVES * 64, 0, s>>>(a);
-  else if (nv <= 4) k_route_decode<4><<<grid, RD_WAVES * 64, 0, s>>>(a);
-  else if (nv <= 8) k_route_decode<8><<<grid, RD_WAVES * 64, 0, s>>>(a);
-  else k_route_decode<16><<<grid, RD_WAVES * 64, 0, s>>>(a);
+  auto go = [&](auto nv_c) {
+    constexpr int NVc = decltype(nv_c)::value;
+    if (tt == 1)
+      k_route_decode<NVc, 1><<<grid, RD_WAVES * 64, 0, s>>>(a);
+    else
+      k_route_decode<NVc, 2><<<grid, RD_WAVES * 64, 0, s>>>(a);
+  };
+  if (nv <= 1) go(std::integral_constant<int, 1>());
+  else if (nv <= 2) go(std::integral_constant<int, 2>());
+  else if (nv <= 4) go(std::integral_constant<int, 4>());
+  else if (nv <= 8) go(std::integral_constant<int, 8>());
+  else go(std::integral_constant<int, 16>());
   return hipGetLastError();
 }
 
