@@ -335,3 +335,51 @@ def test_forward_parity_at_shape_limits(torch, oracle, edge, T):
     assert not torch.isnan(y).any()
     check_close(to_np(y), hl.forward(to_np(x), T), f"edge {edge} T={T}")
     del layer
+
+
+def _random_shapes(n, seed=2024):
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        H = int(rng.choice([128, 256, 384, 512, 1024, 2048]))
+        E = int(rng.choice([1, 2, 3, 7, 16, 33, 64, 100, 256]))
+        k = int(rng.integers(1, min(E, 12) + 1))
+        I = int(rng.choice([128, 256, 384, 512]))
+        Is = int(rng.choice([0, 128, 256, 512]))
+        T = int(rng.choice([1, 2, 3, 7, 16, 17, 64, 65, 255, 256, 300]))
+        out.append((H, E, k, I, Is, T))
+    return out
+
+
+@pytest.mark.parametrize("H,E,k,I,Is,T", _random_shapes(14))
+def test_forward_parity_random_shapes(torch, oracle, H, E, k, I, Is, T):
+    """Seeded random shapes (odd expert counts, k = E, no shared expert,
+    K of one group, token counts either side of every regime boundary):
+    bit-exact routing and forward parity."""
+    import dataclasses
+    from ainfer_amd.moe import MoeLayer, make_input
+    from ainfer_amd.synthetic import CONFIGS
+    print(f"[case] random H={H} E={E} k={k} I={I} Is={Is} T={T}", flush=True)
+    cfg = dataclasses.replace(CONFIGS["c0"], name=f"rnd_{H}_{E}_{k}_{I}_{Is}", hidden=H,
+                              n_experts=E, top_k=k, inter=I, shared_inter=Is)
+    _layers.clear()
+    torch.cuda.empty_cache()
+    layer = MoeLayer(cfg)
+    x = make_input(cfg, T, tag=T + E)
+    ws = layer.workspace(T)
+    hl = host_copy(oracle, layer)
+    idx, w, sg, lg = layer.route(x, ws, want_logits=True)
+    counts, offsets, perm, inv = layer.dispatch(idx, ws)
+    torch.cuda.synchronize()
+    r_idx, r_w, r_sg, r_lg = hl.route(to_np(x), T)
+    assert np.array_equal(to_np(lg).view(np.uint32), r_lg.view(np.uint32)), "logits"
+    assert np.array_equal(to_np(idx), r_idx), "top-k"
+    c, o, p, iv = oracle.dispatch(r_idx, E)
+    assert np.array_equal(to_np(perm), p) and np.array_equal(to_np(counts), c)
+    y = torch.full((T, H), float("nan"), dtype=torch.bfloat16, device="cuda")
+    layer.forward(x, y, ws)
+    torch.cuda.synchronize()
+    assert not torch.isnan(y).any()
+    check_close(to_np(y), hl.forward(to_np(x), T), f"random {H},{E},{k},{I},{Is} T={T}")
+    assert layer.workspace_check(ws) == 0
+    del layer
