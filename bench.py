@@ -183,6 +183,131 @@ def run_gemv_w4a8(steps, copies=8, M=17408, K=5120):
             "reference_b60_replay_us": 283.0}
 
 
+def run_c3(steps, warmup=5):
+    """H4096 E512 k10 I1024 + shared, 64 tokens (the
+    16-token-tile streaming kernels).  One layer is 3.3 GB, far above the
+    256 MB MALL, so one copy suffices."""
+    import torch
+    from ainfer_amd.moe import MoeLayer, make_input
+    from ainfer_amd.synthetic import CONFIGS, algorithmic_bytes
+    cfg, T = CONFIGS["c3"], 64
+    layer = MoeLayer(cfg)
+    xs = [make_input(cfg, T, tag=3000 + i) for i in range(8)]
+    ws = layer.workspace(T)
+    y = torch.empty(T, cfg.hidden, dtype=torch.bfloat16, device="cuda")
+    for i in range(warmup):
+        layer.forward(xs[i % 8], y, ws)
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for i in range(steps):
+        layer.forward(xs[i % 8], y, ws)
+    t1.record()
+    torch.cuda.synchronize()
+    us = t0.elapsed_time(t1) * 1e3 / steps
+    U = sum(unique_experts(layer, x, ws) for x in xs) / len(xs)
+    nbytes = algorithmic_bytes(cfg, T, round(U))
+    out = {"us_per_step": round(us, 2), "us_per_token": round(us / T, 3), "unique_experts": U,
+           "alg_bytes": nbytes, "layer_hbm_gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+           "layer_hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    del layer, ws, xs, y
+    torch.cuda.empty_cache()
+    return out
+
+
+def run_c4(steps, tokens=(1, 8), warmup=3):
+    """60 blocks of config 3 (RMSNorm -> MoE -> residual,
+    ainfer_moe_block_forward), one decode step = all 60 blocks in sequence on
+    a bf16 residual stream; 200 GB of weights resident."""
+    import torch
+    from ainfer_amd.moe import MoeLayer, make_input
+    from ainfer_amd.synthetic import CONFIGS, algorithmic_bytes
+    cfg = CONFIGS["c4"]
+    layers = [MoeLayer(cfg, layer=i) for i in range(cfg.layers)]
+    torch.cuda.synchronize()
+    out = {}
+    for T in tokens:
+        ws = layers[0].workspace(T)
+        r0 = make_input(cfg, T, tag=4000 + T) * 4
+        a, b = r0.clone(), torch.empty_like(r0)
+        # distinct routed experts per layer along the actual residual stream
+        U = 0.0
+        h = torch.empty_like(r0)
+        from ainfer_amd.moe import rmsnorm
+        cur = r0.clone()
+        for L_ in layers:
+            rmsnorm(cur, h)
+            U += unique_experts(L_, h, ws)
+            nxt = torch.empty_like(cur)
+            L_.block_forward(cur, nxt, ws)
+            cur = nxt
+        for _ in range(warmup):
+            for L_ in layers:
+                L_.block_forward(a, b, ws)
+                a, b = b, a
+        torch.cuda.synchronize()
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        a.copy_(r0)
+        t0.record()
+        for _ in range(steps):
+            for L_ in layers:
+                L_.block_forward(a, b, ws)
+                a, b = b, a
+        t1.record()
+        torch.cuda.synchronize()
+        us = t0.elapsed_time(t1) * 1e3 / steps
+        nbytes = sum(algorithmic_bytes(cfg, T, 0) for _ in layers) + round(U) * cfg.expert_bytes()
+        out[str(T)] = {"us_per_step": round(us, 1), "us_per_token": round(us / T, 2),
+                       "unique_experts_per_layer": round(U / len(layers), 2),
+                       "alg_bytes_per_step": nbytes,
+                       "hbm_gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+                       "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        del ws
+    del layers
+    torch.cuda.empty_cache()
+    return out
+
+
+def measured_peaks():
+    """What this box sustains, beside the spec peaks: a 1 GiB device copy
+    (read + write bytes) and a bf16 8192^3 GEMM through the vendor BLAS."""
+    import torch
+    n = 1 << 30
+    src = torch.ones(n, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(10):
+        dst.copy_(src)
+    t1.record()
+    torch.cuda.synchronize()
+    copy_gbs = 2 * n * 10 / (t0.elapsed_time(t1) * 1e-3) / 1e9
+    del src, dst
+    m = 8192
+    a = torch.randn(m, m, device="cuda", dtype=torch.bfloat16)
+    b = torch.randn(m, m, device="cuda", dtype=torch.bfloat16)
+    for _ in range(3):
+        c = a @ b
+    torch.cuda.synchronize()
+    t0.record()
+    for _ in range(10):
+        c = a @ b
+    t1.record()
+    torch.cuda.synchronize()
+    tfs = 2 * m ** 3 * 10 / (t0.elapsed_time(t1) * 1e-3) / 1e12
+    del a, b, c
+    torch.cuda.empty_cache()
+    return {"hbm_copy_gbs": round(copy_gbs, 1), "hbm_copy_frac_of_spec": round(copy_gbs / HBM_PEAK_GBS, 4),
+            "bf16_gemm_8192_tflops": round(tfs, 1),
+            "bf16_gemm_frac_of_spec": round(tfs / MFMA_BF16_PEAK_TFS, 4)}
+
+
 def cpu_baseline(layer, cfg, T, budget_s):
     """The C oracle on host cores, bounded to about budget_s seconds."""
     import numpy as np
@@ -228,6 +353,9 @@ def main():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemv", action="store_true", help="skip the W4A8 GEMV line")
+    ap.add_argument("--no-c3", action="store_true", help="skip config 3 (H4096, 64 tokens)")
+    ap.add_argument("--no-c4", action="store_true", help="skip config 4 (60-layer stack, 200 GB)")
+    ap.add_argument("--no-peaks", action="store_true", help="skip the measured-peak probes")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="finally copy MIB MiB device-to-device 5 times (PMC calibration)")
@@ -307,6 +435,19 @@ def main():
         gemv = run_gemv_w4a8(args.steps)
         log(f"[bench]   {json.dumps(gemv)}")
 
+    c3 = run_c3(min(args.steps, 100)) if not args.no_c3 else None
+    if c3:
+        log(f"[bench] c3 T=64: {json.dumps(c3)}")
+    c4 = None
+    if not args.no_c4:
+        del layers
+        torch.cuda.empty_cache()
+        log("[bench] c4: 60-layer stack, T=1 and 8")
+        c4 = run_c4(max(3, min(args.steps // 20, 20)))
+        log(f"[bench]   {json.dumps(c4)}")
+        layers = [MoeLayer(c1, layer=0)]
+    peaks = measured_peaks() if not args.no_peaks else None
+
     if args.calib_copy > 0:
         n = args.calib_copy << 20
         src = torch.ones(n, dtype=torch.uint8, device="cuda")
@@ -317,7 +458,8 @@ def main():
         log(f"[bench] calibration copy: 5 x {n} bytes")
 
     if not decode:
-        print(json.dumps({"prefill_c2_T4096": prefill, "gemv_w4a8": gemv}), flush=True)
+        print(json.dumps({"prefill_c2_T4096": prefill, "gemv_w4a8": gemv, "c3_T64": c3,
+                          "c4_stack60": c4, "measured_peaks": peaks}), flush=True)
         return
     Th = 16 if 16 in decode else max(decode)
     d1 = decode[Th]
@@ -357,6 +499,9 @@ def main():
                                 for k, v in d.items()} for T, d in decode.items()},
             "prefill_c2_T4096": prefill,
             "gemv_w4a8": gemv,
+            "c3_T64": c3,
+            "c4_stack60": c4,
+            "measured_peaks": peaks,
         },
     }
     print(json.dumps(out), flush=True)
