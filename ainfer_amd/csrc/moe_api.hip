@@ -264,9 +264,9 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
     } else {
       // bandwidth-bound: three launches whose items hold no waits
       const int mtb = max_tiles_bound(*s, T, DEC_MT);
-      HIP_TRY(launch_expert_stream(0, s->scale_dtype, gu, mtb, 4, RG_GATE_UP, DEC_MT, st));
+      HIP_TRY(launch_expert_stream(0, s->scale_dtype, gu, mtb, 4, DEC_RG_GATE_UP, DEC_MT, st));
       pc->end(4);
-      HIP_TRY(launch_expert_stream(1, s->scale_dtype, dn, mtb, 2, RG_DOWN, DEC_MT, st));
+      HIP_TRY(launch_expert_stream(1, s->scale_dtype, dn, mtb, DEC_KBW_DOWN, DEC_RG_DOWN, DEC_MT, st));
       pc->end(5);
       HIP_TRY(launch_combine(at<uint16_t>(ws, L.o), d.inv, at<float>(ws, L.w), at<float>(ws, L.sg),
                              has_shared, resid, y, T, k, H, st));

@@ -32,6 +32,54 @@ __device__ __forceinline__ float scale_to_f32(uint16_t s) {
     return bf16_to_f32(s);
 }
 
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// 16 blocks of D (4x4) += A (4x4) B (4x4), bf16 in, fp32 out.  Block b:
+// A row i in lane 4b + i, B column j in lane 4b + j (register = k), D
+// element (i, j) in lane 4b + j, register i.
+__device__ __forceinline__ f32x4 mfma_bf16_4x4x4(s16x4 a, s16x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a, b, c, 0, 0, 0);
+}
+
+// Sums over the lanes that differ only in the bits of lane mask M and below
+// (down to bit 2), halving the values a lane holds at each bit: the lane
+// with the bit clear keeps the lower half and receives its partner's lower
+// half, the other the upper.  Bits 5 and 4 swap through permlane32/16_swap,
+// bits 3 and 2 through ds_swizzle.
+template <int N, int M>
+struct HalveSum {
+  // one halving step over lane mask M: v[0, N/2) <- kept half + partner's
+  static __device__ __forceinline__ void step(float *v, int lane) {
+    constexpr int h = N / 2;
+#pragma unroll
+    for (int i = 0; i < h; ++i) {
+      if constexpr (M == 32 || M == 16) {
+        const u32x2 r = M == 32 ? __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]),
+                                                                   __float_as_uint(v[h + i]),
+                                                                   false, false)
+                                : __builtin_amdgcn_permlane16_swap(__float_as_uint(v[i]),
+                                                                   __float_as_uint(v[h + i]),
+                                                                   false, false);
+        v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+      } else {
+        const bool up = lane & M;
+        const float keep = up ? v[h + i] : v[i], send = up ? v[i] : v[h + i];
+        v[i] = keep + __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(send),
+                                                                 (M << 10) | 0x1F));
+      }
+    }
+  }
+  static __device__ __forceinline__ void run(float *v, int lane) {
+    step(v, lane);
+    HalveSum<N / 2, M / 2>::run(v, lane);
+  }
+};
+template <int N>
+struct HalveSum<N, 2> {
+  static __device__ __forceinline__ void run(float *, int) {}
+};
+
 __device__ __forceinline__ f32x4 mfma_bf16_16x16x32(u32x4 a, u32x4 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
                                                  __builtin_bit_cast(bf16x8_t, b), c,

@@ -57,6 +57,9 @@ __device__ unsigned long long g_dtrace[2][1 << 15][5];
 extern "C" int ainfer_debug_trace(void *host) {
   return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_dtrace), sizeof(g_dtrace)) == hipSuccess ? 0 : -1;
 }
+extern "C" int ainfer_debug_land(void *host) {
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_dland), sizeof(g_dland)) == hipSuccess ? 0 : -1;
+}
 #else
 #define DTRACE(K, I)
 #define DTRACE_AT(K, X, I)
@@ -475,12 +478,8 @@ int decode_geometry(const ainfer_moe_shape &s, DecodeGeom *g) {
   g->slabs_gu = (Ngu + 16 * DEC_RG_GU * g->wr_gu - 1) / (16 * DEC_RG_GU * g->wr_gu);
   g->slabs_dn = (s.hidden + 16 * DEC_RG_DN * g->wr_dn - 1) / (16 * DEC_RG_DN * g->wr_dn);
   // A staging only: the K-split partials reuse it (expert_lds_item, COH)
-  auto item_lds = [&](int kbw, int rg, int halves) {
-    const size_t aw = (size_t)DEC_MT * kbw * 256, part = (size_t)halves * rg * 1024;
-    return (size_t)g->nw * (aw + (aw >= part ? 0 : part));
-  };
-  const size_t lds_gu = item_lds(4, DEC_RG_GU, 2);
-  const size_t lds_dn = item_lds(2, DEC_RG_DN, 1);
+  const size_t lds_gu = (size_t)g->nw * item_lds_per_wave(DEC_MT, 4, DEC_RG_GU, 0);
+  const size_t lds_dn = (size_t)g->nw * item_lds_per_wave(DEC_MT, 2, DEC_RG_DN, 1);
   g->lds = lds_gu > lds_dn ? lds_gu : lds_dn;
   if (g->lds > 64 * 1024) return 0;
   return 1;

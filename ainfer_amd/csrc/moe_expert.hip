@@ -187,6 +187,12 @@ __global__ __launch_bounds__(1024) void k_expert_lds(ExpertArgs a) {
 
 }  // namespace
 
+#ifdef AINFER_DECODE_TRACE
+extern "C" int ainfer_debug_land_expert(void *host) {
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_dland), sizeof(g_dland)) == hipSuccess ? 0 : -1;
+}
+#endif
+
 // KBW k-groups per wave (the preferred count, raised until one row group
 // fits in 16 waves, lowered until it divides both K group counts), WK =
 // waves along K, WR = row groups per block.
@@ -257,8 +263,7 @@ hipError_t launch_expert_stream(int mode, int scale_dtype, ExpertArgs a, int max
   size_t lds = sizeof(float) * 2 * (size_t)a.WK * a.WR * rg * 256;
   if (mt == DEC_MT) {
     // A staging; the K-split partials reuse it when they fit (expert_lds_item, ALIAS)
-    const size_t aw = (size_t)DEC_MT * kbw * 256, part = (size_t)(mode == 0 ? 2 : 1) * rg * 1024;
-    lds = (size_t)a.WK * a.WR * (aw + (aw >= part ? 0 : part));
+    lds = (size_t)a.WK * a.WR * item_lds_per_wave(DEC_MT, kbw, rg, mode);
   }
   if (lds > 160 * 1024) return hipErrorInvalidValue;
   const long grid = (long)max_tiles * a.n_slabs;

@@ -124,6 +124,17 @@ bool expert_geometry(int mode, int H, int I, int Is, int pref_kbw, int *KBW, int
 #ifndef RG_DOWN
 #define RG_DOWN 2
 #endif
+// the same for the decode tiles (T > FUSED_EXPERTS_MAX_T), and the down
+// items' preferred k-groups per wave
+#ifndef DEC_RG_GATE_UP
+#define DEC_RG_GATE_UP 1
+#endif
+#ifndef DEC_RG_DOWN
+#define DEC_RG_DOWN 2
+#endif
+#ifndef DEC_KBW_DOWN
+#define DEC_KBW_DOWN 2
+#endif
 // rg: 16-row groups per wave (1, 2 or 4) sharing one load of the token rows;
 // mt: tokens per tile the dispatch produced (DEC_MT: A staged in LDS, or SMALL_MT)
 hipError_t launch_expert_stream(int mode, int scale_dtype, ExpertArgs a, int max_tiles,
@@ -131,6 +142,16 @@ hipError_t launch_expert_stream(int mode, int scale_dtype, ExpertArgs a, int max
 
 // tile height of the small-M expert kernels
 constexpr int SMALL_MT = 16;
+// LDS bytes per wave of a decode expert item (moe_expert_item.h): its A
+// rows (MT x KBW * 256 B), its scales (KBW >= 2: one dword DMA per 256 B),
+// and its K-split partials where they do not fit the A rows.
+__host__ __device__ constexpr int item_scale_lds(int kbw, int rg, int mode) {
+  return kbw >= 2 ? ((mode == 0 ? 2 : 1) * rg * 16 * kbw * 2 + 255) / 256 * 256 : 0;
+}
+__host__ __device__ constexpr int item_lds_per_wave(int mt, int kbw, int rg, int mode) {
+  return mt * kbw * 256 + item_scale_lds(kbw, rg, mode) +
+         (mt * kbw * 256 >= (mode == 0 ? 2 : 1) * rg * 1024 ? 0 : (mode == 0 ? 2 : 1) * rg * 1024);
+}
 constexpr int DEC_MT = 4;  // tile rows of the decode dispatch (T <= EXACT_ROUTER_MAX_T)
 // largest T routed by the fused top-k + dispatch launch
 constexpr int FUSED_DISPATCH_MAX_T = 64;
