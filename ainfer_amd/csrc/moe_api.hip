@@ -260,7 +260,7 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
       HIP_TRY(launch_experts_decode(s->scale_dtype, dg, gu, dn, at<float>(ws, L.w),
                                     at<float>(ws, L.sg), d.inv, resid, y, sync,
                                     max_tiles_bound(*s, T, DEC_MT),
-                                    max_tiles_bound(*s, DECODE_MAX_T, DEC_MT), st));
+                                    max_tiles_bound(*s, DECODE_MAX_T, DEC_MT), T == 1, st));
     } else {
       // bandwidth-bound: three launches whose items hold no waits
       const int mtb = max_tiles_bound(*s, T, DEC_MT);

@@ -1,10 +1,11 @@
-// moe_decode.hip - the decode layer (T <= 16 tokens) in two launches.
+// moe_decode.hip - the decode routing kernel (T <= 16 tokens) and the fused
+// expert kernel (T <= 2).
 //
 // Measured on MI355X: a dependent kernel launch costs about 2.5 us, a flag
 // handed from one workgroup to another through device memory about 0.8 us,
 // same-address device atomics serialise at about 11 ns each, and an
 // agent-scope release or acquire fence (a whole-L2 write-back or
-// invalidate) about 20 ns, serialised.  So the decode layer is two kernels
+// invalidate) about 20 ns, serialised.  So at T = 2 the layer is two kernels
 // whose stages meet through counters that few workgroups touch, with data
 // handed over by sc1 stores and loads instead of fences (moe_common.h):
 //
@@ -26,7 +27,10 @@
 //                   the tile's act rows, writes its o rows, and counts one
 //                   arrival per (token, row slab).  The (k+1)-th arrival of a
 //                   (token, slab) sums the token's k + 1 rows of that slab in
-//                   slot order (the combine).
+//                   slot order (the combine).  At T = 1 the gate/up items
+//                   run first in a launch of their own (k_expert_lds) and
+//                   this kernel holds only the down items, which then wait
+//                   for nothing.
 //
 // A wait only ever names work of lower workgroup index, and workgroups are
 // dispatched in index order, so every awaited workgroup is already running.
@@ -87,9 +91,6 @@ constexpr int SPIN_MAX = 1 << 20;
 #endif
 #ifndef DEC_RG_DN
 #define DEC_RG_DN 2  // 16-row groups per wave, down items
-#endif
-#ifndef DEC_SPLIT
-#define DEC_SPLIT 0  // 1: gate/up in a launch of its own before the down items
 #endif
 
 __device__ __forceinline__ bool spin_until_geq(const int32_t *p, int target) {
@@ -536,7 +537,8 @@ hipError_t launch_route_decode(const void *x, const void *rw, const float *bias,
 hipError_t launch_experts_decode(int scale_dtype, const DecodeGeom &g, ExpertArgs gu,
                                  ExpertArgs dn, const float *w, const float *sg,
                                  const int32_t *inv, const void *resid, void *y,
-                                 int32_t *sync, int max_tiles, int cap, hipStream_t s) {
+                                 int32_t *sync, int max_tiles, int cap, bool split,
+                                 hipStream_t s) {
   if (max_tiles <= 0) return hipSuccess;
   if (max_tiles > cap) return hipErrorInvalidValue;
   ExpertsDecodeArgs a;
@@ -560,7 +562,7 @@ hipError_t launch_experts_decode(int scale_dtype, const DecodeGeom &g, ExpertArg
   const long grid = (long)max_tiles * (g.slabs_gu + g.slabs_dn);
   if (grid > 0x7FFFFFFF) return hipErrorInvalidValue;
   const int threads = g.nw * 64;
-  if (DEC_SPLIT) {
+  if (split) {
     // gate/up in its own launch, then the down items with the combine
     hipError_t e = launch_expert_stream(0, scale_dtype, gu, max_tiles, 4, DEC_RG_GU, DEC_MT, s);
     if (e != hipSuccess) return e;

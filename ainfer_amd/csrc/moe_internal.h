@@ -189,9 +189,13 @@ hipError_t launch_route_decode(const void *x, const void *rw, const float *bias,
                                void *xperm, int T, int H, int E, int k, int has_shared,
                                const DispatchOut *ds, int32_t *sync, uint32_t *slots,
                                hipStream_t s);
-// gate/up + SiLU, down and the combine (y = sum_j w_j o_j + g_s o_s (+ resid))
+// gate/up + SiLU, down and the combine (y = sum_j w_j o_j + g_s o_s (+ resid));
+// split: gate/up in a launch of its own first (measured faster at T = 1,
+// where the down items of a fused launch wait behind the gate/up items for
+// workgroup slots: c3 39.5 -> 33.0 us, c1 equal)
 hipError_t launch_experts_decode(int scale_dtype, const DecodeGeom &g, ExpertArgs gu,
                                  ExpertArgs dn, const float *w, const float *sg,
                                  const int32_t *inv, const void *resid, void *y,
-                                 int32_t *sync, int max_tiles, int cap, hipStream_t s);
+                                 int32_t *sync, int max_tiles, int cap, bool split,
+                                 hipStream_t s);
 hipError_t launch_zero_i32(int32_t *p, int n, hipStream_t s);
