@@ -13,7 +13,7 @@ __device__ __forceinline__ void dispatch_small_block(const int32_t *__restrict__
   __shared__ unsigned long long mask[1024];
   __shared__ int scan_c[256], scan_t[256];
   __shared__ int off_lds[1024];
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, mt = ds.mt;  // tokens per tile (T / mt <= 256)
   for (int e = tid; e < E; e += 256) mask[e] = 0ull;
   __syncthreads();
   for (int i = tid; i < T * k; i += 256)
@@ -26,7 +26,7 @@ __device__ __forceinline__ void dispatch_small_block(const int32_t *__restrict__
   for (int e = e0; e < e0 + per && e < E; ++e) {
     const int c = __popcll(mask[e]);
     c_loc += c;
-    t_loc += (c + SMALL_MT - 1) / SMALL_MT;
+    t_loc += (c + mt - 1) / mt;
   }
   scan_c[tid] = c_loc;
   scan_t[tid] = t_loc;
@@ -45,16 +45,13 @@ __device__ __forceinline__ void dispatch_small_block(const int32_t *__restrict__
     ds.counts[e] = c;
     ds.offsets[e] = off_e;
     off_lds[e] = off_e;
-    for (int m0 = 0; m0 < c; m0 += SMALL_MT)
-      ds.tiles[tile++] = make_int4(e, off_e + m0, min(SMALL_MT, c - m0), 0);
+    for (int m0 = 0; m0 < c; m0 += mt) ds.tiles[tile++] = make_int4(e, off_e + m0, min(mt, c - m0), 0);
     off_e += c;
   }
   const int routed_tiles = scan_t[255];
   if (tid == 0) ds.offsets[E] = scan_c[255];
-  const int nsh = has_shared ? (T + SMALL_MT - 1) / SMALL_MT : 0;
-  if (tid < nsh)
-    ds.tiles[routed_tiles + tid] =
-        make_int4(E, tid * SMALL_MT, min(SMALL_MT, T - tid * SMALL_MT), 0);
+  const int nsh = has_shared ? (T + mt - 1) / mt : 0;
+  if (tid < nsh) ds.tiles[routed_tiles + tid] = make_int4(E, tid * mt, min(mt, T - tid * mt), 0);
   if (tid == 0) *ds.n_tiles = routed_tiles + nsh;
   __syncthreads();
   // placement: rank of token t among the tokens of expert e

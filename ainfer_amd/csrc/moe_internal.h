@@ -78,6 +78,7 @@ struct DispatchOut {
   int4 *tiles2;
   int32_t *n_tiles2;
   int small_max;
+  int mt;  // tokens per tile of dispatch_small_block
 };
 
 hipError_t launch_fill(int kind, uint64_t seed, float std_, size_t n, void *out,
@@ -155,6 +156,7 @@ __host__ __device__ constexpr int item_lds_per_wave(int mt, int kbw, int rg, int
 constexpr int DEC_MT = 4;  // tile rows of the decode dispatch (T <= EXACT_ROUTER_MAX_T)
 // largest T routed by the fused top-k + dispatch launch
 constexpr int FUSED_DISPATCH_MAX_T = 64;
+
 
 // ---- decode layer in two launches (moe_decode.hip), T <= DECODE_MAX_T ----
 constexpr int DECODE_MAX_T = EXACT_ROUTER_MAX_T;
