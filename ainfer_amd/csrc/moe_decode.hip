@@ -75,10 +75,18 @@ constexpr int RD_WAVES = 16;  // waves per k_route_decode workgroup
 // Router units: one router row x TT tokens per wave (TT = 1 up to
 // RD_TT1_MAX tokens, else 2: more, shorter units shorten the routing at few
 // tokens; measured at T = 1, 4, 16 against 2 rows x 4 tokens: -2.9, -3.4,
-// -0.5 us per layer).
+// -0.5 us per layer).  At TT = 1 the workgroups have RD_W1 waves and a lane
+// issues the loads of its whole row at once (c3 T=1: -1 us).
 constexpr int RD_R = 1;       // router rows per wave
 constexpr int RD_TT1_MAX = 4;
 constexpr int RD_NB = 2;      // 8-element chunks per lane whose loads are issued together
+#ifndef RD_W1
+#define RD_W1 4    // waves per workgroup at T <= RD_TT1_MAX (the rows spread over more CUs)
+#endif
+#ifndef RD_NB1
+#define RD_NB1 8   // chunks in flight at T <= RD_TT1_MAX: a whole row up to H = 4096
+#endif
+static_assert(RD_W1 >= RD_TT1_MAX, "the selection runs one wave per token");
 constexpr int SPIN_MAX = 1 << 20;
 #ifndef DEC_WAVES_PER_SIMD
 #define DEC_WAVES_PER_SIMD 6  // register budget of the expert kernel (<= 80 VGPRs)
@@ -134,13 +142,14 @@ struct RouteDecodeArgs {
 // Dispatch of T <= 32 tokens by one workgroup (idx in LDS): 32-bit token masks
 // per expert (order-free atomic OR), counts, a workgroup exclusive scan over
 // experts, tiles of at most DEC_MT tokens, perm / inv / ptok.
+template <int W>
 __device__ __forceinline__ void dispatch_decode(const int32_t *__restrict__ idx, int T, int k,
                                                 int E, int has_shared, const DispatchOut &ds) {
   __shared__ uint32_t msk[1024];
   __shared__ int offl[1024];
-  __shared__ int wsum[RD_WAVES];
+  __shared__ int wsum[W];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  constexpr int NT = RD_WAVES * 64;
+  constexpr int NT = W * 64;
   for (int e = tid; e < E; e += NT) msk[e] = 0u;
   __syncthreads();
   for (int i = tid; i < T * k; i += NT) atomicOr(&msk[idx[i]], 1u << (i / k));
@@ -159,7 +168,7 @@ __device__ __forceinline__ void dispatch_decode(const int32_t *__restrict__ idx,
   __syncthreads();
   int base = 0, tot = 0;
 #pragma unroll
-  for (int w = 0; w < RD_WAVES; ++w) {
+  for (int w = 0; w < W; ++w) {
     const int v = wsum[w];
     base += w < wv ? v : 0;
     tot += v;
@@ -191,11 +200,13 @@ __device__ __forceinline__ void dispatch_decode(const int32_t *__restrict__ idx,
   }
 }
 
-template <int NV, int RD_TT>
-__global__ __launch_bounds__(RD_WAVES * 64) void k_route_decode(RouteDecodeArgs a) {
-  __shared__ uint64_t s_cand[RD_WAVES][68];
-  __shared__ uint64_t s_sel[RD_WAVES][16];
-  __shared__ int s_idx[RD_WAVES * 32];
+// W waves per workgroup (T <= W: the selection runs one wave per token), NB
+// chunks of 8 per lane whose loads are issued together
+template <int NV, int RD_TT, int W, int NB>
+__global__ __launch_bounds__(W * 64) void k_route_decode(RouteDecodeArgs a) {
+  __shared__ uint64_t s_cand[W][68];
+  __shared__ uint64_t s_sel[W][16];
+  __shared__ int s_idx[W * 32];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int T = a.T, H = a.H, E = a.E, k = a.k;
   DTRACE(0, 0);
@@ -205,7 +216,7 @@ __global__ __launch_bounds__(RD_WAVES * 64) void k_route_decode(RouteDecodeArgs 
     // butterfly (the oracle's mo_router_dot) ---------------------------------
     const int nrows = E + (a.gw ? 1 : 0);
     const int ngroups = (nrows + RD_R - 1) / RD_R;
-    const int u = blockIdx.x * RD_WAVES + wave;
+    const int u = blockIdx.x * W + wave;
     const int rbase = (u % ngroups) * RD_R, t0 = (u / ngroups) * RD_TT;
     if (t0 < T) {
       const uint16_t *wr[RD_R];
@@ -220,12 +231,12 @@ __global__ __launch_bounds__(RD_WAVES * 64) void k_route_decode(RouteDecodeArgs 
       for (int i = 0; i < RD_R; ++i)
 #pragma unroll
         for (int j = 0; j < RD_TT; ++j) acc[i][j] = 0.0f;
-      // RD_NB chunks' loads in flight at once; the sums still run over
+      // NB chunks' loads in flight at once; the sums still run over
       // chunks l, l + 64, ... in order
-      for (int cb = lane; cb < nch; cb += 64 * RD_NB) {
-        u32x4 wv[RD_NB][RD_R], xv[RD_NB][RD_TT];
+      for (int cb = lane; cb < nch; cb += 64 * NB) {
+        u32x4 wv[NB][RD_R], xv[NB][RD_TT];
 #pragma unroll
-        for (int b = 0; b < RD_NB; ++b) {
+        for (int b = 0; b < NB; ++b) {
           const int c = min(cb + 64 * b, nch - 1);
 #pragma unroll
           for (int i = 0; i < RD_R; ++i) wv[b][i] = *(const u32x4 *)(wr[i] + (size_t)c * 8);
@@ -234,7 +245,7 @@ __global__ __launch_bounds__(RD_WAVES * 64) void k_route_decode(RouteDecodeArgs 
             xv[b][j] = *(const u32x4 *)(a.x + (size_t)min(t0 + j, T - 1) * H + (size_t)c * 8);
         }
 #pragma unroll
-        for (int b = 0; b < RD_NB; ++b) {
+        for (int b = 0; b < NB; ++b) {
           // past the row end: computed on a clamped chunk and discarded, so
           // no load depends on a branch
           const bool in = cb + 64 * b < nch;
@@ -274,7 +285,7 @@ __global__ __launch_bounds__(RD_WAVES * 64) void k_route_decode(RouteDecodeArgs 
     DTRACE(0, 1);
     return;
   }
-  // ---- the selection workgroup: one wave per token (T <= RD_WAVES) --------
+  // ---- the selection workgroup: one wave per token (T <= W) ---------------
   const int t = wave;
   // the MFMA-order copy of x does not depend on the routing
   if (t < T && a.xperm) write_xperm(a.x + (size_t)t * H, a.xperm, nullptr, t, H, lane);
@@ -319,7 +330,7 @@ __global__ __launch_bounds__(RD_WAVES * 64) void k_route_decode(RouteDecodeArgs 
   }
   DTRACE(0, 2);
   __syncthreads();
-  if (a.ds.tiles) dispatch_decode(s_idx, T, k, E, a.has_shared, a.ds);
+  if (a.ds.tiles) dispatch_decode<W>(s_idx, T, k, E, a.has_shared, a.ds);
   DTRACE(0, 3);
   // off the critical path: the logits output, and the slots cleared for
   // the next call
@@ -516,15 +527,16 @@ hipError_t launch_route_decode(const void *x, const void *rw, const float *bias,
   const int nrows = E + (gw ? 1 : 0);
   const int tt = T <= RD_TT1_MAX ? 1 : 2;
   const int units = (nrows + RD_R - 1) / RD_R * ((T + tt - 1) / tt);
-  a.NR = (units + RD_WAVES - 1) / RD_WAVES;
+  const int wg = tt == 1 ? RD_W1 : RD_WAVES;
+  a.NR = (units + wg - 1) / wg;
   const unsigned grid = a.NR + 1;
   const int nv = (E + 63) / 64;
   auto go = [&](auto nv_c) {
     constexpr int NVc = decltype(nv_c)::value;
     if (tt == 1)
-      k_route_decode<NVc, 1><<<grid, RD_WAVES * 64, 0, s>>>(a);
+      k_route_decode<NVc, 1, RD_W1, RD_NB1><<<grid, RD_W1 * 64, 0, s>>>(a);
     else
-      k_route_decode<NVc, 2><<<grid, RD_WAVES * 64, 0, s>>>(a);
+      k_route_decode<NVc, 2, RD_WAVES, RD_NB><<<grid, RD_WAVES * 64, 0, s>>>(a);
   };
   if (nv <= 1) go(std::integral_constant<int, 1>());
   else if (nv <= 2) go(std::integral_constant<int, 2>());
