@@ -34,7 +34,8 @@
 #ifdef AINFER_DECODE_TRACE
 __device__ unsigned long long g_strace[4096][8];
 #define STRACE(I) \
-  if ((threadIdx.x & 63) == 0 && t < 4096) g_strace[t][I] = __builtin_amdgcn_s_memrealtime()
+  if ((threadIdx.x & 63) == 0 && (!COOP || threadIdx.x == 0) && t < 4096) \
+  g_strace[t][I] = __builtin_amdgcn_s_memrealtime()
 extern "C" int ainfer_debug_strace(void *host) {
   return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_strace), sizeof(g_strace)) == hipSuccess ? 0 : -1;
 }
@@ -202,7 +203,13 @@ constexpr int SEL_WAVES = 4;
 
 // EXACT: `approx` already holds the canonical logits (k_router_logits) and
 // `sgl` the canonical shared-gate logits; the refine is skipped.
-template <int NV, int CH, bool EXACT>
+// COOP (T < GEMM_MIN_T, where one wave per token leaves most of the chip
+// idle and a token's latency is the kernel's): one token per workgroup.
+// Wave 0 takes the approximate top-k and the candidate list, wave 1 writes
+// the MFMA-order copy of x, wave 2 the shared-gate dot, and the candidates'
+// canonical dots are shared by all waves (c3 T=64: the dots were 13 of 25 us
+// per token).
+template <int NV, int CH, bool EXACT, bool COOP = false>
 __global__ __launch_bounds__(256) void k_select(const float *__restrict__ approx,
                                                 const float *__restrict__ sgl,
                                                 const float *__restrict__ wnorm,
@@ -222,13 +229,18 @@ __global__ __launch_bounds__(256) void k_select(const float *__restrict__ approx
   __shared__ float cv[SEL_WAVES][EXACT ? 1 : 1024];
   __shared__ uint64_t s_cand[SEL_WAVES][64];
   __shared__ uint64_t s_sel[SEL_WAVES][16];
+  __shared__ int s_nc;
+  __shared__ float s_sgv;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int t = blockIdx.x * SEL_WAVES + wave;
+  const int t = COOP ? (int)blockIdx.x : (int)blockIdx.x * SEL_WAVES + wave;
+  const int sw = COOP ? 0 : wave;  // this wave's LDS lists
+  const bool lead = !COOP || wave == 0;
+  static_assert(!(COOP && EXACT), "the cooperative form refines approximate logits");
   if (t < T) {
     // the MFMA-order copy of x (and its group sums) does not depend on the
     // routing: written first, its latency hides under the selection
     STRACE(0);
-    if (xperm) write_xperm(x + (size_t)t * H, xperm, xsum, t, H, lane);
+    if (xperm && (!COOP || wave == 1)) write_xperm(x + (size_t)t * H, xperm, xsum, t, H, lane);
     STRACE(1);
     const float *ar = approx + (size_t)t * E;
     // ---- k-th largest approximate logit -------------------------------
@@ -236,14 +248,15 @@ __global__ __launch_bounds__(256) void k_select(const float *__restrict__ approx
     float wn = 0.0f;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
+      if (!lead) break;
       const int e = lane + 64 * i;
       const float v = ar[min(e, E - 1)];  // unconditional: loads issue together
       key[i] = e < E ? ordered_key(v) : 0u;
       if (!EXACT) wn = fmaxf(wn, e < E ? wnorm[min(e, E - 1)] : 0.0f);
     }
-    int seli;
-    uint32_t selk;
-    wave_topk_fast<NV>(key, E, k, lane, seli, selk, s_cand[wave], s_sel[wave]);
+    int seli = 0;
+    uint32_t selk = 0u;
+    if (lead) wave_topk_fast<NV>(key, E, k, lane, seli, selk, s_cand[sw], s_sel[sw]);
     STRACE(2);
     const uint32_t kth = (uint32_t)__shfl((int)selk, k - 1, 64);
     float selv = 0.0f, sgv = 0.0f;
@@ -271,6 +284,7 @@ __global__ __launch_bounds__(256) void k_select(const float *__restrict__ approx
         }
       }
       for (int m = 32; m >= 1; m >>= 1) xs += __shfl_xor(xs, m, 64);
+      if (COOP && wave == 2 && gw) s_sgv = canon_dot<CH>(xc, gw, lane, nch);
       for (int m = 32; m >= 1; m >>= 1) wn = fmaxf(wn, __shfl_xor(wn, m, 64));
       // ---- candidate threshold --------------------------------------------
       const float lk = key_to_float(kth);
@@ -279,51 +293,62 @@ __global__ __launch_bounds__(256) void k_select(const float *__restrict__ approx
       const float thr = lk - 2.0f * d - 0x1p-21f * (fabsf(lk) + 2.0f * d) - 1e-30f * (float)H;
       // ---- candidate list, expert-ascending -------------------------------
       int nc = 0;
+      if (lead) {
 #pragma unroll
-      for (int i = 0; i < NV; ++i) {
-        const int e = lane + 64 * i;
-        const bool c = e < E && key_to_float(key[i]) >= thr;
-        const uint64_t b = __ballot(c);
-        if (c) cl[wave][nc + __popcll(b & ((1ull << lane) - 1ull))] = e;
-        nc += __popcll(b);
+        for (int i = 0; i < NV; ++i) {
+          const int e = lane + 64 * i;
+          const bool c = e < E && key_to_float(key[i]) >= thr;
+          const uint64_t b = __ballot(c);
+          if (c) cl[sw][nc + __popcll(b & ((1ull << lane) - 1ull))] = e;
+          nc += __popcll(b);
+        }
+        if (COOP && lane == 0) s_nc = nc;
       }
       __builtin_amdgcn_wave_barrier();
+      if (COOP) {
+        __syncthreads();
+        nc = s_nc;
+      }
       STRACE(3);
       // ---- canonical logits of the candidates ------------------------------
       {
-        for (int c0 = 0; c0 < nc; c0 += SEL_NB) {
+        const int cstep = COOP ? SEL_WAVES * SEL_NB : SEL_NB;
+        for (int c0 = COOP ? wave * SEL_NB : 0; c0 < nc; c0 += cstep) {
           const uint16_t *rows[SEL_NB];
           int ee[SEL_NB];
 #pragma unroll
           for (int b = 0; b < SEL_NB; ++b) {
-            ee[b] = cl[wave][min(c0 + b, nc - 1)];
+            ee[b] = cl[sw][min(c0 + b, nc - 1)];
             rows[b] = rw + (size_t)ee[b] * H;
           }
           float v[SEL_NB];
           canon_dot_batch<CH, SEL_NB>(xc, rows, lane, nch, v);
 #pragma unroll
           for (int b = 0; b < SEL_NB; ++b)
-            if (lane == 0 && c0 + b < nc) cv[wave][c0 + b] = bias ? v[b] + bias[ee[b]] : v[b];
+            if (lane == 0 && c0 + b < nc) cv[sw][c0 + b] = bias ? v[b] + bias[ee[b]] : v[b];
         }
       }
       __builtin_amdgcn_wave_barrier();
+      if (COOP) __syncthreads();
       STRACE(4);
       // ---- top-k among candidates (value desc, expert asc) ----------------
-      if (nc <= 64 && k <= 16) {
+      if (!lead) {
+        // helper waves are done
+      } else if (nc <= 64 && k <= 16) {
         // rank of each candidate = candidates above it (unique composite keys)
         auto comp = [&](int i) {
-          return ((uint64_t)ordered_key(cv[wave][i]) << 32) | (uint32_t)~(uint32_t)cl[wave][i];
+          return ((uint64_t)ordered_key(cv[sw][i]) << 32) | (uint32_t)~(uint32_t)cl[sw][i];
         };
         const uint64_t mine = lane < nc ? comp(lane) : 0ull;
         int rk = 0;
         for (int j = 0; j < nc; ++j) rk += comp(j) > mine ? 1 : 0;
-        if (lane < nc && rk < k) s_sel[wave][rk] = ((uint64_t)(uint32_t)lane << 32) | (uint32_t)cl[wave][lane];
+        if (lane < nc && rk < k) s_sel[sw][rk] = ((uint64_t)(uint32_t)lane << 32) | (uint32_t)cl[sw][lane];
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
         if (lane < k) {
-          const uint64_t pk = s_sel[wave][lane];
+          const uint64_t pk = s_sel[sw][lane];
           seli = (int)(uint32_t)pk;
-          selv = cv[wave][(int)(pk >> 32)];
+          selv = cv[sw][(int)(pk >> 32)];
         }
       } else {
       uint32_t tmask = 0;  // taken bits per lane slot (nc <= 1024: 16 slots)
@@ -331,7 +356,7 @@ __global__ __launch_bounds__(256) void k_select(const float *__restrict__ approx
         uint32_t bk = 0;
         int bs = 0x7FFFFFFF;
         for (int i = 0; i < 16 && lane + 64 * i < nc; ++i) {
-          const uint32_t kk = ordered_key(cv[wave][lane + 64 * i]);
+          const uint32_t kk = ordered_key(cv[sw][lane + 64 * i]);
           if (!(tmask & (1u << i)) && (bs == 0x7FFFFFFF || kk > bk)) {
             bk = kk;
             bs = lane + 64 * i;
@@ -341,27 +366,29 @@ __global__ __launch_bounds__(256) void k_select(const float *__restrict__ approx
         const int ws = (int)wave_min_u32(bk == wk && bs != 0x7FFFFFFF ? (uint32_t)bs : 0xFFFFFFFFu);
         if ((ws & 63) == lane) tmask |= 1u << (ws >> 6);
         if (lane == j) {
-          seli = cl[wave][ws];
-          selv = cv[wave][ws];
+          seli = cl[sw][ws];
+          selv = cv[sw][ws];
         }
       }
       }
       STRACE(5);
-      if (gw) sgv = canon_dot<CH>(xc, gw, lane, nch);
+      if (gw) sgv = COOP ? s_sgv : canon_dot<CH>(xc, gw, lane, nch);
       STRACE(6);
     }
-    const float vmax = __shfl(selv, 0, 64);
-    const float p = lane < k ? expf(selv - vmax) : 0.0f;
-    float sum = 0.0f;
-    for (int j = 0; j < k; ++j) sum += __shfl(p, j, 64);
-    if (lane < k) {
-      topk_idx[(size_t)t * k + lane] = seli;
-      topk_w[(size_t)t * k + lane] = p / sum;
+    if (lead) {
+      const float vmax = __shfl(selv, 0, 64);
+      const float p = lane < k ? expf(selv - vmax) : 0.0f;
+      float sum = 0.0f;
+      for (int j = 0; j < k; ++j) sum += __shfl(p, j, 64);
+      if (lane < k) {
+        topk_idx[(size_t)t * k + lane] = seli;
+        topk_w[(size_t)t * k + lane] = p / sum;
+      }
+      // ---- shared gate --------------------------------------------------
+      float g = 1.0f;
+      if (gw) g = 1.0f / (1.0f + expf(-sgv));
+      if (lane == 0) sgate[t] = g;
     }
-    // ---- shared gate ----------------------------------------------------
-    float g = 1.0f;
-    if (gw) g = 1.0f / (1.0f + expf(-sgv));
-    if (lane == 0) sgate[t] = g;
     STRACE(7);
   }
   if (!fused) return;
@@ -481,7 +508,7 @@ __global__ __launch_bounds__(1024) void k_select_small(const float *__restrict__
   if (t == 0) dispatch_wave(s_idx, T, k, E, has_shared, ds, s_msk, s_off, lane);
 }
 
-template <int NV, bool EXACT>
+template <int NV, bool EXACT, bool COOP>
 hipError_t launch_select_nv(int ch, unsigned grid, const float *approx, const float *sgl,
                             const float *wnorm,
                             const void *x, const void *rw, const float *bias, const void *gw,
@@ -492,10 +519,10 @@ hipError_t launch_select_nv(int ch, unsigned grid, const float *approx, const fl
   approx, sgl, wnorm, (const uint16_t *)x, (const uint16_t *)rw, bias, (const uint16_t *)gw, idx, \
       w, sg, (uint16_t *)xperm, xsum, T, E, k, H, has_shared, ds, fused
   switch (ch) {
-  case 1: k_select<NV, 1, EXACT><<<grid, 256, 0, s>>>(SEL_ARGS); break;
-  case 2: k_select<NV, 2, EXACT><<<grid, 256, 0, s>>>(SEL_ARGS); break;
-  case 4: k_select<NV, 4, EXACT><<<grid, 256, 0, s>>>(SEL_ARGS); break;
-  default: k_select<NV, 8, EXACT><<<grid, 256, 0, s>>>(SEL_ARGS); break;
+  case 1: k_select<NV, 1, EXACT, COOP><<<grid, 256, 0, s>>>(SEL_ARGS); break;
+  case 2: k_select<NV, 2, EXACT, COOP><<<grid, 256, 0, s>>>(SEL_ARGS); break;
+  case 4: k_select<NV, 4, EXACT, COOP><<<grid, 256, 0, s>>>(SEL_ARGS); break;
+  default: k_select<NV, 8, EXACT, COOP><<<grid, 256, 0, s>>>(SEL_ARGS); break;
   }
 #undef SEL_ARGS
   return hipGetLastError();
@@ -517,11 +544,17 @@ hipError_t launch_select(const float *approx, const float *sgl, const float *wno
   DispatchOut ds;
   memset(&ds, 0, sizeof ds);
   if (fused) ds = *fused;
-  const unsigned g = (T + SEL_WAVES - 1) / SEL_WAVES;
+  // one token per workgroup below the GEMM path (k_select, COOP)
+  const bool coop = !EXACT && T < GEMM_MIN_T;
+  const unsigned g = coop ? (unsigned)T : (T + SEL_WAVES - 1) / SEL_WAVES;
   const int fz = fused ? 1 : 0;
-#define SEL_CALL(NVV)                                                                        \
-  launch_select_nv<NVV, EXACT>(chp, g, approx, sgl, wnorm, x, rw, bias, gw, idx, w, sg, xperm, \
-                               xsum, T, E, k, H, has_shared, ds, fz, s)
+#define SEL_CALL(NVV)                                                                          \
+  (coop ? launch_select_nv<NVV, EXACT, !EXACT>(chp, g, approx, sgl, wnorm, x, rw, bias, gw, idx, \
+                                              w, sg, xperm, xsum, T, E, k, H, has_shared, ds, \
+                                              fz, s)                                          \
+        : launch_select_nv<NVV, EXACT, false>(chp, g, approx, sgl, wnorm, x, rw, bias, gw, idx, \
+                                              w, sg, xperm, xsum, T, E, k, H, has_shared, ds, \
+                                              fz, s))
   if (nv <= 1) return SEL_CALL(1);
   if (nv <= 2) return SEL_CALL(2);
   if (nv <= 4) return SEL_CALL(4);
@@ -542,7 +575,10 @@ hipError_t launch_router_fast(const void *x, const void *rw, const float *bias, 
     return launch_select<false>(approx, nullptr, wnorm, x, rw, bias, gw, idx, w, sg, xperm,
                                 xsum, T, H, E, k, has_shared, fused, s);
   }
-  const int MS = T <= 16 ? 1 : (T <= 32 ? 2 : 4);
+  // one 16-token tile per workgroup: more workgroups share the token reads
+  // (c3 T=64: 55 -> 44 us against 64-token tiles; the router rows are
+  // re-read from L2)
+  constexpr int MS = 1;
   const int mt = 16 * MS;
   // decode: one token tile, K split over up to 16 waves; prefill: 4 waves
   int NW = T <= 64 ? H / 128 : 4;
@@ -550,18 +586,9 @@ hipError_t launch_router_fast(const void *x, const void *rw, const float *bias, 
   while (NW > 1 && (H % (32 * NW))) --NW;
   const dim3 grid((E + 15) / 16, (T + mt - 1) / mt);
   const size_t lds = sizeof(float) * ((size_t)NW * MS * 256 + NW * 16);
-  if (MS == 1)
-    k_router_mfma<1><<<grid, NW * 64, lds, s>>>((const uint16_t *)x, (const uint16_t *)rw, bias,
-                                                approx, wnorm, fused ? fused->ticket : nullptr,
-                                                T, H, E, NW);
-  else if (MS == 2)
-    k_router_mfma<2><<<grid, NW * 64, lds, s>>>((const uint16_t *)x, (const uint16_t *)rw, bias,
-                                                approx, wnorm, fused ? fused->ticket : nullptr,
-                                                T, H, E, NW);
-  else
-    k_router_mfma<4><<<grid, NW * 64, lds, s>>>((const uint16_t *)x, (const uint16_t *)rw, bias,
-                                                approx, wnorm, fused ? fused->ticket : nullptr,
-                                                T, H, E, NW);
+  k_router_mfma<MS><<<grid, NW * 64, lds, s>>>((const uint16_t *)x, (const uint16_t *)rw, bias,
+                                               approx, wnorm, fused ? fused->ticket : nullptr, T,
+                                               H, E, NW);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
   // ---- refine + select ------------------------------------------------------
