@@ -145,7 +145,7 @@ def test_router_ties_and_degenerate_inputs(torch, oracle):
     layer.set_tensor("router_w", rw0)
 
 
-FWD_CASES = [("c0", 1), ("c1", 1), ("c1", 4), ("c1", 16), ("c3", 64)]
+FWD_CASES = [("c0", 1), ("c1", 1), ("c1", 2), ("c1", 4), ("c1", 16), ("c1", 100), ("c3", 1), ("c3", 64)]
 
 
 @pytest.mark.parametrize("name,T", FWD_CASES)
