@@ -18,6 +18,8 @@
 // float(gs) * s * sq is rounded as the reference rounds it, and the terms
 // are added in group order with no contraction, so each y is bit-identical
 // to the reference formula.
+#include <type_traits>
+
 #include "moe_common.h"
 #include "moe_internal.h"
 
@@ -84,11 +86,15 @@ static_assert(GV_WAVES >= 4, "the ordered sum uses one thread per (row, token) o
 // float(gs) * s * sq of groups w, w + GV_WAVES, ... of each chunk into LDS;
 // then 256 threads, one per (row, token), add them in group order.  y is
 // [T][M] fp32.
-template <int SD>
+// STG: the block's weight scales [16][G] and activation scales [16][G] are
+// staged in LDS once (per-lane 2-byte gathers in every pass cost 3 of 18 us
+// at 17408 x 5120); else they are gathered per group.
+template <int SD, bool STG>
 __global__ __launch_bounds__(GV_WAVES * 64) void k_int4_gemv_i8(
     const uint8_t *__restrict__ P, const uint16_t *__restrict__ S, const int8_t *__restrict__ xq,
     const float *__restrict__ sq, int M, int K, int T, float *__restrict__ y) {
   __shared__ float term[GV_CHUNK][256];
+  extern __shared__ __attribute__((aligned(16))) uint8_t gv_lds[];  // STG: [16][G] f32, [16][G] u16
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int m0 = blockIdx.x * 16, t0 = blockIdx.y * 16;
   const int G = K / 128, qd = lane >> 4, c = lane & 15;
@@ -101,6 +107,16 @@ __global__ __launch_bounds__(GV_WAVES * 64) void k_int4_gemv_i8(
   const uint16_t *sp[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) sp[i] = S + (size_t)min(m0 + 4 * qd + i, M - 1) * G;
+  float *sq_l = (float *)gv_lds;
+  uint16_t *sc_l = (uint16_t *)(gv_lds + 16 * G * 4);
+  if constexpr (STG) {
+    for (int i = threadIdx.x; i < 16 * G; i += GV_WAVES * 64) {
+      const int r = i / G, g = i - r * G;
+      sc_l[i] = S[(size_t)min(m0 + r, M - 1) * G + g];
+      sq_l[i] = sq[(size_t)min(t0 + r, T - 1) * G + g];
+    }
+    __syncthreads();
+  }
   const i32x4 ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
   const i32x4 zero = {0, 0, 0, 0};
   float acc = 0.0f;
@@ -117,18 +133,28 @@ __global__ __launch_bounds__(GV_WAVES * 64) void k_int4_gemv_i8(
       wv[jj] = __builtin_nontemporal_load((const u32x4 *)(wp + (size_t)g * 64));
       xav[jj] = *(const u32x4 *)(xp + (size_t)g * 128);
       xbv[jj] = *(const u32x4 *)(xp + (size_t)g * 128 + 16);
+      if constexpr (!STG) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) scv[jj][i] = sp[i][g];
-      sqv[jj] = sqp[g];
+        for (int i = 0; i < 4; ++i) scv[jj][i] = sp[i][g];
+        sqv[jj] = sqp[g];
+      }
     }
 #pragma unroll
     for (int jj = 0; jj < GV_GPW; ++jj) {
       const int j = wave + jj * GV_WAVES;
       const u32x4 w = wv[jj], xa = xav[jj], xb = xbv[jj];
       float sc[4];
+      float sqg;
+      if constexpr (STG) {
+        const int g = c0 + min(j, cn - 1);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) sc[i] = scale_to_f32<SD>(scv[jj][i]);
-      const float sqg = sqv[jj];
+        for (int i = 0; i < 4; ++i) sc[i] = scale_to_f32<SD>(sc_l[(4 * qd + i) * G + g]);
+        sqg = sq_l[c * G + g];
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sc[i] = scale_to_f32<SD>(scv[jj][i]);
+        sqg = sqv[jj];
+      }
       i32x4 a0, a1, b0, b1;
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
@@ -187,11 +213,20 @@ hipError_t launch_act_quant_i8(const void *x, int x_dtype, int T, int K, int8_t 
 hipError_t launch_int4_gemv_i8(const uint8_t *P, const void *S, int scale_dtype, const int8_t *xq,
                                const float *sq, int M, int K, int T, float *y, hipStream_t s) {
   const dim3 grid((M + 15) / 16, (T + 15) / 16);
-  if (scale_dtype == AINFER_SCALE_FP16)
-    k_int4_gemv_i8<AINFER_SCALE_FP16>
-        <<<grid, GV_WAVES * 64, 0, s>>>(P, (const uint16_t *)S, xq, sq, M, K, T, y);
-  else
-    k_int4_gemv_i8<AINFER_SCALE_BF16>
-        <<<grid, GV_WAVES * 64, 0, s>>>(P, (const uint16_t *)S, xq, sq, M, K, T, y);
+  const size_t stg = (size_t)16 * (K / 128) * 6;  // staged scales
+  const bool st = stg <= 48 * 1024;
+  auto go = [&](auto sd_c, auto stg_c) {
+    constexpr int SDc = decltype(sd_c)::value;
+    constexpr bool STc = decltype(stg_c)::value;
+    k_int4_gemv_i8<SDc, STc><<<grid, GV_WAVES * 64, STc ? stg : 0, s>>>(
+        P, (const uint16_t *)S, xq, sq, M, K, T, y);
+  };
+  using F16 = std::integral_constant<int, AINFER_SCALE_FP16>;
+  using B16 = std::integral_constant<int, AINFER_SCALE_BF16>;
+  if (scale_dtype == AINFER_SCALE_FP16) {
+    if (st) go(F16(), std::true_type()); else go(F16(), std::false_type());
+  } else {
+    if (st) go(B16(), std::true_type()); else go(B16(), std::false_type());
+  }
   return hipGetLastError();
 }
