@@ -188,16 +188,91 @@ __device__ __forceinline__ int xcd_remap(int b, int G) {
 
 // MFMA-order copy of one token row (position 8*j+e <- k = 4*e+j inside every
 // 32-element block) and, when xsum is non-null, its 128-wide group sums.
+// RMSNorm applied on the fly (the decode routing kernel at T <= 16, so a
+// block needs no separate RMSNorm launch): the per-token scale and the
+// normalized bf16 values are bit-identical to k_rmsnorm (moe_route.hip).
+struct NormIn {
+  const uint16_t *w;  // norm weight [H] bf16, or null (weight 1)
+  int mode;           // AINFER_NORM_PLAIN / AINFER_NORM_ONE_PLUS
+  float eps;
+  int on;             // 0: x is used as given
+};
+
+// inv = 1 / sqrt(ss / H + eps) (H <= 4096) with ss in fp64 in k_rmsnorm's order: 256
+// partial sums (partial l over j = l, l + 256, ...), then the pairwise tree
+// st = 128 .. 1.  One wave: lane l holds partials l, l + 64, l + 128,
+// l + 192; st = 128 and 64 stay in the lane, st = 32 .. 1 are shuffles (for
+// the lanes below st, l ^ st = l + st).
+__device__ __forceinline__ float row_rms_inv(const uint16_t *__restrict__ xr, int H, float eps,
+                                             int lane) {
+  // loads in two batches of 8 blocks of 256 (H <= 4096), each issued before
+  // its sums; the partial sums still run over m in order
+  double p[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+  for (int m0 = 0; m0 < 16; m0 += 8) {
+    if (256 * m0 >= H) break;
+    uint16_t v[8][4];
+#pragma unroll
+    for (int m = 0; m < 8; ++m)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[m][i] = xr[min(256 * (m0 + m) + 64 * i + lane, H - 1)];
+#pragma unroll
+    for (int m = 0; m < 8; ++m)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (256 * (m0 + m) + 64 * i + lane < H) {
+          const double d = (double)bf16_to_f32(v[m][i]);
+          p[i] += d * d;
+        }
+      }
+  }
+  p[0] += p[2];
+  p[1] += p[3];
+  p[0] += p[1];
+#pragma unroll
+  for (int st = 32; st >= 1; st >>= 1) p[0] += __shfl_xor(p[0], st, 64);
+  const double tot = __shfl(p[0], 0, 64);
+  return 1.0f / sqrtf((float)(tot / H) + eps);
+}
+
+// one packed bf16 pair of x normalized as k_rmsnorm writes it
+__device__ __forceinline__ uint32_t norm_pair(uint32_t xp, uint32_t wp, float inv,
+                                              const NormIn &n) {
+  uint32_t out = 0u;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const float v = bf16_to_f32((uint16_t)(xp >> (16 * h))) * inv;
+    float wt = 1.0f;
+    if (n.w) {
+      const float wv = bf16_to_f32((uint16_t)(wp >> (16 * h)));
+      wt = n.mode == AINFER_NORM_ONE_PLUS ? 1.0f + wv : wv;
+    }
+    out |= (uint32_t)f32_to_bf16(v * wt) << (16 * h);
+  }
+  return out;
+}
+
 __device__ __forceinline__ void write_xperm(const uint16_t *__restrict__ xrow,
                                             uint16_t *__restrict__ xperm,
-                                            float *__restrict__ xsum, int t, int H, int lane) {
+                                            float *__restrict__ xsum, int t, int H, int lane,
+                                            const NormIn *norm = nullptr, float inv = 1.0f) {
   {
     uint16_t *xo = xperm + (size_t)t * H;
     for (int b = lane; b < (H >> 5); b += 64) {
       const u32x4 *src = (const u32x4 *)(xrow + b * 32);
       const u32x4 s0 = src[0], s1 = src[1], s2 = src[2], s3 = src[3];
-      const uint32_t in[16] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3],
-                               s2[0], s2[1], s2[2], s2[3], s3[0], s3[1], s3[2], s3[3]};
+      uint32_t in[16] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3],
+                         s2[0], s2[1], s2[2], s2[3], s3[0], s3[1], s3[2], s3[3]};
+      if (norm && norm->on) {
+        u32x4 wv[4] = {};
+        if (norm->w) {
+          const u32x4 *ws = (const u32x4 *)(norm->w + b * 32);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) wv[i] = ws[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) in[i] = norm_pair(in[i], wv[i >> 2][i & 3], inv, *norm);
+      }
       uint32_t out[16];
 #pragma unroll
       for (int j = 0; j < 4; ++j)

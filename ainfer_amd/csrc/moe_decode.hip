@@ -87,6 +87,7 @@ constexpr int RD_NB = 2;      // 8-element chunks per lane whose loads are issue
 #define RD_NB1 8   // chunks in flight at T <= RD_TT1_MAX: a whole row up to H = 4096
 #endif
 static_assert(RD_W1 >= RD_TT1_MAX, "the selection runs one wave per token");
+static_assert(DECODE_NORM_MAX_T <= RD_TT1_MAX, "the folded RMSNorm exists in the TT = 1 form only");
 constexpr int SPIN_MAX = 1 << 20;
 #ifndef DEC_WAVES_PER_SIMD
 #define DEC_WAVES_PER_SIMD 6  // register budget of the expert kernel (<= 80 VGPRs)
@@ -136,6 +137,7 @@ struct RouteDecodeArgs {
   DispatchOut ds;
   int32_t *sync;
   uint32_t *slots;  // [DECODE_MAX_T][E + 1] ~bits of the logits (sync region)
+  NormIn norm;      // on: x is the residual stream, normalized here (RMSNorm)
   int T, H, E, k, has_shared, NR;
 };
 
@@ -202,7 +204,10 @@ __device__ __forceinline__ void dispatch_decode(const int32_t *__restrict__ idx,
 
 // W waves per workgroup (T <= W: the selection runs one wave per token), NB
 // chunks of 8 per lane whose loads are issued together
-template <int NV, int RD_TT, int W, int NB>
+// NORM: x is the residual stream and the block's RMSNorm is applied here
+// (T <= RD_TT1_MAX only: at two tokens per wave the extra registers cost
+// more than the saved launch)
+template <int NV, int RD_TT, int W, int NB, bool NORM>
 __global__ __launch_bounds__(W * 64) void k_route_decode(RouteDecodeArgs a) {
   __shared__ uint64_t s_cand[W][68];
   __shared__ uint64_t s_sel[W][16];
@@ -226,6 +231,12 @@ __global__ __launch_bounds__(W * 64) void k_route_decode(RouteDecodeArgs a) {
         wr[i] = r < E ? a.rw + (size_t)r * H : a.gw;
       }
       const int nch = H >> 3;
+      // RMSNorm folded in: each token's scale, then x normalized per chunk
+      float inv[RD_TT];
+#pragma unroll
+      for (int j = 0; j < RD_TT; ++j)
+        inv[j] = NORM ? row_rms_inv(a.x + (size_t)min(t0 + j, T - 1) * H, H, a.norm.eps, lane)
+                      : 1.0f;
       float acc[RD_R][RD_TT];
 #pragma unroll
       for (int i = 0; i < RD_R; ++i)
@@ -234,7 +245,7 @@ __global__ __launch_bounds__(W * 64) void k_route_decode(RouteDecodeArgs a) {
       // NB chunks' loads in flight at once; the sums still run over
       // chunks l, l + 64, ... in order
       for (int cb = lane; cb < nch; cb += 64 * NB) {
-        u32x4 wv[NB][RD_R], xv[NB][RD_TT];
+        u32x4 wv[NB][RD_R], xv[NB][RD_TT], nv[NB];
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
           const int c = min(cb + 64 * b, nch - 1);
@@ -243,6 +254,16 @@ __global__ __launch_bounds__(W * 64) void k_route_decode(RouteDecodeArgs a) {
 #pragma unroll
           for (int j = 0; j < RD_TT; ++j)
             xv[b][j] = *(const u32x4 *)(a.x + (size_t)min(t0 + j, T - 1) * H + (size_t)c * 8);
+          nv[b] = NORM && a.norm.w ? *(const u32x4 *)(a.norm.w + (size_t)c * 8)
+                                   : u32x4{0u, 0u, 0u, 0u};
+        }
+        if constexpr (NORM) {
+#pragma unroll
+          for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int j = 0; j < RD_TT; ++j)
+#pragma unroll
+              for (int q = 0; q < 4; ++q) xv[b][j][q] = norm_pair(xv[b][j][q], nv[b][q], inv[j], a.norm);
         }
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
@@ -288,7 +309,10 @@ __global__ __launch_bounds__(W * 64) void k_route_decode(RouteDecodeArgs a) {
   // ---- the selection workgroup: one wave per token (T <= W) ---------------
   const int t = wave;
   // the MFMA-order copy of x does not depend on the routing
-  if (t < T && a.xperm) write_xperm(a.x + (size_t)t * H, a.xperm, nullptr, t, H, lane);
+  if (t < T && a.xperm) {
+    const float inv = NORM ? row_rms_inv(a.x + (size_t)t * H, H, a.norm.eps, lane) : 1.0f;
+    write_xperm(a.x + (size_t)t * H, a.xperm, nullptr, t, H, lane, NORM ? &a.norm : nullptr, inv);
+  }
   DTRACE(0, 1);
   uint32_t raw[NV], graw = 0u;
   if (t < T) {
@@ -501,7 +525,7 @@ hipError_t launch_route_decode(const void *x, const void *rw, const float *bias,
                                float *logits, float *sgl, int32_t *idx, float *w, float *sg,
                                void *xperm, int T, int H, int E, int k, int has_shared,
                                const DispatchOut *ds, int32_t *sync, uint32_t *slots,
-                               hipStream_t s) {
+                               const NormIn *norm, hipStream_t s) {
   if (T <= 0) return hipSuccess;
   if (T > DECODE_MAX_T || T > RD_WAVES || E > 1024) return hipErrorInvalidValue;
   RouteDecodeArgs a;
@@ -519,6 +543,8 @@ hipError_t launch_route_decode(const void *x, const void *rw, const float *bias,
   if (ds) a.ds = *ds;
   a.sync = sync;
   a.slots = slots;
+  if (norm) a.norm = *norm;
+  if (a.norm.on && T > RD_TT1_MAX) return hipErrorInvalidValue;  // see k_route_decode
   a.T = T;
   a.H = H;
   a.E = E;
@@ -533,10 +559,12 @@ hipError_t launch_route_decode(const void *x, const void *rw, const float *bias,
   const int nv = (E + 63) / 64;
   auto go = [&](auto nv_c) {
     constexpr int NVc = decltype(nv_c)::value;
-    if (tt == 1)
-      k_route_decode<NVc, 1, RD_W1, RD_NB1><<<grid, RD_W1 * 64, 0, s>>>(a);
+    if (tt == 1 && a.norm.on)
+      k_route_decode<NVc, 1, RD_W1, RD_NB1, true><<<grid, RD_W1 * 64, 0, s>>>(a);
+    else if (tt == 1)
+      k_route_decode<NVc, 1, RD_W1, RD_NB1, false><<<grid, RD_W1 * 64, 0, s>>>(a);
     else
-      k_route_decode<NVc, 2, RD_WAVES, RD_NB><<<grid, RD_WAVES * 64, 0, s>>>(a);
+      k_route_decode<NVc, 2, RD_WAVES, RD_NB, false><<<grid, RD_WAVES * 64, 0, s>>>(a);
   };
   if (nv <= 1) go(std::integral_constant<int, 1>());
   else if (nv <= 2) go(std::integral_constant<int, 2>());

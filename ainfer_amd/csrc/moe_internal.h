@@ -160,6 +160,9 @@ constexpr int FUSED_DISPATCH_MAX_T = 64;
 
 // ---- decode layer in two launches (moe_decode.hip), T <= DECODE_MAX_T ----
 constexpr int DECODE_MAX_T = EXACT_ROUTER_MAX_T;
+// ainfer_moe_block_forward folds the RMSNorm into the decode routing kernel
+// up to this many tokens (its one-token-per-wave form)
+constexpr int DECODE_NORM_MAX_T = 4;
 // up to this many tokens the expert stages run fused in one launch
 // (k_experts_decode); above it as gate/up, down and combine launches (the
 // fused items' handoffs cost more than the two launches they save)
@@ -190,7 +193,7 @@ hipError_t launch_route_decode(const void *x, const void *rw, const float *bias,
                                float *logits, float *sgl, int32_t *idx, float *w, float *sg,
                                void *xperm, int T, int H, int E, int k, int has_shared,
                                const DispatchOut *ds, int32_t *sync, uint32_t *slots,
-                               hipStream_t s);
+                               const NormIn *norm, hipStream_t s);
 // gate/up + SiLU, down and the combine (y = sum_j w_j o_j + g_s o_s (+ resid));
 // split: gate/up in a launch of its own first (measured faster at T = 1,
 // where the down items of a fused launch wait behind the gate/up items for

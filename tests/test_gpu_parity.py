@@ -260,6 +260,39 @@ def test_block_forward_and_stack(torch, oracle):
     check_close(to_np(r_gpu), oracle.bf16_to_f32(r_ref), "3-block stack")
 
 
+@pytest.mark.parametrize("mode", ["plain", "one_plus"])
+def test_block_forward_fused_norm(torch, oracle, mode):
+    """At T <= 16 the routing kernel applies the block's RMSNorm itself.  Each
+    token's output must equal bit for bit the same token's output at T = 17,
+    which normalizes with the separate RMSNorm kernel (every later stage works
+    per token), and match the oracle's block within tolerance."""
+    from ainfer_amd import _lib as L
+    from ainfer_amd.moe import MoeLayer, make_input
+    from ainfer_amd.synthetic import CONFIGS
+    import dataclasses
+    nm = L.NORM_PLAIN if mode == "plain" else L.NORM_ONE_PLUS
+    cfg = dataclasses.replace(CONFIGS["c4"], n_experts=64, layers=1)
+    _layers.clear()
+    layer = MoeLayer(cfg, layer=7)
+    x = make_input(cfg, 17, tag=41) * 3
+    g = torch.Generator().manual_seed(5)
+    nw = (torch.randn(cfg.hidden, generator=g) * 0.5 + (0.0 if nm == L.NORM_ONE_PLUS else 1.0))
+    nw = nw.to(torch.bfloat16).cuda()
+    ws = layer.workspace(17)
+    ref17 = torch.empty_like(x)
+    layer.block_forward(x, ref17, ws, norm_w=nw, norm_mode=nm)
+    hl = host_copy(oracle, layer)
+    for T in (1, 2, 4, 16):
+        print(f"[case] fused norm {mode} T={T}", flush=True)
+        out = torch.empty_like(x[:T])
+        layer.block_forward(x[:T].contiguous(), out, ws, norm_w=nw, norm_mode=nm)
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref17[:T]), f"T={T}: fused RMSNorm differs from k_rmsnorm's"
+        want = hl.block_forward(to_np(x[:T].contiguous()), T, norm_w=to_np(nw), mode=nm)
+        check_close(to_np(out), oracle.bf16_to_f32(want), f"fused norm T={T}")
+    assert layer.workspace_check(ws) == 0
+
+
 def test_zero_tokens_and_errors(torch, oracle):
     from ainfer_amd import _lib as L
     layer = get_layer(torch, "c0")
