@@ -237,6 +237,16 @@ ExpertArgs expert_args(const ainfer_moe_shape *s, const ainfer_moe_weights *w, c
 #endif
 // norm (decode path only, ainfer_moe_block_forward): x is the residual stream and
 // the routing kernel applies the RMSNorm itself
+// k-groups per wave of the 4-token down items: whole 256-byte row segments
+// once the down K (the intermediate size) has 8 groups or more
+#ifndef DOWN_KBW4_MIN_I
+#define DOWN_KBW4_MIN_I 1024  // c3 T=64: down 149.5 -> 139.5 us; c1 (I = 512) keeps 2
+#endif
+int down_kbw(const ainfer_moe_shape &s) {
+  const int I = s.inter > s.shared_inter ? s.inter : s.shared_inter;
+  return I >= DOWN_KBW4_MIN_I ? 4 : DEC_KBW_DOWN;
+}
+
 int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const void *x,
                const void *resid, void *y, int T, void *ws, hipStream_t st,
                ProfCall *pc, const NormIn *norm = nullptr) {
@@ -272,7 +282,7 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
       const int mtb = max_tiles_bound(*s, T, DEC_MT);
       HIP_TRY(launch_expert_stream(0, s->scale_dtype, gu, mtb, 4, DEC_RG_GATE_UP, DEC_MT, st));
       pc->end(4);
-      HIP_TRY(launch_expert_stream(1, s->scale_dtype, dn, mtb, DEC_KBW_DOWN, DEC_RG_DOWN, DEC_MT, st));
+      HIP_TRY(launch_expert_stream(1, s->scale_dtype, dn, mtb, down_kbw(*s), DEC_RG_DOWN, DEC_MT, st));
       pc->end(5);
       HIP_TRY(launch_combine(at<uint16_t>(ws, L.o), d.inv, at<float>(ws, L.w), at<float>(ws, L.sg),
                              has_shared, resid, y, T, k, H, st));
@@ -384,7 +394,7 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
   const int smt = DEC_MT;  // tiles of the dispatch above
   const int max_tiles = max_tiles_bound(*s, T, smt);
   // k-groups per wave and 16-row groups per wave, measured at T = 1, 4, 16
-  const int kbw = 4, kbw_down = 2;
+  const int kbw = 4, kbw_down = down_kbw(*s);
   // gate/up + SiLU-mul
   a.w0 = w->w_gate;
   a.w1 = w->w_up;

@@ -262,10 +262,13 @@ def test_block_forward_and_stack(torch, oracle):
 
 @pytest.mark.parametrize("mode", ["plain", "one_plus"])
 def test_block_forward_fused_norm(torch, oracle, mode):
-    """At T <= 16 the routing kernel applies the block's RMSNorm itself.  Each
-    token's output must equal bit for bit the same token's output at T = 17,
-    which normalizes with the separate RMSNorm kernel (every later stage works
-    per token), and match the oracle's block within tolerance."""
+    """At T <= 4 the routing kernel applies the block's RMSNorm itself (one
+    code path for T = 1..4).  At T = 3 and 4 every later stage is the one
+    T = 17 runs (4-token tiles, per-token arithmetic), and T = 17 normalizes
+    with the separate RMSNorm kernel: each token's output must be equal bit
+    for bit.  T = 1 and 2 run the fused expert kernel, whose down items split
+    K differently, so there the check is the oracle's block within tolerance
+    (as at every T)."""
     from ainfer_amd import _lib as L
     from ainfer_amd.moe import MoeLayer, make_input
     from ainfer_amd.synthetic import CONFIGS
@@ -282,12 +285,13 @@ def test_block_forward_fused_norm(torch, oracle, mode):
     ref17 = torch.empty_like(x)
     layer.block_forward(x, ref17, ws, norm_w=nw, norm_mode=nm)
     hl = host_copy(oracle, layer)
-    for T in (1, 2, 4, 16):
+    for T in (1, 2, 3, 4, 16):
         print(f"[case] fused norm {mode} T={T}", flush=True)
         out = torch.empty_like(x[:T])
         layer.block_forward(x[:T].contiguous(), out, ws, norm_w=nw, norm_mode=nm)
         torch.cuda.synchronize()
-        assert torch.equal(out, ref17[:T]), f"T={T}: fused RMSNorm differs from k_rmsnorm's"
+        if T >= 3:
+            assert torch.equal(out, ref17[:T]), f"T={T}: fused RMSNorm differs from k_rmsnorm's"
         want = hl.block_forward(to_np(x[:T].contiguous()), T, norm_w=to_np(nw), mode=nm)
         check_close(to_np(out), oracle.bf16_to_f32(want), f"fused norm T={T}")
     assert layer.workspace_check(ws) == 0
