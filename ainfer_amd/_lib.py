@@ -22,7 +22,7 @@ EXPORTS = (
     "ainfer_moe_forward", "ainfer_moe_block_forward", "ainfer_moe_route",
     "ainfer_moe_dispatch", "ainfer_moe_rmsnorm", "ainfer_moe_fill",
     "ainfer_moe_act_quant_i8", "ainfer_moe_int4_gemv_i8",
-    "ainfer_moe_profile_enable", "ainfer_moe_profile_read",
+    "ainfer_moe_profile_enable", "ainfer_moe_profile_read", "ainfer_moe_debug_spin_limit",
 )
 N_STAGES = 7
 STAGES = ("rmsnorm", "router", "topk", "dispatch", "gate_up", "down", "combine")
@@ -73,6 +73,7 @@ def lib():
         L.ainfer_moe_act_quant_i8.argtypes = [P, I32, I32, I32, P, P, P]
         L.ainfer_moe_int4_gemv_i8.argtypes = [P, P, I32, P, P, I32, I32, I32, P, P]
         L.ainfer_moe_profile_enable.argtypes = [I32]
+        L.ainfer_moe_debug_spin_limit.argtypes = [I32]
         L.ainfer_moe_profile_read.argtypes = [C.POINTER(C.c_float), I32, C.POINTER(I32)]
         for name in EXPORTS:
             getattr(L, name).restype = getattr(L, name).restype or C.c_int

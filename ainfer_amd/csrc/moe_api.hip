@@ -285,7 +285,8 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
       HIP_TRY(launch_expert_stream(1, s->scale_dtype, dn, mtb, down_kbw(*s), DEC_RG_DOWN, DEC_MT, st));
       pc->end(5);
       HIP_TRY(launch_combine(at<uint16_t>(ws, L.o), d.inv, at<float>(ws, L.w), at<float>(ws, L.sg),
-                             has_shared, resid, y, T, k, H, st));
+                             has_shared, resid, y, T, k, H,
+                           at<int32_t>(ws, L.sync) + SY_ERR, st));
       pc->end(6);
       return AINFER_OK;
     }
@@ -376,7 +377,8 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
     }
     pc->end(5);
     HIP_TRY(launch_combine(at<uint16_t>(ws, L.o), d.inv, at<float>(ws, L.w), at<float>(ws, L.sg),
-                           has_shared, resid, y, T, k, H, st));
+                           has_shared, resid, y, T, k, H,
+                           at<int32_t>(ws, L.sync) + SY_ERR, st));
     pc->end(6);
     return AINFER_OK;
   }
@@ -425,7 +427,8 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
   HIP_TRY(launch_expert_stream(1, s->scale_dtype, a, max_tiles, kbw_down, RG_DOWN, smt, st));
   pc->end(5);
   HIP_TRY(launch_combine(at<uint16_t>(ws, L.o), d.inv, at<float>(ws, L.w), at<float>(ws, L.sg),
-                         has_shared, resid, y, T, k, H, st));
+                         has_shared, resid, y, T, k, H,
+                           at<int32_t>(ws, L.sync) + SY_ERR, st));
   pc->end(6);
   return AINFER_OK;
 }
@@ -680,6 +683,12 @@ int ainfer_moe_profile_read(float *stage_us, int32_t n_stages, int32_t *n_calls)
   for (int i = 0; i < n_stages && i < NSTAGE; ++i)
     stage_us[i] = g_prof.cnt[i] ? (float)(g_prof.sum_us[i] / g_prof.cnt[i]) : 0.0f;
   if (n_calls) *n_calls = g_prof.calls;
+  return AINFER_OK;
+}
+
+int ainfer_moe_debug_spin_limit(int32_t polls) {
+  if (polls < 0) return AINFER_ERR_ARG;
+  g_spin_max = polls;
   return AINFER_OK;
 }
 

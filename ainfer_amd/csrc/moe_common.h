@@ -198,7 +198,36 @@ struct NormIn {
   int on;             // 0: x is used as given
 };
 
-// inv = 1 / sqrt(ss / H + eps) (H <= 4096) with ss in fp64 in k_rmsnorm's order: 256
+// float(ss / H) of an RMSNorm row whose fp64 sum of squares is tot, when that
+// float is the same for every summation order of the squares.  The reference
+// sums sequentially for N != 5120 and as a 256-lane tree for N = 5120
+// (tools/cmdlist/kernels.cpp:86-107).  Any order of H non-negative terms lies
+// within (H-1)*2^-53*(1+tiny) of the exact sum (recursive-summation bound), so
+// two orders differ by less than H*2^-52 relative and the quotients by H by
+// less than (H+8)*2^-52.  If both ends of that interval around tot/H round to
+// one float, every order gives that float and the result is bit-identical to
+// the reference's.  Otherwise (about 2^25*H*2^-52 of rows: 1 in 30000 at
+// H = 4096) it returns false and the caller sums sequentially.
+__device__ __forceinline__ bool rms_mean_f(double tot, int H, float &mean) {
+  const double d = tot / H;
+  const double m = (double)(H + 8) * 0x1p-52;
+  mean = (float)d;
+  return (float)(d * (1.0 - m)) == (float)(d * (1.0 + m));
+}
+
+// Sequential fp64 sum of squares of a bf16 row (the reference order for
+// N != 5120): the rare fallback of rms_mean_f.
+__device__ __forceinline__ double row_sumsq_seq(const uint16_t *__restrict__ xr, int H) {
+  double ss = 0.0;
+  for (int j = 0; j < H; ++j) {
+    const double v = (double)bf16_to_f32(xr[j]);
+    ss += v * v;
+  }
+  return ss;
+}
+
+// inv = 1 / sqrt(mean + eps) (H <= 4096) with the mean from rms_mean_f over ss in
+// fp64 in k_rmsnorm's order: 256
 // partial sums (partial l over j = l, l + 256, ...), then the pairwise tree
 // st = 128 .. 1.  One wave: lane l holds partials l, l + 64, l + 128,
 // l + 192; st = 128 and 64 stay in the lane, st = 32 .. 1 are shuffles (for
@@ -232,7 +261,13 @@ __device__ __forceinline__ float row_rms_inv(const uint16_t *__restrict__ xr, in
 #pragma unroll
   for (int st = 32; st >= 1; st >>= 1) p[0] += __shfl_xor(p[0], st, 64);
   const double tot = __shfl(p[0], 0, 64);
-  return 1.0f / sqrtf((float)(tot / H) + eps);
+  float mean;
+  if (!rms_mean_f(tot, H, mean)) {  // wave-uniform
+    double ss = 0.0;
+    if (lane == 0) ss = row_sumsq_seq(xr, H);
+    mean = (float)(__shfl(ss, 0, 64) / H);
+  }
+  return 1.0f / sqrtf(mean + eps);
 }
 
 // one packed bf16 pair of x normalized as k_rmsnorm writes it

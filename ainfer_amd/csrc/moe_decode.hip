@@ -35,7 +35,12 @@
 // A wait only ever names work of lower workgroup index, and workgroups are
 // dispatched in index order, so every awaited workgroup is already running.
 // Waits are bounded (SPIN_MAX polls); one that runs out sets the error word
-// of the sync region and carries on.
+// of the sync region and carries on.  The error word is sticky: while it is
+// set, every combine (this kernel's and k_combine) writes NaN outputs, so a
+// call whose handoff failed, and every later call on that workspace until
+// ainfer_moe_workspace_init clears it, returns visibly bad rows rather than
+// silently wrong ones (a late arrival can leave a counter non-zero, which
+// would let a later call's waits pass early).
 //
 // Every counter is reset by its last user (the logit slots by the selection
 // workgroup, gu_done/dn_done by a tile's last down item, a (token, slab)
@@ -102,8 +107,8 @@ constexpr int SPIN_MAX = 1 << 20;
 #define DEC_RG_DN 2  // 16-row groups per wave, down items
 #endif
 
-__device__ __forceinline__ bool spin_until_geq(const int32_t *p, int target) {
-  for (int it = 0; it < SPIN_MAX; ++it) {
+__device__ __forceinline__ bool spin_until_geq(const int32_t *p, int target, int spin) {
+  for (int it = 0; it < spin; ++it) {
     if (__hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= target) return true;
     __builtin_amdgcn_s_sleep(8);
   }
@@ -112,8 +117,9 @@ __device__ __forceinline__ bool spin_until_geq(const int32_t *p, int target) {
 
 // Workgroup-wide: thread 0 polls.  What the awaited workgroups published is
 // then read with sc1 loads (moe_common.h).
-__device__ __forceinline__ void block_wait_geq(const int32_t *p, int target, int32_t *err) {
-  if (threadIdx.x == 0 && !spin_until_geq(p, target)) atomicOr(err, 1);
+__device__ __forceinline__ void block_wait_geq(const int32_t *p, int target, int32_t *err,
+                                               int spin) {
+  if (threadIdx.x == 0 && !spin_until_geq(p, target, spin)) atomicOr(err, 1);
   __syncthreads();
 }
 
@@ -139,6 +145,7 @@ struct RouteDecodeArgs {
   uint32_t *slots;  // [DECODE_MAX_T][E + 1] ~bits of the logits (sync region)
   NormIn norm;      // on: x is the residual stream, normalized here (RMSNorm)
   int T, H, E, k, has_shared, NR;
+  int spin;         // polls before a wait gives up (0: at once)
 };
 
 // Dispatch of T <= 32 tokens by one workgroup (idx in LDS): 32-bit token masks
@@ -325,8 +332,8 @@ __global__ __launch_bounds__(W * 64) void k_route_decode(RouteDecodeArgs a) {
       uint32_t nz = graw | (a.gw ? 0u : 1u);
 #pragma unroll
       for (int i = 0; i < NV; ++i) nz = min(nz, raw[i]);
-      if (__all(nz != 0u)) break;
-      if (it == SPIN_MAX) {
+      if (a.spin > 0 && __all(nz != 0u)) break;
+      if (it >= a.spin) {
         if (lane == 0) atomicOr(a.sync + SY_ERR, 1);
         break;
       }
@@ -383,6 +390,7 @@ struct ExpertsDecodeArgs {
   uint16_t *y;
   int32_t *sync;
   int max_tiles, cap;  // grid tiles; capacity of the per-tile counter arrays
+  int spin;            // polls before a wait gives up (0: at once)
 };
 
 // One item per workgroup.  A down item only ever waits for gate/up items of
@@ -431,7 +439,7 @@ __global__ __launch_bounds__(1024, DEC_WAVES_PER_SIMD) void k_experts_decode(Exp
     const int32_t *gdone = &gu_done[tile * SY_STRIDE];
     int32_t *err = a.sync + SY_ERR;
     expert_lds_item<SD, KBW_DN, RG_DN, DEC_MT, 1, true, !SPLIT>(a.dn, td, slab, lds, [=]() {
-      if (!SPLIT) block_wait_geq(gdone, sg, err);
+      if (!SPLIT) block_wait_geq(gdone, sg, err, a.spin);
       DTRACE_AT(1, item, 1);
     });
     if (threadIdx.x >= 64) return;
@@ -464,6 +472,9 @@ __global__ __launch_bounds__(1024, DEC_WAVES_PER_SIMD) void k_experts_decode(Exp
     const __amdgpu_buffer_rsrc_t orr = make_rsrc(a.dn.o, 0x7FFFFFFFu);
     const int rows = 16 * RG_DN * a.dn.WR, r0 = slab * rows;
     const size_t Tk = (size_t)a.dn.T * k;
+    // a wait of this or an earlier call on the workspace ran out (this
+    // workgroup's own timeout is already visible here): NaN outputs
+    const bool bad = __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
     constexpr int CB = 4;  // slots whose loads are issued together
     for (int i = 0; i < mcnt; ++i) {
       const int t = __builtin_amdgcn_readfirstlane(__shfl(tok, i, 64));
@@ -489,13 +500,15 @@ __global__ __launch_bounds__(1024, DEC_WAVES_PER_SIMD) void k_experts_decode(Exp
           acc = __builtin_fmaf(a.sg[t],
                                bf16_to_f32(ld_dev_u16(orr, (uint32_t)(((Tk + t) * H + h) * 2))), acc);
         if (a.resid) acc += bf16_to_f32(a.resid[(size_t)t * H + h]);
-        if (r0 + hr < H) a.y[(size_t)t * H + h] = f32_to_bf16(acc);
+        if (r0 + hr < H) a.y[(size_t)t * H + h] = bad ? (uint16_t)0x7FC0u : f32_to_bf16(acc);
       }
     }
   }
 }
 
 }  // namespace
+
+int g_spin_max = SPIN_MAX;
 
 int decode_geometry(const ainfer_moe_shape &s, DecodeGeom *g) {
   int kbw, wk, wr;
@@ -550,6 +563,7 @@ hipError_t launch_route_decode(const void *x, const void *rw, const float *bias,
   a.E = E;
   a.k = k;
   a.has_shared = has_shared;
+  a.spin = g_spin_max;
   const int nrows = E + (gw ? 1 : 0);
   const int tt = T <= RD_TT1_MAX ? 1 : 2;
   const int units = (nrows + RD_R - 1) / RD_R * ((T + tt - 1) / tt);
@@ -599,6 +613,7 @@ hipError_t launch_experts_decode(int scale_dtype, const DecodeGeom &g, ExpertArg
   a.sync = sync;
   a.max_tiles = max_tiles;
   a.cap = cap;
+  a.spin = g_spin_max;
   const long grid = (long)max_tiles * (g.slabs_gu + g.slabs_dn);
   if (grid > 0x7FFFFFFF) return hipErrorInvalidValue;
   const int threads = g.nw * 64;

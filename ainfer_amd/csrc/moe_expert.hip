@@ -69,10 +69,13 @@ __global__ __launch_bounds__(1024) void k_expert(ExpertArgs a) {
   if (MODE == 0) {
     const int tok = shared ? pos0 + mm : a.ptok[pos0 + mm];
     abase = a.a_routed;
-    aoff = (uint32_t)tok * (uint32_t)a.H * 2u;
+    aoff = (uint32_t)tok * (uint32_t)a.H * 2u;  // < T * H * 2 <= 2^29
   } else {
-    abase = shared ? a.a_shared : a.a_routed;
-    aoff = (uint32_t)(pos0 + mm) * (uint32_t)K * 2u;
+    // the tile's first row moves the (uniform) base in 64-bit arithmetic, so
+    // the 32-bit buffer offset only spans the tile: (T*k) * I * 2 bytes can
+    // pass 2^31 at large T, the tile's 16 rows never do
+    abase = (shared ? a.a_shared : a.a_routed) + (size_t)pos0 * K;
+    aoff = (uint32_t)mm * (uint32_t)K * 2u;
   }
   if (m >= mcnt) aoff = BUF_OOB;
   const __amdgpu_buffer_rsrc_t arsrc = make_rsrc(abase, 0x7FFFFFFFu);

@@ -112,7 +112,10 @@ hipError_t launch_dispatch(const int32_t *idx, int T, int k, int E, int mt, int 
                            hipStream_t s);
 hipError_t launch_combine(const uint16_t *o, const int32_t *inv, const float *w, const float *sg,
                           int has_shared, const void *resid, void *y, int T, int k, int H,
-                          hipStream_t s);
+                          const int32_t *err, hipStream_t s);
+// polls a bounded device wait makes before it gives up (sets the workspace's
+// error word); ainfer_moe_debug_spin_limit changes it for tests
+extern int g_spin_max;
 // false when the shape has no wave geometry (more than 8 waves along K)
 bool expert_geometry(int mode, int H, int I, int Is, int pref_kbw, int *KBW, int *WK,
                      int *WR);

@@ -88,9 +88,11 @@ hipError_t launch_fill(int kind, uint64_t seed, float std_, size_t n, void *out,
 }
 
 // ---------------------------------------------------------------------------
-// RMSNorm: one 256-thread block per row; fp64 sum of squares in the fixed
-// order lane-strided + pairwise tree (the shape of RMSNormW,
-// tools/cmdlist/kernels.cpp:94-113), fp32 normalise, bf16 out.
+// RMSNorm: one 256-thread block per row; fp64 sum of squares as a
+// lane-strided + pairwise tree (the shape of RMSNormW's N = 5120 form,
+// tools/cmdlist/kernels.cpp:94-113), whose float mean rms_mean_f proves equal
+// to the reference's sequential order, with a sequential re-sum for the rows
+// where it cannot; fp32 normalise, bf16 out.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_rmsnorm(const uint16_t *__restrict__ x,
                                                  const uint16_t *__restrict__ w, int mode,
@@ -109,8 +111,14 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const uint16_t *__restrict__ x,
     if (lid < st) ps[lid] += ps[lid + st];
     __syncthreads();
   }
-  double tot = ps[0];
-  float inv = 1.0f / sqrtf((float)(tot / H) + eps);
+  float mean;
+  if (!rms_mean_f(ps[0], H, mean)) {  // block-uniform; see rms_mean_f
+    __syncthreads();
+    if (lid == 0) ps[0] = row_sumsq_seq(xr, H);
+    __syncthreads();
+    mean = (float)(ps[0] / H);
+  }
+  float inv = 1.0f / sqrtf(mean + eps);
   for (int j = lid; j < H; j += 256) {
     float wt = 1.0f;
     if (w) {
@@ -371,7 +379,8 @@ __global__ __launch_bounds__(256) void k_combine(const uint16_t *__restrict__ o,
                                                  const float *__restrict__ w,
                                                  const float *__restrict__ sg, int has_shared,
                                                  const uint16_t *__restrict__ resid,
-                                                 uint16_t *__restrict__ y, int T, int k, int H) {
+                                                 uint16_t *__restrict__ y, int T, int k, int H,
+                                                 const int32_t *__restrict__ err) {
   typedef uint32_t vec_t __attribute__((ext_vector_type(CPT / 2)));
   // grid (T, ceil(H / (CPT * blockDim.x))): the token is uniform, so its
   // slots' positions and weights are scalar loads
@@ -422,20 +431,26 @@ __global__ __launch_bounds__(256) void k_combine(const uint16_t *__restrict__ o,
 #pragma unroll
   for (int q = 0; q < CPT / 2; ++q)
     out[q] = (uint32_t)f32_to_bf16(acc[2 * q]) | ((uint32_t)f32_to_bf16(acc[2 * q + 1]) << 16);
+  // a bounded device wait of this or an earlier call on the workspace ran
+  // out: the output is not to be trusted, so it is made NaN (until re-init)
+  if (err && *err) {
+#pragma unroll
+    for (int q = 0; q < CPT / 2; ++q) out[q] = 0x7FC07FC0u;
+  }
   *(vec_t *)(y + (size_t)t * H + h0) = out;
 }
 
 hipError_t launch_combine(const uint16_t *o, const int32_t *inv, const float *w, const float *sg,
                           int has_shared, const void *resid, void *y, int T, int k, int H,
-                          hipStream_t s) {
+                          const int32_t *err, hipStream_t s) {
   if (T == 0) return hipSuccess;
   // few tokens: 64-thread blocks, so the layer's columns spread over more CUs
   const int nt = T <= 64 ? 64 : 256;
   if (H % 8 == 0)
     k_combine<8><<<dim3(T, (H / 8 + nt - 1) / nt), nt, 0, s>>>(
-        o, inv, w, sg, has_shared, (const uint16_t *)resid, (uint16_t *)y, T, k, H);
+        o, inv, w, sg, has_shared, (const uint16_t *)resid, (uint16_t *)y, T, k, H, err);
   else
     k_combine<4><<<dim3(T, (H / 4 + nt - 1) / nt), nt, 0, s>>>(
-        o, inv, w, sg, has_shared, (const uint16_t *)resid, (uint16_t *)y, T, k, H);
+        o, inv, w, sg, has_shared, (const uint16_t *)resid, (uint16_t *)y, T, k, H, err);
   return hipGetLastError();
 }

@@ -135,7 +135,11 @@ int ainfer_moe_workspace_init(const ainfer_moe_shape *shape, void *workspace,
  * the workspace), AINFER_ERR_WORKSPACE when other words are left non-zero
  * (overlapping calls on one workspace).  A diagnostic, not for the hot loop;
  * it has no counterpart in the reference, whose waits are host fences
- * (decode_l0.cpp:484-493). */
+ * (decode_l0.cpp:484-493).
+ * A wait that runs out also sets a sticky error word in the workspace: from
+ * then on every forward/block_forward on that workspace writes NaN to all of
+ * its output rows (the call itself still returns AINFER_OK, since it only
+ * enqueues), until ainfer_moe_workspace_init clears the word. */
 int ainfer_moe_workspace_check(const ainfer_moe_shape *shape, const void *workspace,
                                size_t workspace_bytes, void *stream);
 /* The whole layer: y[T][H] (bf16) = MoE(x[T][H] bf16).
@@ -211,6 +215,12 @@ int ainfer_moe_act_quant_i8(const void *x, int32_t x_dtype, int32_t T, int32_t K
 int ainfer_moe_int4_gemv_i8(const uint8_t *packed, const void *scales,
                             int32_t scale_dtype, const int8_t *q, const float *sq,
                             int32_t M, int32_t K, int32_t T, float *y, void *stream);
+
+/* Test hook: the number of polls a bounded device-side wait of the decode
+ * path makes before it gives up (default 2^20, about 10 ms).  0 makes every
+ * such wait give up at once, so tests can drive the timeout path while every
+ * kernel still exits normally.  Process-wide; no reference counterpart. */
+int ainfer_moe_debug_spin_limit(int32_t polls);
 
 /* ---- synthetic data (counter-based, bit-identical to the CPU oracle) --- */
 enum {

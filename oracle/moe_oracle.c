@@ -265,9 +265,11 @@ void mo_silu_mul(const double *g, const double *u, double *out, int n) {
 /* RMSNormW, tools/cmdlist/kernels.cpp:73-116: sum of squares in fp64,
  * inv = 1/sqrt(float(ss/N) + eps) in fp32, y = x*inv*(1+w) (ONE_PLUS) or
  * x*inv*w (PLAIN, the form of reference/operators_t14.npz).  The fp64 sum
- * follows the device kernel's fixed order: 256 lanes, lane l sums
- * j = l, l+256, ... sequentially, then a pairwise tree (st = 128 .. 1),
- * the same shape as kernels.cpp:98-107. */
+ * follows the reference's order exactly: for N = 5120, 256 work-items each
+ * sum j = l, l+256, ... sequentially, then a pairwise tree st = 128 .. 1
+ * (kernels.cpp:98-107); for any other N one work-item sums j = 0 .. N-1 in
+ * order (kernels.cpp:86-97, the same loop as the eager rmsnorm of
+ * tools/decode/decode.cpp:512-529). */
 static double sumsq_tree(const float *x, int H) {
   double ps[256];
   for (int l = 0; l < 256; ++l) {
@@ -280,11 +282,21 @@ static double sumsq_tree(const float *x, int H) {
   return ps[0];
 }
 
+static double sumsq_seq(const float *x, int H) {
+  double ss = 0.0;
+  for (int j = 0; j < H; ++j) ss += (double)x[j] * (double)x[j];
+  return ss;
+}
+
+double mo_rms_sumsq(const float *x, int H) {
+  return H == 5120 ? sumsq_tree(x, H) : sumsq_seq(x, H);
+}
+
 void mo_rmsnorm_f32(const float *x, const float *w, int mode, float eps,
                     float *y, int T, int H) {
   for (int t = 0; t < T; ++t) {
     const float *xr = x + (size_t)t * H;
-    double tot = sumsq_tree(xr, H);
+    double tot = mo_rms_sumsq(xr, H);
     float inv = 1.0f / sqrtf((float)(tot / H) + eps);
     for (int j = 0; j < H; ++j) {
       float wt = w ? (mode == AINFER_NORM_ONE_PLUS ? 1.0f + w[j] : w[j])

@@ -74,6 +74,9 @@ void mo_ref_gemv_inputs(int M, int K, int n_vec, uint8_t *packed, uint16_t *scal
 
 /* pointwise */
 void mo_silu_mul(const double *g, const double *u, double *out, int n);
+/* fp64 sum of squares in the reference RMSNormW order (tree at N = 5120,
+ * sequential otherwise) */
+double mo_rms_sumsq(const float *x, int H);
 void mo_rmsnorm_f32(const float *x, const float *w, int mode, float eps,
                     float *y, int T, int H);
 void mo_rmsnorm_bf16(const uint16_t *x, const uint16_t *w, int mode, float eps,

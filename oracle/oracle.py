@@ -61,6 +61,8 @@ def lib():
         L.mo_dequant_int4.argtypes = [P, P, I, I, I, P]
         L.mo_quantize_int4.argtypes = [P, I, I, P, P]
         L.mo_silu_mul.argtypes = [P, P, P, I]
+        L.mo_rms_sumsq.restype = C.c_double
+        L.mo_rms_sumsq.argtypes = [P, I]
         L.mo_rmsnorm_f32.argtypes = [P, P, I, F, P, I, I]
         L.mo_rmsnorm_bf16.argtypes = [P, P, I, F, P, I, I]
         L.mo_router_dot.restype = F
@@ -210,6 +212,11 @@ def rmsnorm_f32(x, w, mode, eps=1e-6):
     lib().mo_rmsnorm_f32(ptr(x), ptr(None if w is None else np.ascontiguousarray(w, np.float32)),
                          mode, C.c_float(eps), ptr(y), T, H)
     return y
+
+
+def rms_sumsq(x) -> float:
+    x = np.ascontiguousarray(x, np.float32)
+    return lib().mo_rms_sumsq(ptr(x), x.size)
 
 
 def rmsnorm_bf16(x, w, mode, eps=1e-6):

@@ -117,6 +117,89 @@ def test_rmsnorm_matches_reference_fixture_plain_form(oracle):
     assert np.abs(wrong - want).max() > 0.1     # the (1+w) form is not the fixture's
 
 
+def test_rmsnorm_one_plus_form(oracle):
+    """(1+w) form of RMSNormW (kernels.cpp:114-115): w = 0 gives the
+    unit-weight output, and a random w gives the plain form applied to the
+    fp32 weight 1+w, bit for bit."""
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((4, 384)) * 2).astype(np.float32)
+    unit = oracle.rmsnorm_f32(x, None, oracle.NORM_PLAIN)
+    zero = oracle.rmsnorm_f32(x, np.zeros(384, np.float32), oracle.NORM_ONE_PLUS)
+    assert np.array_equal(unit, zero)
+    w = (rng.standard_normal(384) * 0.3).astype(np.float32)
+    one_plus = oracle.rmsnorm_f32(x, w, oracle.NORM_ONE_PLUS)
+    plain = oracle.rmsnorm_f32(x, (np.float32(1.0) + w).astype(np.float32), oracle.NORM_PLAIN)
+    assert np.array_equal(one_plus, plain)
+    # and against an fp64 evaluation of the closed form
+    inv = 1.0 / np.sqrt((x.astype(np.float64) ** 2).mean(axis=1, keepdims=True) + 1e-6)
+    np.testing.assert_allclose(one_plus, x * inv * (1.0 + w), rtol=1e-6, atol=1e-6)
+
+
+def test_rmsnorm_sum_order_follows_reference(oracle):
+    """RMSNormW sums squares sequentially for N != 5120 (kernels.cpp:86-97)
+    and as 256 strided partials + a pairwise tree for N = 5120 (:98-107).
+    np.cumsum accumulates in order, so its last element is the sequential
+    sum; the tree is rebuilt with numpy reshapes."""
+    rng = np.random.default_rng(4)
+    for H in (4096, 2048, 1000, 5120):
+        for _ in range(20):
+            x = (rng.standard_normal(H) * rng.choice([1e-3, 1.0, 50.0])).astype(np.float32)
+            sq = x.astype(np.float64) ** 2
+            if H == 5120:
+                ps = sq.reshape(20, 256)
+                acc = np.zeros(256)
+                for r in range(20):
+                    acc = acc + ps[r]
+                st = 128
+                while st:
+                    acc = acc[:st] + acc[st:2 * st]
+                    st //= 2
+                want = acc[0]
+            else:
+                want = np.cumsum(sq)[-1]
+            assert oracle.rms_sumsq(x) == want, H
+
+
+def _rms_mean_stable(tot, H):
+    """Python statement of the order-independence test the device RMSNorm
+    applies (moe_common.h rms_mean_f)."""
+    d = tot / H
+    m = (H + 8) * 2.0 ** -52
+    return np.float32(d * (1 - m)) == np.float32(d * (1 + m)), np.float32(d)
+
+
+def test_rmsnorm_mean_is_order_independent_when_stable(oracle):
+    """Where the interval test passes, the float mean from the tree order and
+    from the sequential order are equal; rows where the two orders' fp64
+    sums differ occur, so the test is not vacuous."""
+    rng = np.random.default_rng(5)
+    H = 4096
+    differ = stable = 0
+    for _ in range(3000):
+        x = oracle.bf16_to_f32(oracle.f32_to_bf16(
+            (rng.standard_normal(H) * 4).astype(np.float32))).astype(np.float64)
+        seq = np.cumsum(x * x)[-1]
+        tree = (x * x).reshape(16, 256).sum(axis=0)
+        st = 128
+        while st:
+            tree = tree[:st] + tree[st:2 * st]
+            st //= 2
+        tree = tree[0]
+        differ += seq != tree
+        ok, mean = _rms_mean_stable(tree, H)
+        if ok:
+            stable += 1
+            assert mean == np.float32(seq / H)
+    assert differ > 10 and stable > 2900
+    # a row whose mean is exactly a float midpoint fails the test (the device
+    # then re-sums sequentially): 2048 ones and two 2^-7, mean 0.5 + 2^-25
+    x = np.zeros(H)
+    x[:2048] = 1.0
+    x[2048:2050] = 2.0 ** -7
+    ok, _ = _rms_mean_stable(np.cumsum(x * x)[-1], H)
+    assert not ok
+
+
 # ---------------------------------------------------------------- router ---
 def test_router_dot_exact_cases(oracle):
     one = np.full(2048, 0x3F80, np.uint16)     # bf16 1.0
@@ -237,6 +320,39 @@ def test_router_logits_bias_added(oracle):
         for e in range(cfg.n_experts):
             want = np.float32(oracle.router_dot(x[t], rw[e])) + hl.a["router_bias"][e]
             assert lg[t, e] == np.float32(want)
+
+
+def test_shared_gate_sigmoid_against_closed_form(oracle):
+    """g_s = sigmoid(dot(x, shared_gate_w)): a single non-zero term makes the
+    logit exact, so g_s is checked against 1/(1+exp(-L)) in fp64 at L = 0
+    (exactly 0.5), both signs, the large-|L| limits, and g_s = 1 with no
+    gate vector."""
+    import math
+    cfg, hl = _tiny_layer(oracle)
+    H = cfg.hidden
+    Ls = [0.0, 2.0, -2.0, 0.5, -7.0, 20.0, -20.0, 100.0, -100.0]
+    T = len(Ls)
+    x = np.zeros((T, H), np.uint16)
+    x[:, 3] = 0x3F80                                    # bf16 1.0 at k = 3
+    outs = []
+    for t, L in enumerate(Ls):
+        gw = np.zeros(H, np.uint16)
+        gw[3] = oracle.f32_to_bf16(np.float32([L]))[0]
+        arrays = dict(hl.a)
+        arrays["shared_gate_w"] = gw
+        h2 = oracle.HostLayer(cfg.shape_tuple(), arrays)
+        _, _, sg, _ = h2.route(np.ascontiguousarray(x[t:t + 1]), 1)
+        outs.append(float(sg[0]))
+    for L, g in zip(Ls, outs):
+        want = 1.0 / (1.0 + math.exp(-L))
+        assert abs(g - want) <= 1e-6 * want + 1e-30, (L, g, want)
+    assert outs[0] == 0.5
+    assert outs[1] > 0.5 > outs[2] and abs(outs[1] + outs[2] - 1.0) < 1e-7
+    assert outs[5] > 0.999999 and outs[6] < 1e-8 and outs[7] == 1.0 and outs[8] < 1e-40
+    arrays = dict(hl.a)
+    arrays["shared_gate_w"] = None
+    _, _, sg, _ = oracle.HostLayer(cfg.shape_tuple(), arrays).route(x, T)
+    assert (sg == 1.0).all()
 
 
 def test_block_forward_is_norm_then_moe_plus_residual(oracle):
