@@ -63,8 +63,14 @@ __device__ __forceinline__ void wait_vm() {
   asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
 }
 
+// Every LDS read this wave issued completes before the barrier: s_barrier
+// alone does not wait for them, and the compiler is free to place the
+// lgkmcnt wait of a fragment read after the barrier (with the MFMA that uses
+// it).  A wave past the barrier may then refill that ring stage by DMA while
+// the read is still queued.  (Without this wait the router GEMM below read a
+// refilled stage now and then: wrong approximate logits, wrong top-k.)
 __device__ __forceinline__ void block_barrier() {
-  asm volatile("" ::: "memory");
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
 }

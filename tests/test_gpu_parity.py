@@ -91,6 +91,7 @@ def test_route_and_dispatch_bit_exact(torch, oracle, name, T):
     xh = to_np(x)
     r_idx, r_w, r_sg, r_lg = hl.route(xh, T)
     assert np.array_equal(to_np(lg).view(np.uint32), r_lg.view(np.uint32)), "logits"
+    _report_topk_mismatch(to_np(idx), r_idx, r_lg)
     assert np.array_equal(to_np(idx), r_idx), "top-k indices"
     np.testing.assert_allclose(to_np(w), r_w, rtol=2e-6, atol=1e-7)
     np.testing.assert_allclose(to_np(sg), r_sg, rtol=2e-6, atol=1e-7)
@@ -99,6 +100,18 @@ def test_route_and_dispatch_bit_exact(torch, oracle, name, T):
     assert np.array_equal(to_np(offsets), o)
     assert np.array_equal(to_np(perm), p), "dispatch permutation"
     assert np.array_equal(to_np(inv), iv)
+
+
+def _report_topk_mismatch(got, want, logits):
+    """Print the rows whose top-k differs (indices and the logits of every
+    expert either side picked) before the assertion fails."""
+    bad = np.where((got != want).any(axis=1))[0]
+    if len(bad):
+        print(f"[topk] {len(bad)} rows differ: {bad[:16].tolist()}", flush=True)
+        for t in bad[:4]:
+            es = sorted(set(got[t].tolist()) | set(want[t].tolist()))
+            print(f"[topk] t={t} got={got[t].tolist()} want={want[t].tolist()} "
+                  f"logits={[(e, float(logits[t, e])) for e in es]}", flush=True)
 
 
 def _route_check(torch, oracle, layer, x, what):
