@@ -23,12 +23,13 @@ FLAGS = [
 
 def build_library(verbose: bool = False) -> Path:
     """Compile every HIP source into ainfer_amd/libainfer_moe.so."""
-    objs = []
-    for src in SOURCES:
-        obj = CSRC / (src + ".o")
-        cmd = [HIPCC, *[f for f in FLAGS if f != "-shared"], "-c", str(CSRC / src), "-o", str(obj)]
-        _run(cmd, verbose)
-        objs.append(str(obj))
+    from concurrent.futures import ThreadPoolExecutor
+    objs = [str(CSRC / (src + ".o")) for src in SOURCES]
+    cmds = [[HIPCC, *[f for f in FLAGS if f != "-shared"], "-c", str(CSRC / src), "-o", obj]
+            for src, obj in zip(SOURCES, objs)]
+    jobs = max(1, min(len(cmds), (os.cpu_count() or 1) // 2, 8))
+    with ThreadPoolExecutor(jobs) as pool:
+        list(pool.map(lambda c: _run(c, verbose), cmds))
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(LIB), *objs], verbose)
     return LIB
 
