@@ -8,7 +8,9 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "libainfer_moe.so"
 
 OK = 0
-ERR_SHAPE, ERR_NULL, ERR_WORKSPACE, ERR_TOKENS, ERR_HIP, ERR_ARG, ERR_SYNC = -1, -2, -3, -4, -5, -6, -7
+ERR_SHAPE, ERR_NULL, ERR_WORKSPACE, ERR_TOKENS, ERR_HIP, ERR_ARG, ERR_SYNC, ERR_SCRATCH = (
+    -1, -2, -3, -4, -5, -6, -7, -8)
+NOALLOC_SCRATCH_BYTES = 16 << 20
 SCALE_BF16, SCALE_FP16 = 0, 1
 NORM_PLAIN, NORM_ONE_PLUS = 0, 1
 ACT_F32, ACT_BF16 = 0, 1
@@ -19,7 +21,8 @@ MAX_TOKENS = 65536
 EXPORTS = (
     "ainfer_moe_strerror", "ainfer_moe_validate", "ainfer_moe_workspace_bytes",
     "ainfer_moe_workspace_init", "ainfer_moe_workspace_check",
-    "ainfer_moe_forward", "ainfer_moe_block_forward", "ainfer_moe_route",
+    "ainfer_moe_forward", "ainfer_moe_block_forward", "ainfer_moe_block_forward_noalloc",
+    "ainfer_moe_route",
     "ainfer_moe_dispatch", "ainfer_moe_rmsnorm", "ainfer_moe_fill",
     "ainfer_moe_act_quant_i8", "ainfer_moe_int4_gemv_i8",
     "ainfer_moe_profile_enable", "ainfer_moe_profile_read", "ainfer_moe_debug_spin_limit",
@@ -66,6 +69,7 @@ def lib():
         L.ainfer_moe_workspace_check.argtypes = [sp, P, SZ, P]
         L.ainfer_moe_forward.argtypes = [sp, wp, P, P, I32, P, SZ, P]
         L.ainfer_moe_block_forward.argtypes = [sp, wp, P, I32, F, P, P, I32, P, SZ, P]
+        L.ainfer_moe_block_forward_noalloc.argtypes = [sp, wp, P, I32, F, P, P, I32, P]
         L.ainfer_moe_route.argtypes = [sp, wp, P, I32, P, P, P, P, P, SZ, P]
         L.ainfer_moe_dispatch.argtypes = [sp, P, I32, P, P, P, P, P, SZ, P]
         L.ainfer_moe_rmsnorm.argtypes = [P, P, I32, F, P, I32, I32, P]

@@ -3,6 +3,7 @@
 // down -> combine.  Host code; every device buffer comes from the caller.
 #include <string.h>
 
+#include <mutex>
 #include <vector>
 
 #include "moe_common.h"
@@ -433,6 +434,71 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
   return AINFER_OK;
 }
 
+int check_block_args(const ainfer_moe_shape *s, const ainfer_moe_weights *w, int norm_mode,
+                     float eps, const void *resid_in, const void *resid_out, int T) {
+  int rc = ainfer_moe_validate(s);
+  if (rc) return rc;
+  if (T < 0 || T > AINFER_MOE_MAX_TOKENS) return AINFER_ERR_TOKENS;
+  if ((rc = check_weights(s, w))) return rc;
+  if (norm_mode != AINFER_NORM_PLAIN && norm_mode != AINFER_NORM_ONE_PLUS) return AINFER_ERR_ARG;
+  if (!(eps >= 0.0f)) return AINFER_ERR_ARG;
+  if (T == 0) return AINFER_OK;
+  if (!resid_in || !resid_out) return AINFER_ERR_NULL;
+  return AINFER_OK;
+}
+
+// h = RMSNorm(resid_in); resid_out = resid_in + MoE(h), on a checked workspace
+int do_block(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const void *norm_w,
+             int norm_mode, float eps, const void *resid_in, void *resid_out, int T, void *ws,
+             hipStream_t st) {
+  const Layout L = layout_of(*s, T);
+  void *h = at<void>(ws, L.h);
+  ProfCall pc(st);
+  pc.start();
+  DecodeGeom dg;
+  if (T <= DECODE_NORM_MAX_T && decode_geometry(*s, &dg)) {
+    // decode at up to 4 tokens: the routing kernel normalizes x itself (one
+    // launch fewer per block: c4 T=1 about 2470 -> 2235 us per 60-block
+    // step); the values are those k_rmsnorm writes
+    NormIn n;
+    n.w = (const uint16_t *)norm_w;
+    n.mode = norm_mode;
+    n.eps = eps;
+    n.on = 1;
+    pc.end(0);
+    return do_forward(s, w, resid_in, resid_in, resid_out, T, ws, st, &pc, &n);
+  }
+  HIP_TRY(launch_rmsnorm(resid_in, norm_w, norm_mode, eps, h, T, s->hidden, st));
+  pc.end(0);
+  return do_forward(s, w, h, resid_in, resid_out, T, ws, st, &pc);
+}
+
+// ---- the no-allocation entry's scratch ---------------------------------------
+// One copy per GPU, alive until the process ends.  Host code must never pass
+// the array's name to a kernel or a copy (on the host it is only a stand-in
+// symbol); it uses the per-device address hipGetSymbolAddress returns.
+__device__ __align__(256) unsigned char scratch[AINFER_MOE_NOALLOC_SCRATCH_BYTES];
+
+constexpr int NOALLOC_MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[NOALLOC_MAX_DEVICES];
+
+// The current device's scratch address, looked up once per device.
+int noalloc_scratch(void **out) {
+  int dev = -1;
+  HIP_TRY(hipGetDevice(&dev));
+  if (dev < 0 || dev >= NOALLOC_MAX_DEVICES) return AINFER_ERR_HIP;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p || ((uintptr_t)p & 255)) return AINFER_ERR_HIP;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return AINFER_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -447,6 +513,8 @@ const char *ainfer_moe_strerror(int status) {
   case AINFER_ERR_HIP: return "HIP runtime error";
   case AINFER_ERR_ARG: return "argument out of range";
   case AINFER_ERR_SYNC: return "a device-side wait ran out (workspace synchronisation words)";
+  case AINFER_ERR_SCRATCH:
+    return "the call needs more workspace than the no-allocation entry's static scratch holds";
   default: return "unknown status";
   }
 }
@@ -521,36 +589,28 @@ int ainfer_moe_block_forward(const ainfer_moe_shape *s, const ainfer_moe_weights
                              const void *norm_w, int32_t norm_mode, float eps,
                              const void *resid_in, void *resid_out, int32_t T, void *ws,
                              size_t ws_bytes, void *stream) {
-  int rc = ainfer_moe_validate(s);
-  if (rc) return rc;
-  if (T < 0 || T > AINFER_MOE_MAX_TOKENS) return AINFER_ERR_TOKENS;
-  if ((rc = check_weights(s, w))) return rc;
-  if (norm_mode != AINFER_NORM_PLAIN && norm_mode != AINFER_NORM_ONE_PLUS) return AINFER_ERR_ARG;
-  if (!(eps >= 0.0f)) return AINFER_ERR_ARG;
-  if (T == 0) return AINFER_OK;
-  if (!resid_in || !resid_out) return AINFER_ERR_NULL;
+  int rc = check_block_args(s, w, norm_mode, eps, resid_in, resid_out, T);
+  if (rc || T == 0) return rc;
   if ((rc = check_ws(s, T, ws, ws_bytes))) return rc;
-  const Layout L = layout_of(*s, T);
+  return do_block(s, w, norm_w, norm_mode, eps, resid_in, resid_out, T, ws, (hipStream_t)stream);
+}
+
+int ainfer_moe_block_forward_noalloc(const ainfer_moe_shape *s, const ainfer_moe_weights *w,
+                                     const void *norm_w, int32_t norm_mode, float eps,
+                                     const void *resid_in, void *resid_out, int32_t T,
+                                     void *stream) {
+  int rc = check_block_args(s, w, norm_mode, eps, resid_in, resid_out, T);
+  if (rc || T == 0) return rc;
+  if (layout_of(*s, T).total > AINFER_MOE_NOALLOC_SCRATCH_BYTES) return AINFER_ERR_SCRATCH;
+  void *ws = nullptr;
+  if ((rc = noalloc_scratch(&ws))) return rc;
   hipStream_t st = (hipStream_t)stream;
-  void *h = at<void>(ws, L.h);
-  ProfCall pc(st);
-  pc.start();
-  DecodeGeom dg;
-  if (T <= DECODE_NORM_MAX_T && decode_geometry(*s, &dg)) {
-    // decode at up to 4 tokens: the routing kernel normalizes x itself (one
-    // launch fewer per block: c4 T=1 about 2470 -> 2235 us per 60-block
-    // step); the values are those k_rmsnorm writes
-    NormIn n;
-    n.w = (const uint16_t *)norm_w;
-    n.mode = norm_mode;
-    n.eps = eps;
-    n.on = 1;
-    pc.end(0);
-    return do_forward(s, w, resid_in, resid_in, resid_out, T, ws, st, &pc, &n);
-  }
-  HIP_TRY(launch_rmsnorm(resid_in, norm_w, norm_mode, eps, h, T, s->hidden, st));
-  pc.end(0);
-  return do_forward(s, w, h, resid_in, resid_out, T, ws, st, &pc);
+  // every call starts from zeroed synchronisation words (a fill kernel, so the
+  // call stays capturable into a HIP graph): a bounded wait that ran out in
+  // an earlier call (that call's outputs are NaN) leaves nothing behind
+  const Layout L0 = layout_of(*s, 0);
+  HIP_TRY(launch_zero_i32(at<int32_t>(ws, L0.sync), (int)L0.sync_words, st));
+  return do_block(s, w, norm_w, norm_mode, eps, resid_in, resid_out, T, ws, st);
 }
 
 int ainfer_moe_route(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const void *x,

@@ -106,6 +106,14 @@ class MoeLayer:
             C.byref(self.shape), C.byref(self.weights), _ptr(norm_w), norm_mode, eps,
             _ptr(resid_in), _ptr(resid_out), T, _ptr(ws), ws.numel(), _stream(stream)))
 
+    def block_forward_noalloc(self, resid_in, resid_out, norm_w=None, norm_mode=L.NORM_PLAIN,
+                              eps=1e-6, stream=None):
+        """block_forward on the library's static per-GPU scratch (no workspace)."""
+        T = resid_in.shape[0]
+        return L.check(L.lib().ainfer_moe_block_forward_noalloc(
+            C.byref(self.shape), C.byref(self.weights), _ptr(norm_w), norm_mode, eps,
+            _ptr(resid_in), _ptr(resid_out), T, _stream(stream)))
+
     def route(self, x, ws, want_logits=False, stream=None):
         T, E, k = x.shape[0], self.cfg.n_experts, self.cfg.top_k
         dev = self.device

@@ -64,7 +64,9 @@ enum {
   AINFER_ERR_TOKENS = -4,     /* T < 0 or above the supported maximum       */
   AINFER_ERR_HIP = -5,        /* a HIP runtime call failed                  */
   AINFER_ERR_ARG = -6,        /* another argument is out of range           */
-  AINFER_ERR_SYNC = -7        /* a device-side wait ran out (decode path)   */
+  AINFER_ERR_SYNC = -7,       /* a device-side wait ran out (decode path)   */
+  AINFER_ERR_SCRATCH = -8     /* the call needs more than the static scratch
+                                 of ainfer_moe_block_forward_noalloc holds    */
 };
 
 enum { AINFER_SCALE_BF16 = 0, AINFER_SCALE_FP16 = 1 };
@@ -160,6 +162,30 @@ int ainfer_moe_block_forward(const ainfer_moe_shape *shape,
                              const void *resid_in, void *resid_out, int32_t T,
                              void *workspace, size_t workspace_bytes,
                              void *stream);
+
+/* Bytes of the static device scratch behind ainfer_moe_block_forward_noalloc
+ * (one copy per GPU the library runs on, held until the process ends). */
+#define AINFER_MOE_NOALLOC_SCRATCH_BYTES (16u << 20)
+
+/* ainfer_moe_block_forward without a workspace argument: the workspace is a
+ * static device array of AINFER_MOE_NOALLOC_SCRATCH_BYTES per GPU, and the
+ * call makes no allocation of any kind (no hipMalloc, no allocating library
+ * routine).  It has no counterpart in the reference; it is for callers that
+ * cannot allocate: code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation.  A call whose workspace_bytes(shape, T)
+ * exceeds the scratch returns AINFER_ERR_SCRATCH (16 MiB holds, e.g., every
+ * decode call up to 16 tokens and H4096/E512/k10/I1024 up to 64 tokens).
+ * Every call on one GPU shares that GPU's scratch and starts by zeroing its
+ * synchronisation words, so no workspace_init is needed and a wait that ran
+ * out in one call (its outputs are NaN) does not affect the next; calls that
+ * overlap on one GPU (different streams, or different host threads) race and
+ * give wrong results.  Outputs are bit-identical to ainfer_moe_block_forward
+ * on the same inputs. */
+int ainfer_moe_block_forward_noalloc(const ainfer_moe_shape *shape,
+                                     const ainfer_moe_weights *weights,
+                                     const void *norm_w, int32_t norm_mode, float eps,
+                                     const void *resid_in, void *resid_out, int32_t T,
+                                     void *stream);
 
 /* ---- stage-level entries (the pieces forward composes) ----------------- */
 
