@@ -201,29 +201,78 @@ struct NormIn {
 // float(ss / H) of an RMSNorm row whose fp64 sum of squares is tot, when that
 // float is the same for every summation order of the squares.  The reference
 // sums sequentially for N != 5120 and as a 256-lane tree for N = 5120
-// (tools/cmdlist/kernels.cpp:86-107).  Any order of H non-negative terms lies
-// within (H-1)*2^-53*(1+tiny) of the exact sum (recursive-summation bound), so
-// two orders differ by less than H*2^-52 relative and the quotients by H by
-// less than (H+8)*2^-52.  If both ends of that interval around tot/H round to
-// one float, every order gives that float and the result is bit-identical to
-// the reference's.  Otherwise (about 2^25*H*2^-52 of rows: 1 in 30000 at
-// H = 4096) it returns false and the caller sums sequentially.
-__device__ __forceinline__ bool rms_mean_f(double tot, int H, float &mean) {
+// (tools/cmdlist/kernels.cpp:86-107).  Two sufficient tests:
+//  1. exact sums.  A bf16 x = M * 2^(e - 134) (M < 256 an integer, e the
+//     exponent field, 1 for subnormals), so x^2 is a multiple of
+//     q = 2^(2 * emin - 268), emin the smallest exponent field of the row's
+//     non-zero elements.  Every partial sum in any order is a multiple of q
+//     no larger than the total; when the total is below 2^53 * q all of them
+//     are representable, no addition rounds, and every order gives tot
+//     exactly.  bf16 rows usually pass this (their squares have 16-bit
+//     significands), and they are also the rows whose tot / H tends to fall
+//     on a float rounding midpoint, where test 2 must fail.
+//  2. rounding that cannot matter.  Any order of H non-negative terms lies
+//     within (H-1)*2^-53*(1+tiny) of the exact sum (recursive-summation bound),
+//     so two orders differ by less than H*2^-52 relative and the quotients by
+//     H by less than (H+8)*2^-52.  If both ends of that interval around tot/H
+//     round to one float, every order gives that float.
+// Otherwise it returns false and the caller sums sequentially (rows that
+// hold both tiny and large elements and land within 2^-40 of a midpoint).
+__device__ __forceinline__ bool rms_mean_f(double tot, int emin, int H, float &mean) {
   const double d = tot / H;
-  const double m = (double)(H + 8) * 0x1p-52;
   mean = (float)d;
+  if (emin > 0 && tot < __builtin_ldexp(1.0, 2 * emin - 268 + 53)) return true;
+  const double m = (double)(H + 8) * 0x1p-52;
   return (float)(d * (1.0 - m)) == (float)(d * (1.0 + m));
 }
 
+// exponent field of a bf16 for rms_mean_f's quantum: 1 for subnormals, a
+// large value for zeros (they add nothing)
+__device__ __forceinline__ int bf16_qexp(uint16_t u) {
+  const int e = (u >> 7) & 0xFF;
+  return (u & 0x7FFF) == 0 ? 0x7FFF : (e == 0 ? 1 : e);
+}
+
 // Sequential fp64 sum of squares of a bf16 row (the reference order for
-// N != 5120): the rare fallback of rms_mean_f.
-__device__ __forceinline__ double row_sumsq_seq(const uint16_t *__restrict__ xr, int H) {
+// N != 5120): the rare fallback of rms_mean_f, run by one lane.  Loads are
+// issued 16 elements at a time; the additions stay in element order.
+__device__ __attribute__((noinline)) double row_sumsq_seq(const uint16_t *__restrict__ xr,
+                                                          int H) {
   double ss = 0.0;
-  for (int j = 0; j < H; ++j) {
+  int j = 0;
+  if (((uintptr_t)xr & 15) == 0)
+    for (; j + 16 <= H; j += 16) {
+      const u32x4 a = *(const u32x4 *)(xr + j), b = *(const u32x4 *)(xr + j + 8);
+      const uint32_t w[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const double v = (double)bf16_to_f32((uint16_t)(w[i] >> (16 * h)));
+          ss += v * v;
+        }
+    }
+  for (; j < H; ++j) {
     const double v = (double)bf16_to_f32(xr[j]);
     ss += v * v;
   }
   return ss;
+}
+
+// inv = 1 / sqrt(mean + eps) from a wave's fp64 sum of squares of row xr in any
+// order (tot, wave-uniform) and the smallest exponent field emin: the mean is
+// the reference's whenever rms_mean_f proves it, else the row is re-summed
+// sequentially by lane 0.
+__device__ __forceinline__ float rms_inv_finish(double tot, int emin,
+                                                const uint16_t *__restrict__ xr, int H, float eps,
+                                                int lane) {
+  float mean;
+  if (!rms_mean_f(tot, emin, H, mean)) {  // wave-uniform
+    double ss = 0.0;
+    if (lane == 0) ss = row_sumsq_seq(xr, H);
+    mean = (float)(__shfl(ss, 0, 64) / H);
+  }
+  return 1.0f / sqrtf(mean + eps);
 }
 
 // inv = 1 / sqrt(mean + eps) (H <= 4096) with the mean from rms_mean_f over ss in
@@ -237,6 +286,7 @@ __device__ __forceinline__ float row_rms_inv(const uint16_t *__restrict__ xr, in
   // loads in two batches of 8 blocks of 256 (H <= 4096), each issued before
   // its sums; the partial sums still run over m in order
   double p[4] = {0.0, 0.0, 0.0, 0.0};
+  int emin = 0x7FFF;
 #pragma unroll
   for (int m0 = 0; m0 < 16; m0 += 8) {
     if (256 * m0 >= H) break;
@@ -252,6 +302,7 @@ __device__ __forceinline__ float row_rms_inv(const uint16_t *__restrict__ xr, in
         if (256 * (m0 + m) + 64 * i + lane < H) {
           const double d = (double)bf16_to_f32(v[m][i]);
           p[i] += d * d;
+          emin = min(emin, bf16_qexp(v[m][i]));
         }
       }
   }
@@ -261,13 +312,9 @@ __device__ __forceinline__ float row_rms_inv(const uint16_t *__restrict__ xr, in
 #pragma unroll
   for (int st = 32; st >= 1; st >>= 1) p[0] += __shfl_xor(p[0], st, 64);
   const double tot = __shfl(p[0], 0, 64);
-  float mean;
-  if (!rms_mean_f(tot, H, mean)) {  // wave-uniform
-    double ss = 0.0;
-    if (lane == 0) ss = row_sumsq_seq(xr, H);
-    mean = (float)(__shfl(ss, 0, 64) / H);
-  }
-  return 1.0f / sqrtf(mean + eps);
+#pragma unroll
+  for (int st = 32; st >= 1; st >>= 1) emin = min(emin, __shfl_xor(emin, st, 64));
+  return rms_inv_finish(tot, emin, xr, H, eps, lane);
 }
 
 // one packed bf16 pair of x normalized as k_rmsnorm writes it

@@ -238,12 +238,13 @@ __global__ __launch_bounds__(W * 64) void k_route_decode(RouteDecodeArgs a) {
         wr[i] = r < E ? a.rw + (size_t)r * H : a.gw;
       }
       const int nch = H >> 3;
-      // RMSNorm folded in: each token's scale, then x normalized per chunk
+      // RMSNorm folded in: each token's scale from the x chunks the loop
+      // below loads (the whole row: one pass, H <= 64 * NB * 8), then x
+      // normalized per chunk
+      static_assert(!NORM || 64 * NB * 8 >= 4096, "the folded RMSNorm needs the whole row");
       float inv[RD_TT];
 #pragma unroll
-      for (int j = 0; j < RD_TT; ++j)
-        inv[j] = NORM ? row_rms_inv(a.x + (size_t)min(t0 + j, T - 1) * H, H, a.norm.eps, lane)
-                      : 1.0f;
+      for (int j = 0; j < RD_TT; ++j) inv[j] = 1.0f;
       float acc[RD_R][RD_TT];
 #pragma unroll
       for (int i = 0; i < RD_R; ++i)
@@ -265,6 +266,35 @@ __global__ __launch_bounds__(W * 64) void k_route_decode(RouteDecodeArgs a) {
                                    : u32x4{0u, 0u, 0u, 0u};
         }
         if constexpr (NORM) {
+          // sum of squares in any order (rms_mean_f's tests hold for every
+          // order), four independent fp64 chains per lane
+#pragma unroll
+          for (int j = 0; j < RD_TT; ++j) {
+            double p4[4] = {0.0, 0.0, 0.0, 0.0};
+            int emin = 0x7FFF;
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+              if (cb + 64 * b >= nch) continue;
+#pragma unroll
+              for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                  const uint16_t u = (uint16_t)(xv[b][j][q] >> (16 * h));
+                  const double v = (double)bf16_to_f32(u);
+                  p4[q] += v * v;
+                  emin = min(emin, bf16_qexp(u));
+                }
+            }
+            double tot = (p4[0] + p4[1]) + (p4[2] + p4[3]);
+#pragma unroll
+            for (int st = 32; st >= 1; st >>= 1) {
+              tot += __shfl_xor(tot, st, 64);
+              emin = min(emin, __shfl_xor(emin, st, 64));
+            }
+            tot = __shfl(tot, 0, 64);  // lanes may round differently: one value
+            inv[j] = rms_inv_finish(tot, emin, a.x + (size_t)min(t0 + j, T - 1) * H, H,
+                                    a.norm.eps, lane);
+          }
 #pragma unroll
           for (int b = 0; b < NB; ++b)
 #pragma unroll

@@ -98,21 +98,29 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const uint16_t *__restrict__ x,
                                                  const uint16_t *__restrict__ w, int mode,
                                                  float eps, uint16_t *__restrict__ y, int H) {
   __shared__ double ps[256];
+  __shared__ int pe[256];
   const int t = blockIdx.x, lid = threadIdx.x;
   const uint16_t *xr = x + (size_t)t * H;
   double ss = 0.0;
+  int emin = 0x7FFF;
   for (int j = lid; j < H; j += 256) {
-    double v = (double)bf16_to_f32(xr[j]);
+    const uint16_t u = xr[j];
+    double v = (double)bf16_to_f32(u);
     ss += v * v;
+    emin = min(emin, bf16_qexp(u));
   }
   ps[lid] = ss;
+  pe[lid] = emin;
   __syncthreads();
   for (int st = 128; st > 0; st >>= 1) {
-    if (lid < st) ps[lid] += ps[lid + st];
+    if (lid < st) {
+      ps[lid] += ps[lid + st];
+      pe[lid] = min(pe[lid], pe[lid + st]);
+    }
     __syncthreads();
   }
   float mean;
-  if (!rms_mean_f(ps[0], H, mean)) {  // block-uniform; see rms_mean_f
+  if (!rms_mean_f(ps[0], pe[0], H, mean)) {  // block-uniform; see rms_mean_f
     __syncthreads();
     if (lid == 0) ps[0] = row_sumsq_seq(xr, H);
     __syncthreads();

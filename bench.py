@@ -1,25 +1,33 @@
 #!/usr/bin/env python3
 """Benchmark of the INT4 MoE layer on one MI355X.
 
-Headline (the JSON line's `value`): config c1 decode, 16 tokens -- layer
-microseconds per token (H2048, 512 experts, top-10, I512, + shared expert,
-INT4 g128 fp16 scales).  `details` adds c1 at 1 and 4 tokens and the c2
-prefill (4096 tokens, Zipf(1.1) routing) in tokens/s and % of bf16 MFMA peak.
+Headline (the JSON line's `value`): config c4, the 60-block decode step at 1
+token -- microseconds per token of the whole step (each block: RMSNorm ->
+MoE layer H4096, 512 experts, top-10, I1024 + shared expert, INT4 g128 fp16
+scales -> residual add; 200 GB of weights resident).  It is the largest
+BASELINE config that fits one GPU.  `details` adds c4 at 8 tokens, c1 decode
+at 1/4/16 tokens, the c2 prefill (4096 tokens, Zipf(1.1) routing) in tokens/s
+and % of bf16 MFMA peak, c3 (64 tokens) and the W4A8 GEMV.
 
-`roofline.traffic` (HBM bytes per launch of the dominant decode kernel) is read
-from the committed rocprofv3 PMC summary profiles/<kernel>_c1_T16_traffic.md
-(FETCH_SIZE + WRITE_SIZE, scaled by the same counters on a copy of known
-size, made with --calib-copy); null when that file is absent.
+`roofline` prices the dominant kernel of a c4 block: its algorithmic bytes
+per launch over its mean device time (HIP events on the launch stream, each
+pair also spanning the launch gap before the kernel, so an upper bound on
+the time).  `roofline.traffic` (HBM bytes per launch of that kernel) is read
+from the committed rocprofv3 PMC summary
+profiles/<kernel>_c4_T<T>_traffic.md (FETCH_SIZE + WRITE_SIZE, scaled by the
+same counters on a copy of known size, made with --calib-copy); null when
+that file is absent.
 
-Inputs are resident in HBM before the timed region.  Decode steps cycle over
-NL distinct layer copies and NX distinct token batches so the weights each
-step reads are not left in the 256 MB MALL by the previous step.  Per-kernel
-device times come from HIP events the library records on the launch stream
-(ainfer_moe_profile_*) in a second pass over the same steps; the headline
-timed region runs without them.
+Inputs are resident in HBM before the timed region.  c4 reads 60 distinct
+layers per step (200 GB, far above the 256 MB MALL).  c1 decode steps cycle
+over NL distinct layer copies and NX distinct token batches for the same
+reason.  Per-kernel device times come from HIP events the library records on
+the launch stream (ainfer_moe_profile_*) in a second pass over the same
+steps; the headline timed region runs without them.
 
 The CPU baseline is the C oracle (oracle/libmoe_oracle.so, `port`) on the
-box's host cores, on a bounded sample of the same decode workload.
+box's host cores: one c4 block (layer 0, the same synthetic weights) timed
+for a bounded sample, median x 60 blocks.
 """
 import argparse
 import json
@@ -62,9 +70,10 @@ def experts_bytes(cfg, U, T):
     return w + 2 * T * cfg.hidden * 2
 
 
-def measured_traffic(kernel, T):
-    """HBM bytes per launch of `kernel` from the committed PMC summary, or None."""
-    f = ROOT / "profiles" / f"{kernel}_c1_T{T}_traffic.md"
+def measured_traffic(kernel, workload):
+    """HBM bytes per launch of `kernel` from the committed PMC summary
+    profiles/<kernel>_<workload>_traffic.md, or None."""
+    f = ROOT / "profiles" / f"{kernel}_{workload}_traffic.md"
     if not f.exists():
         return None
     for line in f.read_text().splitlines():
@@ -216,25 +225,29 @@ def run_c3(steps, warmup=5):
     return out
 
 
-def run_c4(steps, tokens=(1, 8), warmup=3):
+def run_c4(steps, tokens=(1, 8), warmup=3, keep_layer0=False):
     """60 blocks of config 3 (RMSNorm -> MoE -> residual,
     ainfer_moe_block_forward), one decode step = all 60 blocks in sequence on
-    a bf16 residual stream; 200 GB of weights resident."""
+    a bf16 residual stream; 200 GB of weights resident.  A second pass over
+    the same steps reads per-stage device times (HIP events on the launch
+    stream, mean per block)."""
     import torch
-    from ainfer_amd.moe import MoeLayer, make_input
+    from ainfer_amd import _lib as L
+    from ainfer_amd.moe import MoeLayer, make_input, rmsnorm
     from ainfer_amd.synthetic import CONFIGS, algorithmic_bytes
     cfg = CONFIGS["c4"]
+    log(f"[bench] c4: allocating {cfg.layers} layers "
+        f"({cfg.layers * cfg.layer_weight_bytes() / 1e9:.1f} GB)")
     layers = [MoeLayer(cfg, layer=i) for i in range(cfg.layers)]
     torch.cuda.synchronize()
     out = {}
     for T in tokens:
+        log(f"[bench] c4 T={T}")
         ws = layers[0].workspace(T)
         r0 = make_input(cfg, T, tag=4000 + T) * 4
-        a, b = r0.clone(), torch.empty_like(r0)
         # distinct routed experts per layer along the actual residual stream
         U = 0.0
         h = torch.empty_like(r0)
-        from ainfer_amd.moe import rmsnorm
         cur = r0.clone()
         for L_ in layers:
             rmsnorm(cur, h)
@@ -242,32 +255,60 @@ def run_c4(steps, tokens=(1, 8), warmup=3):
             nxt = torch.empty_like(cur)
             L_.block_forward(cur, nxt, ws)
             cur = nxt
-        for _ in range(warmup):
-            for L_ in layers:
-                L_.block_forward(a, b, ws)
-                a, b = b, a
+        # one decode step = one fresh token batch through all 60 blocks: block
+        # 0 reads x_s, the others update the residual in place
+        xs = [make_input(cfg, T, tag=4100 + 16 * T + i) * 4 for i in range(8)]
+        y = torch.empty_like(r0)
+
+        def step(s):
+            layers[0].block_forward(xs[s % len(xs)], y, ws)
+            for L_ in layers[1:]:
+                L_.block_forward(y, y, ws)
+        for s in range(warmup):
+            step(s)
         torch.cuda.synchronize()
         t0 = torch.cuda.Event(enable_timing=True)
         t1 = torch.cuda.Event(enable_timing=True)
-        a.copy_(r0)
         t0.record()
-        for _ in range(steps):
-            for L_ in layers:
-                L_.block_forward(a, b, ws)
-                a, b = b, a
+        for s in range(steps):
+            step(s)
         t1.record()
         torch.cuda.synchronize()
         us = t0.elapsed_time(t1) * 1e3 / steps
+        # profiled pass: mean device time per stage and block
+        L.profile_enable(True)
+        for s in range(steps):
+            step(s)
+        torch.cuda.synchronize()
+        st, _ = L.profile_read()
+        L.profile_enable(False)
+        Ul = U / len(layers)
         nbytes = sum(algorithmic_bytes(cfg, T, 0) for _ in layers) + round(U) * cfg.expert_bytes()
+        # dominant kernel of a block: the gate/up expert kernel when it runs
+        # on its own (stage 4), else the fused expert kernel (stage 5)
+        if st["gate_up"] > 0:
+            dom = {"kernel": "k_expert_lds<fp16, gate/up> (gate/up + SiLU of the routed and "
+                             "shared experts)", "file": "k_expert_gate_up",
+                   "alg_bytes": gateup_bytes(cfg, Ul), "us": st["gate_up"]}
+        else:
+            dom = {"kernel": "k_experts_decode (gate/up + down + combine)",
+                   "file": "k_experts_decode",
+                   "alg_bytes": experts_bytes(cfg, Ul, T), "us": st["down"]}
+        dom["gbs"] = dom["alg_bytes"] / (dom["us"] * 1e-6) / 1e9 if dom["us"] else 0.0
         out[str(T)] = {"us_per_step": round(us, 1), "us_per_token": round(us / T, 2),
-                       "unique_experts_per_layer": round(U / len(layers), 2),
+                       "us_per_block": round(us / len(layers), 2),
+                       "unique_experts_per_layer": round(Ul, 2),
                        "alg_bytes_per_step": nbytes,
                        "hbm_gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
-                       "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+                       "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                       "stage_us_per_block": {k: round(v, 3) for k, v in st.items() if v > 0},
+                       "dominant": dom}
+        log(f"[bench]   c4 T={T}: {json.dumps(out[str(T)])}")
         del ws
+    keep = layers[0] if keep_layer0 else None
     del layers
     torch.cuda.empty_cache()
-    return out
+    return out, keep
 
 
 def measured_peaks():
@@ -308,55 +349,76 @@ def measured_peaks():
             "bf16_gemm_frac_of_spec": round(tfs / MFMA_BF16_PEAK_TFS, 4)}
 
 
-def cpu_baseline(layer, cfg, T, budget_s):
-    """The C oracle on host cores, bounded to about budget_s seconds."""
+def host_cpu():
+    """(cores this process may run on, CPU model name) of the host."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return n, model
+
+
+def cpu_baseline(cfg, T, budget_s, blocks=1, layer=0):
+    """The C oracle's block (RMSNorm -> MoE -> residual) on host cores,
+    bounded to about budget_s seconds; the median block time is scaled by
+    `blocks` (the stack's depth: its blocks are alike in work)."""
     import numpy as np
-    import torch
     from oracle import oracle as O
-    from ainfer_amd.moe import make_input
+    from ainfer_amd.synthetic import input_seed
 
-    def host(t):
-        if t is None:
-            return None
-        if t.dtype in (torch.bfloat16, torch.float16):
-            return t.view(torch.int16).cpu().numpy().view(np.uint16)
-        return t.cpu().numpy()
-
-    hl = O.HostLayer(cfg.shape_tuple(), {n: host(t) for n, t in layer.t.items()})
-    threads = max(1, min(os.cpu_count() or 1, 16))
-    xs = [host(make_input(cfg, T, tag=9000 + i)) for i in range(8)]
-    hl.forward(xs[0], T, threads)  # warm
+    hl = O.HostLayer.synthetic(cfg, layer=layer)
+    avail, model = host_cpu()
+    threads = max(1, min(avail, 16))
+    # residual rows ~ 4 N(0,1) in bf16 bits, the same generator as the GPU's inputs
+    xs = [O.f32_to_bf16(O.bf16_to_f32(O.fill(O.FILL_BF16_NORMAL, input_seed(cfg.seed, 9000 + i),
+                                             1.0, T * cfg.hidden)) * 4).reshape(T, cfg.hidden)
+          for i in range(8)]
+    hl.block_forward(xs[0], T, threads=threads)  # warm
     times = []
     t_end = time.perf_counter() + budget_s
     i = 0
     while (time.perf_counter() < t_end or len(times) < 3) and len(times) < 2000:
         t = time.perf_counter()
-        hl.forward(xs[i % len(xs)], T, threads)
+        hl.block_forward(xs[i % len(xs)], T, threads=threads)
         times.append(time.perf_counter() - t)
         i += 1
     times.sort()
     med = times[len(times) // 2]
-    return {"value": med * 1e6 / T, "unit": "us/token", "cores": threads, "kind": "port",
-            "sample": f"c1 decode T={T}: {len(times)} layer calls of the C oracle "
-                      f"(median), {threads} threads, {len(xs)} distinct inputs"}
+    return {"value": round(med * blocks * 1e6 / T, 1), "unit": "us/token", "cores": threads,
+            "kind": "port", "host_cpus": avail, "cpu_model": model,
+            "sample": f"{cfg.name} T={T}: {len(times)} calls of the C oracle's block "
+                      f"(RMSNorm + MoE layer + residual) on layer {layer}, median "
+                      f"{med * 1e3:.2f} ms x {blocks} blocks, {threads} threads, "
+                      f"{len(xs)} distinct inputs"}
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=10,
+                    help="timed 60-block c4 steps (the headline); c1 decode runs 20x as many")
+    ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--layers", type=int, default=8, help="distinct c1 layer copies cycled")
     ap.add_argument("--tokens", default="1,4,16", help="c1 decode batch sizes")
+    ap.add_argument("--c4-tokens", default="1,8", help="c4 batch sizes (the first is the headline)")
     ap.add_argument("--prefill-steps", type=int, default=10)
     ap.add_argument("--no-prefill", action="store_true")
-    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-decode", action="store_true", help="skip the c1 decode lines")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemv", action="store_true", help="skip the W4A8 GEMV line")
     ap.add_argument("--no-c3", action="store_true", help="skip config 3 (H4096, 64 tokens)")
-    ap.add_argument("--no-c4", action="store_true", help="skip config 4 (60-layer stack, 200 GB)")
+    ap.add_argument("--no-c4", action="store_true",
+                    help="skip config 4 (no headline line: prints the details only)")
     ap.add_argument("--no-peaks", action="store_true", help="skip the measured-peak probes")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="finally copy MIB MiB device-to-device 5 times (PMC calibration)")
     args = ap.parse_args()
@@ -371,47 +433,45 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     stream = torch.cuda.current_stream()
-    c1 = CONFIGS["c1"]
-    log(f"[bench] allocating {args.layers} c1 layers "
-        f"({args.layers * c1.layer_weight_bytes() / 1e9:.1f} GB)")
-    layers = [MoeLayer(c1, layer=i) for i in range(args.layers)]
-    torch.cuda.synchronize()
+    c4cfg = CONFIGS["c4"]
 
+    # ---- headline: the 60-block c4 decode step -----------------------------
+    c4 = None
+    c4_tokens = [int(v) for v in args.c4_tokens.split(",")]
+    if not args.no_c4:
+        c4, _ = run_c4(args.steps, tokens=c4_tokens, warmup=args.warmup)
+
+    # ---- details -----------------------------------------------------------
+    c1 = CONFIGS["c1"]
     decode = {}
-    for T in ([] if args.no_decode else [int(v) for v in args.tokens.split(",")]):
-        log(f"[bench] c1 decode T={T}")
-        ms, st, U = run_decode(layers, c1, T, args.steps, args.warmup, 64, stream)
-        nbytes = algorithmic_bytes(c1, T, round(U))
-        # T <= 16: stage 2 is the routing kernel; the expert stages are one
-        # fused kernel (stage 5, T <= 2) or gate/up, down and combine
-        route_us = st["topk"]
-        ex_us = st["gate_up"] + st["down"] + st["combine"]
-        ex_bytes = experts_bytes(c1, U, T)
-        ex_gbs = ex_bytes / (ex_us * 1e-6) / 1e9 if ex_us > 0 else 0.0
-        if st["gate_up"] > 0:   # dominant kernel: gate/up
-            dom = ("k_expert_gate_up", "k_expert_lds<fp16, gate/up> (dominant decode kernel)",
-                   gateup_bytes(c1, U), st["gate_up"])
-        else:                   # dominant kernel: the fused expert kernel
-            dom = ("k_experts_decode",
-                   "k_experts_decode (gate/up + down + combine; dominant decode kernel)",
-                   ex_bytes, ex_us)
-        decode[T] = {
-            "us_per_step": ms * 1e3, "us_per_token": ms * 1e3 / T,
-            "unique_experts": U, "alg_bytes": nbytes,
-            "layer_hbm_gbs": nbytes / (ms * 1e-3) / 1e9,
-            "layer_hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
-            "route_us": round(route_us, 3), "experts_us": round(ex_us, 3),
-            "experts_gbs": ex_gbs, "experts_alg_bytes": ex_bytes,
-            "stage_us": {k: round(v, 3) for k, v in st.items() if v > 0},
-            "dominant": {"file": dom[0], "kernel": dom[1], "alg_bytes": dom[2],
-                         "us": round(dom[3], 3), "gbs": dom[2] / (dom[3] * 1e-6) / 1e9 if dom[3] else 0},
-        }
-        log(f"[bench]   {json.dumps(decode[T])}")
+    if not args.no_decode:
+        log(f"[bench] allocating {args.layers} c1 layers "
+            f"({args.layers * c1.layer_weight_bytes() / 1e9:.1f} GB)")
+        layers = [MoeLayer(c1, layer=i) for i in range(args.layers)]
+        torch.cuda.synchronize()
+        for T in [int(v) for v in args.tokens.split(",")]:
+            log(f"[bench] c1 decode T={T}")
+            ms, st, U = run_decode(layers, c1, T, 20 * args.steps, 20 * args.warmup, 64, stream)
+            nbytes = algorithmic_bytes(c1, T, round(U))
+            ex_us = st["gate_up"] + st["down"] + st["combine"]
+            ex_bytes = experts_bytes(c1, U, T)
+            decode[T] = {
+                "us_per_step": ms * 1e3, "us_per_token": ms * 1e3 / T,
+                "unique_experts": U, "alg_bytes": nbytes,
+                "layer_hbm_gbs": nbytes / (ms * 1e-3) / 1e9,
+                "layer_hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                "route_us": round(st["topk"], 3), "experts_us": round(ex_us, 3),
+                "experts_gbs": ex_bytes / (ex_us * 1e-6) / 1e9 if ex_us > 0 else 0.0,
+                "stage_us": {k: round(v, 3) for k, v in st.items() if v > 0},
+            }
+            if st["gate_up"] > 0:
+                decode[T]["gate_up_gbs"] = gateup_bytes(c1, U) / (st["gate_up"] * 1e-6) / 1e9
+            log(f"[bench]   {json.dumps(decode[T])}")
+        del layers
+        torch.cuda.empty_cache()
 
     prefill = None
     if not args.no_prefill:
-        del layers
-        torch.cuda.empty_cache()
         c2 = CONFIGS["c2"]
         T = 4096
         log("[bench] c2 prefill T=4096")
@@ -427,25 +487,18 @@ def main():
             "gate_up_tflops": gu_flops / (st["gate_up"] * 1e-6) / 1e12 if st["gate_up"] else 0,
         }
         log(f"[bench]   {json.dumps(prefill)}")
-        layers = [MoeLayer(c1, layer=0)]
+        del layer2
+        torch.cuda.empty_cache()
 
     gemv = None
     if not args.no_gemv:
         log("[bench] W4A8 GEMV 17408x5120")
-        gemv = run_gemv_w4a8(args.steps)
+        gemv = run_gemv_w4a8(20 * args.steps)
         log(f"[bench]   {json.dumps(gemv)}")
 
-    c3 = run_c3(min(args.steps, 100)) if not args.no_c3 else None
+    c3 = run_c3(100) if not args.no_c3 else None
     if c3:
         log(f"[bench] c3 T=64: {json.dumps(c3)}")
-    c4 = None
-    if not args.no_c4:
-        del layers
-        torch.cuda.empty_cache()
-        log("[bench] c4: 60-layer stack, T=1 and 8")
-        c4 = run_c4(max(3, min(args.steps // 20, 20)))
-        log(f"[bench]   {json.dumps(c4)}")
-        layers = [MoeLayer(c1, layer=0)]
     peaks = measured_peaks() if not args.no_peaks else None
 
     if args.calib_copy > 0:
@@ -457,52 +510,53 @@ def main():
         torch.cuda.synchronize()
         log(f"[bench] calibration copy: 5 x {n} bytes")
 
-    if not decode:
-        print(json.dumps({"prefill_c2_T4096": prefill, "gemv_w4a8": gemv, "c3_T64": c3,
-                          "c4_stack60": c4, "measured_peaks": peaks}), flush=True)
+    details = {
+        "c4_stack60": c4,
+        "decode_c1": {str(T): {k: (round(v, 4) if isinstance(v, float) else v)
+                               for k, v in d.items()} for T, d in decode.items()},
+        "prefill_c2_T4096": prefill,
+        "gemv_w4a8": gemv,
+        "c3_T64": c3,
+        "measured_peaks": peaks,
+    }
+    if c4 is None:
+        print(json.dumps(details), flush=True)
         return
-    Th = 16 if 16 in decode else max(decode)
-    d1 = decode[Th]
+    Th = c4_tokens[0]
+    h = c4[str(Th)]
+    dom = h["dominant"]
 
     cpu = None
     if not args.no_cpu:
-        log(f"[bench] cpu baseline T={Th}")
-        cpu = cpu_baseline(layers[0], c1, Th, args.cpu_seconds)
+        log(f"[bench] cpu baseline: c4 block T={Th}, x{c4cfg.layers}")
+        cpu = cpu_baseline(c4cfg, Th, args.cpu_seconds, blocks=c4cfg.layers)
         log(f"[bench]   {json.dumps(cpu)}")
     out = {
         "metric": METRIC,
-        "value": round(d1["us_per_token"], 3),
+        "value": h["us_per_token"],
         "unit": "us/token",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": d1["us_per_step"] / 1e3,
+        "ms_per_step": round(h["us_per_step"] / 1e3, 4),
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (seeded counter-based generator; random-init INT4 weights)",
-        "config": {"workload": f"c1 decode T={Th}: H2048 E512 top-10 I512 + 1 shared expert "
-                               "(sigmoid gate), INT4 g128 fp16 scales",
-                   "layer_copies": args.layers, "global_batch": Th,
-                   "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "achieved": round(d1["dominant"]["gbs"], 1),
+        "config": {"workload": f"c4 decode T={Th}: 60 sequential blocks (RMSNorm -> MoE layer "
+                               "-> residual), each H4096 E512 top-10 I1024 + 1 shared expert "
+                               "(sigmoid gate), INT4 g128 fp16 scales, 200 GB resident",
+                   "global_batch": Th, "layers": c4cfg.layers, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(dom["gbs"], 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(d1["dominant"]["gbs"] / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic(d1["dominant"]["file"], Th),
-                     "kernel": d1["dominant"]["kernel"],
-                     "alg_bytes_per_launch": round(d1["dominant"]["alg_bytes"])},
+                     "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(dom["file"], f"c4_T{Th}"),
+                     "kernel": dom["kernel"],
+                     "alg_bytes_per_launch": round(dom["alg_bytes"]),
+                     "us_per_launch": round(dom["us"], 3)},
         "cpu_baseline": cpu,
-        "details": {
-            f"layer_hbm_frac_T{Th}": round(d1["layer_hbm_frac"], 4),
-            "decode": {str(T): {k: (round(v, 4) if isinstance(v, float) else v)
-                                for k, v in d.items()} for T, d in decode.items()},
-            "prefill_c2_T4096": prefill,
-            "gemv_w4a8": gemv,
-            "c3_T64": c3,
-            "c4_stack60": c4,
-            "measured_peaks": peaks,
-        },
+        "details": dict(step_hbm_frac=h["hbm_frac"], **details),
     }
     print(json.dumps(out), flush=True)
 

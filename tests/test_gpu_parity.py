@@ -227,13 +227,18 @@ def test_prefill_zipf_parity_on_token_sample(torch, oracle):
     assert torch.equal(y.view(torch.int16), y2.view(torch.int16))
 
 
-def midpoint_row(H, torch):
-    """A row whose mean square is exactly a float midpoint (0.5 + 2^-25):
-    the device's order-independence test fails on it, so the RMSNorm takes
+def midpoint_row(H, torch, tiny=True):
+    """A row (H = 2048 or 4096) whose mean square is a float midpoint,
+    0.5 + 2^-25: H/2 ones and H/2048 elements 2^-7.  Its sum of squares is
+    exact in every order, so the device takes the tree sum (exactness test).
+    With `tiny`, one element 2^-40 makes the sum inexact while the mean stays
+    within 2^-70 of the midpoint: neither test passes and the RMSNorm takes
     its sequential re-sum."""
     r = torch.zeros(H, dtype=torch.float32)
     r[:H // 2] = 1.0
-    r[H // 2:H // 2 + 2] = 2.0 ** -7
+    r[H // 2:H // 2 + H // 2048] = 2.0 ** -7
+    if tiny:
+        r[H - 3] = 2.0 ** -40
     return r.to(torch.bfloat16)
 
 
@@ -246,6 +251,9 @@ def test_rmsnorm_bit_exact(torch, oracle):
         x = torch.randn(T, H, device="cuda").to(torch.bfloat16) * 3
         if H == 4096 or H == 2048:
             x[0] = midpoint_row(H, torch).cuda()
+            if T > 2:
+                x[1] = midpoint_row(H, torch, tiny=False).cuda()
+                x[2, 7] = 2.0 ** -50      # inexact sum: the interval test
         w = torch.randn(H, device="cuda").to(torch.bfloat16)
         for mode in (L.NORM_PLAIN, L.NORM_ONE_PLUS):
             for ww in (None, w):
@@ -306,6 +314,8 @@ def test_block_forward_fused_norm(torch, oracle, mode):
     layer = MoeLayer(cfg, layer=7)
     x = make_input(cfg, 17, tag=41) * 3
     x[1] = midpoint_row(cfg.hidden, torch).cuda()   # the sequential re-sum in both kernels
+    x[2] = midpoint_row(cfg.hidden, torch, tiny=False).cuda()  # exact sum on a midpoint
+    x[3, 11] = 2.0 ** -50                           # inexact sum: the interval test
     g = torch.Generator().manual_seed(5)
     nw = (torch.randn(cfg.hidden, generator=g) * 0.5 + (0.0 if nm == L.NORM_ONE_PLUS else 1.0))
     nw = nw.to(torch.bfloat16).cuda()

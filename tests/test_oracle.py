@@ -160,44 +160,85 @@ def test_rmsnorm_sum_order_follows_reference(oracle):
             assert oracle.rms_sumsq(x) == want, H
 
 
-def _rms_mean_stable(tot, H):
-    """Python statement of the order-independence test the device RMSNorm
-    applies (moe_common.h rms_mean_f)."""
+def _qexp_min(xb):
+    """Smallest exponent field over a bf16 row's non-zero elements (1 for
+    subnormals), as the device RMSNorm computes it (moe_common.h bf16_qexp)."""
+    e = ((xb >> 7) & 0xFF).astype(np.int64)
+    e = np.where(e == 0, 1, e)
+    e = np.where((xb & 0x7FFF) == 0, 0x7FFF, e)
+    return int(e.min())
+
+
+def _rms_mean_stable(tot, H, emin=0):
+    """Python statement of the two order-independence tests the device
+    RMSNorm applies (moe_common.h rms_mean_f): (1) every partial sum exact
+    (total below 2^53 quanta of the smallest square), (2) the interval of
+    every order's rounding around tot/H inside one float."""
     d = tot / H
+    if emin > 0 and tot < math.ldexp(1.0, 2 * emin - 268 + 53):
+        return True, np.float32(d)
     m = (H + 8) * 2.0 ** -52
     return np.float32(d * (1 - m)) == np.float32(d * (1 + m)), np.float32(d)
 
 
+def _tree_sum(sq):
+    tree = sq.reshape(-1, 256).sum(axis=0)
+    st = 128
+    while st:
+        tree = tree[:st] + tree[st:2 * st]
+        st //= 2
+    return tree[0]
+
+
 def test_rmsnorm_mean_is_order_independent_when_stable(oracle):
-    """Where the interval test passes, the float mean from the tree order and
-    from the sequential order are equal; rows where the two orders' fp64
-    sums differ occur, so the test is not vacuous."""
+    """Where either test passes, the float mean from the tree order and from
+    the sequential order are equal; where the exactness test passes, the two
+    fp64 sums (and math.fsum's correctly rounded one) are equal outright.
+    Rows where the two orders' fp64 sums differ occur, so the tests are not
+    vacuous, and almost every row passes one test (the device's sequential
+    re-sum is rare)."""
     rng = np.random.default_rng(5)
     H = 4096
-    differ = stable = 0
-    for _ in range(3000):
-        x = oracle.bf16_to_f32(oracle.f32_to_bf16(
-            (rng.standard_normal(H) * 4).astype(np.float32))).astype(np.float64)
-        seq = np.cumsum(x * x)[-1]
-        tree = (x * x).reshape(16, 256).sum(axis=0)
-        st = 128
-        while st:
-            tree = tree[:st] + tree[st:2 * st]
-            st //= 2
-        tree = tree[0]
+    differ = stable = exact = 0
+    n = 3000
+    for i in range(n):
+        # standard normal rows, and rows of the synthetic generator's lattice
+        # (Irwin-Hall bytes), with an occasional tiny element
+        if i % 2:
+            f = (rng.standard_normal(H) * 4).astype(np.float32)
+        else:
+            f = (oracle.bf16_to_f32(oracle.fill(oracle.FILL_BF16_NORMAL, 100 + i, 1.0, H)) * 4)
+        if i % 7 == 0:
+            f[rng.integers(H)] = 2.0 ** -float(rng.integers(20, 60))
+        xb = oracle.f32_to_bf16(f.astype(np.float32))
+        x = oracle.bf16_to_f32(xb).astype(np.float64)
+        sq = x * x
+        seq = np.cumsum(sq)[-1]
+        tree = _tree_sum(sq)
         differ += seq != tree
-        ok, mean = _rms_mean_stable(tree, H)
+        emin = _qexp_min(xb)
+        if tot_exact := (tree < math.ldexp(1.0, 2 * emin - 268 + 53)):
+            exact += 1
+            assert seq == tree == math.fsum(sq)
+        ok, mean = _rms_mean_stable(tree, H, emin)
         if ok:
             stable += 1
             assert mean == np.float32(seq / H)
-    assert differ > 10 and stable > 2900
-    # a row whose mean is exactly a float midpoint fails the test (the device
-    # then re-sums sequentially): 2048 ones and two 2^-7, mean 0.5 + 2^-25
+        assert ok or not tot_exact
+    assert differ > 10 and exact > n // 2 and stable >= n - 3, (differ, exact, stable)
+    # a row whose mean is exactly a float midpoint passes only by exactness;
+    # with a tiny element added it passes neither (the device re-sums
+    # sequentially): 2048 ones and two 2^-7, mean 0.5 + 2^-25
     x = np.zeros(H)
     x[:2048] = 1.0
     x[2048:2050] = 2.0 ** -7
-    ok, _ = _rms_mean_stable(np.cumsum(x * x)[-1], H)
-    assert not ok
+    xb = oracle.f32_to_bf16(x.astype(np.float32))
+    tot = np.cumsum(x * x)[-1]
+    assert _rms_mean_stable(tot, H, 0)[0] is np.False_
+    assert _rms_mean_stable(tot, H, _qexp_min(xb))[0]
+    x[3000] = 2.0 ** -40
+    xb = oracle.f32_to_bf16(x.astype(np.float32))
+    assert not _rms_mean_stable(np.cumsum(x * x)[-1], H, _qexp_min(xb))[0]
 
 
 # ---------------------------------------------------------------- router ---
