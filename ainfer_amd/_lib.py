@@ -16,12 +16,14 @@ NORM_PLAIN, NORM_ONE_PLUS = 0, 1
 ACT_F32, ACT_BF16 = 0, 1
 FILL_BYTES, FILL_BF16_NORMAL, FILL_FP16_ABSNORMAL, FILL_BF16_ABSNORMAL = 0, 1, 2, 3
 MAX_TOKENS = 65536
+STACK_MAX_TOKENS = 4
 
 # every symbol include/ainfer_moe.h declares
 EXPORTS = (
     "ainfer_moe_strerror", "ainfer_moe_validate", "ainfer_moe_workspace_bytes",
     "ainfer_moe_workspace_init", "ainfer_moe_workspace_check",
     "ainfer_moe_forward", "ainfer_moe_block_forward", "ainfer_moe_block_forward_noalloc",
+    "ainfer_moe_stack_workspace_bytes", "ainfer_moe_stack_table_bytes", "ainfer_moe_stack_prepare", "ainfer_moe_stack_forward",
     "ainfer_moe_route",
     "ainfer_moe_dispatch", "ainfer_moe_rmsnorm", "ainfer_moe_fill",
     "ainfer_moe_act_quant_i8", "ainfer_moe_int4_gemv_i8",
@@ -70,6 +72,12 @@ def lib():
         L.ainfer_moe_forward.argtypes = [sp, wp, P, P, I32, P, SZ, P]
         L.ainfer_moe_block_forward.argtypes = [sp, wp, P, I32, F, P, P, I32, P, SZ, P]
         L.ainfer_moe_block_forward_noalloc.argtypes = [sp, wp, P, I32, F, P, P, I32, P]
+        L.ainfer_moe_stack_workspace_bytes.restype = SZ
+        L.ainfer_moe_stack_workspace_bytes.argtypes = [sp, I32, I32]
+        L.ainfer_moe_stack_table_bytes.restype = SZ
+        L.ainfer_moe_stack_table_bytes.argtypes = [I32]
+        L.ainfer_moe_stack_prepare.argtypes = [sp, wp, C.POINTER(C.c_void_p), I32, P, SZ, P]
+        L.ainfer_moe_stack_forward.argtypes = [sp, P, I32, I32, F, P, P, I32, P, SZ, P]
         L.ainfer_moe_route.argtypes = [sp, wp, P, I32, P, P, P, P, P, SZ, P]
         L.ainfer_moe_dispatch.argtypes = [sp, P, I32, P, P, P, P, P, SZ, P]
         L.ainfer_moe_rmsnorm.argtypes = [P, P, I32, F, P, I32, I32, P]

@@ -67,6 +67,7 @@ struct ProfCall {
 };
 
 struct Layout {
+  size_t stack_flags, stack_cap, stack_end;
   size_t sync, sync_words, slots, tiles2, n_tiles2, logits, sg_logit, idx, w, sg, xperm, chunk_counts, rank, counts, offsets, perm, inv,
       ptok, tiles, n_tiles, ticket, act, act_s, o, h, wnorm, xsum, asum, asum_s, total;
 };
@@ -103,6 +104,11 @@ Layout layout_of(const ainfer_moe_shape &s, int Tm) {
     L.sync_words = L.slots + (size_t)DECODE_MAX_T * (E + 1);
     L.sync = take(L.sync_words * 4);
   }
+  // the decode-stack kernel's tagged logit slots and item flags: also the
+  // same place for every T, zeroed with the sync region
+  L.stack_cap = (size_t)max_tiles_bound(s, DECODE_NORM_MAX_T, DEC_MT);
+  L.stack_flags = take((size_t)stack_flag_words(s, (int)L.stack_cap) * 4);
+  L.stack_end = off;
   L.logits = take(T * E * 4);
   L.sg_logit = take(T * 4);
   L.idx = take(T * k * 4);
@@ -238,15 +244,7 @@ ExpertArgs expert_args(const ainfer_moe_shape *s, const ainfer_moe_weights *w, c
 #endif
 // norm (decode path only, ainfer_moe_block_forward): x is the residual stream and
 // the routing kernel applies the RMSNorm itself
-// k-groups per wave of the 4-token down items: whole 256-byte row segments
-// once the down K (the intermediate size) has 8 groups or more
-#ifndef DOWN_KBW4_MIN_I
-#define DOWN_KBW4_MIN_I 1024  // c3 T=64: down 149.5 -> 139.5 us; c1 (I = 512) keeps 2
-#endif
-int down_kbw(const ainfer_moe_shape &s) {
-  const int I = s.inter > s.shared_inter ? s.inter : s.shared_inter;
-  return I >= DOWN_KBW4_MIN_I ? 4 : DEC_KBW_DOWN;
-}
+int down_kbw(const ainfer_moe_shape &s) { return down_kbw_of(s); }
 
 int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const void *x,
                const void *resid, void *y, int T, void *ws, hipStream_t st,
@@ -273,7 +271,13 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
     pc->end(2);
     ExpertArgs gu = expert_args(s, w, L, ws, d, T, 0), dn = expert_args(s, w, L, ws, d, T, 1);
     if (T <= FUSED_EXPERTS_MAX_T) {
-      // latency-bound: gate/up, down and combine in one launch
+      // latency-bound: gate/up, down and combine in one launch (T = 1: the
+      // gate/up items in a launch of their own first)
+      if (T == 1) {
+        HIP_TRY(launch_expert_stream(0, s->scale_dtype, gu, max_tiles_bound(*s, T, DEC_MT), 4,
+                                     DEC_RG_GATE_UP, DEC_MT, st));
+        pc->end(4);
+      }
       HIP_TRY(launch_experts_decode(s->scale_dtype, dg, gu, dn, at<float>(ws, L.w),
                                     at<float>(ws, L.sg), d.inv, resid, y, sync,
                                     max_tiles_bound(*s, T, DEC_MT),
@@ -551,7 +555,8 @@ int ainfer_moe_workspace_init(const ainfer_moe_shape *s, void *ws, size_t ws_byt
   if (rc) return rc;
   if ((rc = check_ws(s, 0, ws, ws_bytes))) return rc;
   const Layout L = layout_of(*s, 0);
-  HIP_TRY(launch_zero_i32(at<int32_t>(ws, L.sync), (int)L.sync_words, (hipStream_t)stream));
+  HIP_TRY(launch_zero_i32(at<int32_t>(ws, L.sync), (int)((L.stack_end - L.sync) / 4),
+                          (hipStream_t)stream));
   return AINFER_OK;
 }
 
@@ -611,6 +616,74 @@ int ainfer_moe_block_forward_noalloc(const ainfer_moe_shape *s, const ainfer_moe
   const Layout L0 = layout_of(*s, 0);
   HIP_TRY(launch_zero_i32(at<int32_t>(ws, L0.sync), (int)L0.sync_words, st));
   return do_block(s, w, norm_w, norm_mode, eps, resid_in, resid_out, T, ws, st);
+}
+
+size_t ainfer_moe_stack_table_bytes(int32_t n_layers) {
+  return n_layers > 0 ? (size_t)n_layers * sizeof(StackLayer) : 0;
+}
+
+int ainfer_moe_stack_prepare(const ainfer_moe_shape *s, const ainfer_moe_weights *layers,
+                             const void *const *norm_w, int32_t n_layers, void *table,
+                             size_t table_bytes, void *stream) {
+  int rc = ainfer_moe_validate(s);
+  if (rc) return rc;
+  if (n_layers <= 0) return AINFER_ERR_ARG;
+  if (!layers || !table) return AINFER_ERR_NULL;
+  if (((uintptr_t)table) & 15 || table_bytes < ainfer_moe_stack_table_bytes(n_layers))
+    return AINFER_ERR_ARG;
+  std::vector<StackLayer> h((size_t)n_layers);
+  for (int l = 0; l < n_layers; ++l) {
+    if ((rc = check_weights(s, &layers[l]))) return rc;
+    memset(&h[l], 0, sizeof(StackLayer));
+    h[l].w = layers[l];
+    h[l].norm_w = norm_w ? norm_w[l] : nullptr;
+    if (h[l].norm_w && ((uintptr_t)h[l].norm_w & 15)) return AINFER_ERR_ARG;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  HIP_TRY(hipMemcpyAsync(table, h.data(), h.size() * sizeof(StackLayer), hipMemcpyHostToDevice,
+                         st));
+  HIP_TRY(hipStreamSynchronize(st));  // h is released on return
+  return AINFER_OK;
+}
+
+size_t ainfer_moe_stack_workspace_bytes(const ainfer_moe_shape *s, int32_t max_tokens,
+                                        int32_t n_layers) {
+  if (ainfer_moe_validate(s) != AINFER_OK) return 0;
+  if (max_tokens < 1 || max_tokens > DECODE_NORM_MAX_T || n_layers < 1) return 0;
+  StackGeom g;
+  if (!stack_geometry(*s, max_tokens, &g)) return 0;
+  return layout_of(*s, 1).total + (size_t)n_layers * stack_layer_bytes(*s, max_tokens, nullptr);
+}
+
+int ainfer_moe_stack_forward(const ainfer_moe_shape *s, const void *table, int32_t n_layers,
+                             int32_t norm_mode, float eps, const void *resid_in,
+                             void *resid_out, int32_t T, void *ws, size_t ws_bytes,
+                             void *stream) {
+  int rc = ainfer_moe_validate(s);
+  if (rc) return rc;
+  if (T < 0 || T > DECODE_NORM_MAX_T) return AINFER_ERR_TOKENS;
+  if (n_layers < 0) return AINFER_ERR_ARG;
+  if (norm_mode != AINFER_NORM_PLAIN && norm_mode != AINFER_NORM_ONE_PLUS) return AINFER_ERR_ARG;
+  if (!(eps >= 0.0f)) return AINFER_ERR_ARG;
+  if (T == 0 || n_layers == 0) return AINFER_OK;
+  if (!table || !resid_in || !resid_out) return AINFER_ERR_NULL;
+  if (((uintptr_t)table) & 15 || ((uintptr_t)resid_in) & 15 || ((uintptr_t)resid_out) & 15)
+    return AINFER_ERR_ARG;
+  StackGeom g;
+  if (!stack_geometry(*s, T, &g)) return AINFER_ERR_SHAPE;
+  if (!ws) return AINFER_ERR_NULL;
+  if (((uintptr_t)ws) & 255) return AINFER_ERR_WORKSPACE;
+  const Layout L = layout_of(*s, 1);
+  if (ws_bytes < L.total + (size_t)n_layers * stack_layer_bytes(*s, T, nullptr))
+    return AINFER_ERR_WORKSPACE;
+  StackWs w;
+  w.flags = at<int32_t>(ws, L.stack_flags);
+  w.cap = (int)L.stack_cap;
+  w.layers = at<uint8_t>(ws, L.total);
+  w.err = at<int32_t>(ws, L.sync) + SY_ERR;
+  HIP_TRY(launch_decode_stack(s->scale_dtype, *s, g, (const StackLayer *)table, n_layers,
+                              resid_in, resid_out, T, norm_mode, eps, w, (hipStream_t)stream));
+  return AINFER_OK;
 }
 
 int ainfer_moe_route(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const void *x,

@@ -171,6 +171,15 @@ template <typename V>
 __device__ __forceinline__ void st_dev(V *p, V v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// threadIdx.x, opaque to the optimiser: in a persistent kernel's loops it
+// keeps lane-dependent addresses from being hoisted out of the loop and held
+// live (spilled) across every phase.  No instructions.
+__device__ __forceinline__ int tid_opaque() {
+  int t = threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
+}
+
 // every store this wave issued has completed
 __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 

@@ -119,8 +119,9 @@ __device__ __forceinline__ void expert_lds_item(const ExpertArgs &a, int4 t, int
   const int KB = K >> 7;
   if (slab * a.WR * RG * 16 >= N) return;
 
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
+  const int tx = tid_opaque();
+  const int wave = __builtin_amdgcn_readfirstlane(tx >> 6);
+  const int lane = tx & 63;
   const int kw = wave % a.WK, wr = wave / a.WK;
   const int m = lane & 15, q = lane >> 4;
   const int n0 = (slab * a.WR + wr) * RG * 16;
@@ -306,7 +307,7 @@ __device__ __forceinline__ void expert_lds_item(const ExpertArgs &a, int4 t, int
   if (ALIAS && wave != 0) return;
   // tokens < mcnt <= MT only
   const int nthr = ALIAS ? 64 : nw * 64;
-  for (int idx = ALIAS ? lane : (int)threadIdx.x; idx < a.WR * RG * 16 * MT; idx += nthr) {
+  for (int idx = ALIAS ? lane : tx; idx < a.WR * RG * 16 * MT; idx += nthr) {
     const int rgrp = idx / (16 * MT), cell = idx % (16 * MT);  // rgrp = wr * RG + g
     const int rwr = rgrp / RG, g = rgrp % RG;
     const int tm = cell >> 4, tn = cell & 15;

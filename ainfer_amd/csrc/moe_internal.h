@@ -201,9 +201,49 @@ hipError_t launch_route_decode(const void *x, const void *rw, const float *bias,
 // split: gate/up in a launch of its own first (measured faster at T = 1,
 // where the down items of a fused launch wait behind the gate/up items for
 // workgroup slots: c3 39.5 -> 33.0 us, c1 equal)
+// (split: only the down items and the combine; the caller has launched the
+// gate/up items, k_expert_lds, just before)
 hipError_t launch_experts_decode(int scale_dtype, const DecodeGeom &g, ExpertArgs gu,
                                  ExpertArgs dn, const float *w, const float *sg,
                                  const int32_t *inv, const void *resid, void *y,
                                  int32_t *sync, int max_tiles, int cap, bool split,
                                  hipStream_t s);
 hipError_t launch_zero_i32(int32_t *p, int n, hipStream_t s);
+
+// k-groups per wave of the 4-token down items: whole 256-byte row segments
+// once the down K (the intermediate size) has 8 groups or more
+#ifndef DOWN_KBW4_MIN_I
+#define DOWN_KBW4_MIN_I 1024  // c3 T=64: down 149.5 -> 139.5 us; c1 (I = 512) keeps 2
+#endif
+inline int down_kbw_of(const ainfer_moe_shape &s) {
+  const int I = s.inter > s.shared_inter ? s.inter : s.shared_inter;
+  return I >= DOWN_KBW4_MIN_I ? 4 : DEC_KBW_DOWN;
+}
+
+// ---- persistent decode stack (moe_stack.hip) ------------------------------
+// One entry of the device layer table (ainfer_moe_stack_prepare).
+struct StackLayer {
+  ainfer_moe_weights w;
+  const void *norm_w;  // RMSNorm weight [H] bf16, or null (unit)
+  const void *pad;
+};
+struct StackGeom {
+  int nw, wk_gu, wr_gu, wk_dn, wr_dn, kbw_dn, slabs_gu, slabs_dn;
+  size_t lds;
+};
+// The stack kernel's workspace pieces: its counters and item flags (in the
+// zeroed head of the workspace) and the per-layer regions.
+struct StackWs {
+  int32_t *flags;    // stack_flag_words
+  int cap;           // tile capacity of the item flag arrays
+  uint8_t *layers;   // n_layers regions of stack_layer_bytes(T)
+  int32_t *err;
+};
+// bytes of one layer's region at T tokens (offs: the 6 piece offsets)
+size_t stack_layer_bytes(const ainfer_moe_shape &s, int T, size_t *offs);
+// false when the shape has no stack geometry at T tokens (use block_forward)
+bool stack_geometry(const ainfer_moe_shape &s, int T, StackGeom *g);
+int stack_flag_words(const ainfer_moe_shape &s, int cap);
+hipError_t launch_decode_stack(int scale_dtype, const ainfer_moe_shape &s, const StackGeom &g,
+                               const StackLayer *layers, int L, const void *x0, void *r, int T,
+                               int norm_mode, float eps, const StackWs &w, hipStream_t st);

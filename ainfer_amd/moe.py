@@ -139,6 +139,46 @@ class MoeLayer:
         return counts, offsets, perm[:T * k], inv[:T * k]
 
 
+class MoeStack:
+    """L decoder-block MLP halves run as one persistent launch
+    (ainfer_moe_stack_forward, T <= 4): the layers' weights and per-layer
+    RMSNorm weights go into a device table once (ainfer_moe_stack_prepare)."""
+
+    def __init__(self, layers, norm_ws=None, device="cuda"):
+        assert layers, "a stack needs at least one layer"
+        self.layers = list(layers)
+        self.shape = self.layers[0].shape
+        n = len(self.layers)
+        lib = L.lib()
+        self.table = torch.empty(lib.ainfer_moe_stack_table_bytes(n), dtype=torch.uint8,
+                                 device=device)
+        arr = (L.Weights * n)(*[ly.weights for ly in self.layers])
+        self.norm_ws = list(norm_ws) if norm_ws is not None else None
+        nw = None
+        if self.norm_ws is not None:
+            assert len(self.norm_ws) == n
+            nw = (C.c_void_p * n)(*[_ptr(w) for w in self.norm_ws])
+        L.check(lib.ainfer_moe_stack_prepare(C.byref(self.shape), arr, nw, n,
+                                             _ptr(self.table), self.table.numel(), None))
+
+    def workspace(self, max_tokens: int) -> torch.Tensor:
+        lib = L.lib()
+        n = lib.ainfer_moe_stack_workspace_bytes(C.byref(self.shape), max_tokens, len(self.layers))
+        if n == 0:
+            raise L.MoeError("invalid shape or token count for a stack workspace")
+        ws = torch.empty(n + 256, dtype=torch.uint8, device=self.table.device)
+        off = (-ws.data_ptr()) % 256
+        ws = ws[off:off + n]
+        L.check(lib.ainfer_moe_workspace_init(C.byref(self.shape), _ptr(ws), n, _stream(None)))
+        return ws
+
+    def forward(self, resid_in, resid_out, ws, norm_mode=L.NORM_PLAIN, eps=1e-6, stream=None):
+        T = resid_in.shape[0]
+        return L.check(L.lib().ainfer_moe_stack_forward(
+            C.byref(self.shape), _ptr(self.table), len(self.layers), norm_mode, eps,
+            _ptr(resid_in), _ptr(resid_out), T, _ptr(ws), ws.numel(), _stream(stream)))
+
+
 def make_input(cfg: MoeConfig, T: int, tag: int = 0, device="cuda", stream=None):
     """x[T][H] bf16 ~ N(0, 1) (standardised Irwin-Hall), seeded by (cfg.seed, tag)."""
     x = torch.empty(T, cfg.hidden, dtype=torch.bfloat16, device=device)

@@ -225,7 +225,7 @@ def run_c3(steps, warmup=5):
     return out
 
 
-def run_c4(steps, tokens=(1, 8), warmup=3, keep_layer0=False):
+def run_c4(steps, tokens=(1, 8), warmup=3, keep_layer0=False, stack=True):
     """60 blocks of config 3 (RMSNorm -> MoE -> residual,
     ainfer_moe_block_forward), one decode step = all 60 blocks in sequence on
     a bf16 residual stream; 200 GB of weights resident.  A second pass over
@@ -233,7 +233,7 @@ def run_c4(steps, tokens=(1, 8), warmup=3, keep_layer0=False):
     stream, mean per block)."""
     import torch
     from ainfer_amd import _lib as L
-    from ainfer_amd.moe import MoeLayer, make_input, rmsnorm
+    from ainfer_amd.moe import MoeLayer, MoeStack, make_input, rmsnorm
     from ainfer_amd.synthetic import CONFIGS, algorithmic_bytes
     cfg = CONFIGS["c4"]
     log(f"[bench] c4: allocating {cfg.layers} layers "
@@ -295,6 +295,22 @@ def run_c4(steps, tokens=(1, 8), warmup=3, keep_layer0=False):
                    "file": "k_experts_decode",
                    "alg_bytes": experts_bytes(cfg, Ul, T), "us": st["down"]}
         dom["gbs"] = dom["alg_bytes"] / (dom["us"] * 1e-6) / 1e9 if dom["us"] else 0.0
+        stack_us = None
+        use_stack = stack
+        if use_stack and T <= L.STACK_MAX_TOKENS:
+            # the same step as one persistent launch (ainfer_moe_stack_forward)
+            stk = MoeStack(layers)
+            sws = stk.workspace(T)
+            for s in range(warmup):
+                stk.forward(xs[s % len(xs)], y, sws)
+            torch.cuda.synchronize()
+            t0.record()
+            for s in range(steps):
+                stk.forward(xs[s % len(xs)], y, sws)
+            t1.record()
+            torch.cuda.synchronize()
+            stack_us = round(t0.elapsed_time(t1) * 1e3 / steps, 1)
+            del stk, sws
         out[str(T)] = {"us_per_step": round(us, 1), "us_per_token": round(us / T, 2),
                        "us_per_block": round(us / len(layers), 2),
                        "unique_experts_per_layer": round(Ul, 2),
@@ -302,7 +318,8 @@ def run_c4(steps, tokens=(1, 8), warmup=3, keep_layer0=False):
                        "hbm_gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
                        "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                        "stage_us_per_block": {k: round(v, 3) for k, v in st.items() if v > 0},
-                       "dominant": dom}
+                       "dominant": dom,
+                       "stack_launch_us_per_step": stack_us}
         log(f"[bench]   c4 T={T}: {json.dumps(out[str(T)])}")
         del ws
     keep = layers[0] if keep_layer0 else None
@@ -418,6 +435,8 @@ def main():
     ap.add_argument("--no-c4", action="store_true",
                     help="skip config 4 (no headline line: prints the details only)")
     ap.add_argument("--no-peaks", action="store_true", help="skip the measured-peak probes")
+    ap.add_argument("--no-stack", action="store_true",
+                    help="skip the one-launch stack timing of c4 (ainfer_moe_stack_forward)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="finally copy MIB MiB device-to-device 5 times (PMC calibration)")
@@ -439,7 +458,7 @@ def main():
     c4 = None
     c4_tokens = [int(v) for v in args.c4_tokens.split(",")]
     if not args.no_c4:
-        c4, _ = run_c4(args.steps, tokens=c4_tokens, warmup=args.warmup)
+        c4, _ = run_c4(args.steps, tokens=c4_tokens, warmup=args.warmup, stack=not args.no_stack)
 
     # ---- details -----------------------------------------------------------
     c1 = CONFIGS["c1"]

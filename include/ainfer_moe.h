@@ -163,6 +163,39 @@ int ainfer_moe_block_forward(const ainfer_moe_shape *shape,
                              void *workspace, size_t workspace_bytes,
                              void *stream);
 
+/* ---- decode stack: many blocks in one launch ----------------------------
+ * The reference records each layer's command list once at init and replays
+ * the recorded lists every decode step (tools/decode/decode_l0.cpp:553-677,
+ * the MLP part :663-674).  Here the init step writes a device table of the
+ * layers' weights (ainfer_moe_stack_prepare) and one call runs all of them:
+ *   for l in 0..n_layers-1:  r = bf16(r + MoE_l(RMSNorm_l(r)))
+ * with r = resid_in at the start and resid_out at the end (resid_out may
+ * alias resid_in).  Each layer's output is bit-identical to
+ * ainfer_moe_block_forward on the same input, so the stack equals n_layers
+ * chained block_forward calls.  T <= 4 tokens (AINFER_ERR_TOKENS above);
+ * shapes without a stack geometry (K split of more than 8 waves) return
+ * AINFER_ERR_SHAPE, and callers use block_forward.  The workspace
+ * (ainfer_moe_stack_workspace_bytes: every layer's intermediates get a
+ * region of their own, about 0.5 MB per layer at H4096/E512/k10/I1024,
+ * T = 4) is initialised once with ainfer_moe_workspace_init; it also serves
+ * the per-block entries at T = 1.  Calls on one workspace must not overlap. */
+size_t ainfer_moe_stack_workspace_bytes(const ainfer_moe_shape *shape,
+                                        int32_t max_tokens, int32_t n_layers);
+size_t ainfer_moe_stack_table_bytes(int32_t n_layers);
+/* layers: host array [n_layers] of device weight pointers (validated as in
+ * forward); norm_w: host array [n_layers] of device RMSNorm weights ([H]
+ * bf16, 16-byte aligned, NULL entries = unit weight), or NULL for all unit.
+ * table: device memory of ainfer_moe_stack_table_bytes, 16-byte aligned.
+ * Blocks until the table is written (an init-time call). */
+int ainfer_moe_stack_prepare(const ainfer_moe_shape *shape,
+                             const ainfer_moe_weights *layers,
+                             const void *const *norm_w, int32_t n_layers,
+                             void *table, size_t table_bytes, void *stream);
+int ainfer_moe_stack_forward(const ainfer_moe_shape *shape, const void *table,
+                             int32_t n_layers, int32_t norm_mode, float eps,
+                             const void *resid_in, void *resid_out, int32_t T,
+                             void *workspace, size_t workspace_bytes, void *stream);
+
 /* Bytes of the static device scratch behind ainfer_moe_block_forward_noalloc
  * (one copy per GPU the library runs on, held until the process ends). */
 #define AINFER_MOE_NOALLOC_SCRATCH_BYTES (16u << 20)
@@ -266,9 +299,10 @@ int ainfer_moe_fill(int32_t kind, uint64_t seed, float std_, size_t n,
  * tools/decode/decode_l0.cpp:705,714-725,870-884, with device events) -----
  * While enabled, forward/block_forward record a HIP event on the caller's
  * stream before and after every kernel.  For T <= 16 stage 2 is the routing
- * kernel (logits, top-k, weights, dispatch) and stages 1 and 3 read 0; for
- * T <= 2 stage 5 is the fused expert kernel (gate/up, down and combine) and
- * stages 4 and 6 read 0.  ainfer_moe_profile_read()
+ * kernel (logits, top-k, weights, dispatch) and stages 1 and 3 read 0; at
+ * T = 1 stage 5 is the down + combine kernel (stage 4 the gate/up kernel) and
+ * at T = 2 the fused expert kernel (gate/up, down and combine), with stage 6
+ * (and at T = 2 stage 4) reading 0.  ainfer_moe_profile_read()
  * waits for them and returns, per stage, the mean device time in
  * microseconds over the calls since enable, and the call count.  Stages:
  * 0 rmsnorm, 1 router, 2 top-k (+ dispatch when T <= 64), 3 dispatch,
