@@ -144,6 +144,14 @@ P *at(void *ws, size_t off) {
   return (P *)((char *)ws + off);
 }
 
+// Calls above AINFER_MOE_CHUNK_TOKENS tokens run as consecutive chunks of at
+// most that many tokens on one workspace (the chunked prefill of the
+// reference's recorded ChunkGemm lists): the workspace and every buffer offset
+// stay those of one chunk.  Each token's routing and expert rows are computed
+// within its chunk.
+constexpr int CHUNK = AINFER_MOE_CHUNK_TOKENS;
+int chunk_of(int T) { return T < CHUNK ? T : CHUNK; }
+
 int check_ws(const ainfer_moe_shape *s, int T, void *ws, size_t ws_bytes) {
   if (!ws) return AINFER_ERR_NULL;
   if (((uintptr_t)ws) & 255) return AINFER_ERR_WORKSPACE;
@@ -505,6 +513,42 @@ int noalloc_scratch(void **out) {
 
 }  // namespace
 
+namespace {
+int do_route(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const void *x, int T,
+             int32_t *topk_idx, float *topk_w, float *shared_gate, float *logits, void *ws,
+             hipStream_t st) {
+  const Layout L = layout_of(*s, T);
+  DecodeGeom dg;
+  if (T <= DECODE_MAX_T && decode_geometry(*s, &dg)) {
+    // the decode routing kernel, without its dispatch
+    HIP_TRY(launch_route_decode(x, w->router_w, w->router_bias, w->shared_gate_w,
+                                logits ? logits : at<float>(ws, L.logits),
+                                at<float>(ws, L.sg_logit), topk_idx, topk_w, shared_gate, nullptr,
+                                T, s->hidden, s->n_experts, s->top_k, s->shared_inter > 0,
+                                nullptr, at<int32_t>(ws, L.sync),
+                                at<uint32_t>(ws, L.sync) + L.slots, nullptr, st));
+    return AINFER_OK;
+  }
+  if (T <= EXACT_ROUTER_MAX_T) {
+    HIP_TRY(launch_router_exact(x, w->router_w, w->router_bias, w->shared_gate_w,
+                                logits ? logits : at<float>(ws, L.logits),
+                                at<float>(ws, L.sg_logit), topk_idx, topk_w, shared_gate, nullptr,
+                                T, s->hidden, s->n_experts, s->top_k, s->shared_inter > 0,
+                                nullptr, st));
+    return AINFER_OK;
+  }
+  HIP_TRY(launch_router_fast(x, w->router_w, w->router_bias, w->shared_gate_w,
+                             at<float>(ws, L.logits), at<float>(ws, L.wnorm), topk_idx, topk_w,
+                             shared_gate, nullptr, nullptr, T, s->hidden, s->n_experts,
+                             s->top_k, s->shared_inter > 0, nullptr, st));
+  // the full canonical logits, on request (lane-strided chunk order, VALU)
+  if (logits)
+    HIP_TRY(launch_router(x, w->router_w, w->router_bias, w->shared_gate_w, logits,
+                          at<float>(ws, L.sg_logit), nullptr, T, s->hidden, s->n_experts, st));
+  return AINFER_OK;
+}
+}  // namespace
+
 extern "C" {
 
 const char *ainfer_moe_strerror(int status) {
@@ -546,7 +590,7 @@ int ainfer_moe_validate(const ainfer_moe_shape *s) {
 size_t ainfer_moe_workspace_bytes(const ainfer_moe_shape *s, int32_t max_tokens) {
   if (ainfer_moe_validate(s) != AINFER_OK) return 0;
   if (max_tokens < 0 || max_tokens > AINFER_MOE_MAX_TOKENS) return 0;
-  return layout_of(*s, max_tokens).total;
+  return layout_of(*s, chunk_of(max_tokens)).total;
 }
 
 int ainfer_moe_workspace_init(const ainfer_moe_shape *s, void *ws, size_t ws_bytes,
@@ -584,10 +628,16 @@ int ainfer_moe_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, c
   if ((rc = check_weights(s, w))) return rc;
   if (T == 0) return AINFER_OK;
   if (!x || !y) return AINFER_ERR_NULL;
-  if ((rc = check_ws(s, T, ws, ws_bytes))) return rc;
-  ProfCall pc((hipStream_t)stream);
-  pc.start();
-  return do_forward(s, w, x, nullptr, y, T, ws, (hipStream_t)stream, &pc);
+  if ((rc = check_ws(s, chunk_of(T), ws, ws_bytes))) return rc;
+  const size_t row = (size_t)s->hidden * 2;
+  for (int t0 = 0; t0 < T; t0 += CHUNK) {
+    ProfCall pc((hipStream_t)stream);
+    pc.start();
+    if ((rc = do_forward(s, w, (const char *)x + t0 * row, nullptr, (char *)y + t0 * row,
+                         chunk_of(T - t0), ws, (hipStream_t)stream, &pc)))
+      return rc;
+  }
+  return AINFER_OK;
 }
 
 int ainfer_moe_block_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w,
@@ -596,8 +646,13 @@ int ainfer_moe_block_forward(const ainfer_moe_shape *s, const ainfer_moe_weights
                              size_t ws_bytes, void *stream) {
   int rc = check_block_args(s, w, norm_mode, eps, resid_in, resid_out, T);
   if (rc || T == 0) return rc;
-  if ((rc = check_ws(s, T, ws, ws_bytes))) return rc;
-  return do_block(s, w, norm_w, norm_mode, eps, resid_in, resid_out, T, ws, (hipStream_t)stream);
+  if ((rc = check_ws(s, chunk_of(T), ws, ws_bytes))) return rc;
+  const size_t row = (size_t)s->hidden * 2;
+  for (int t0 = 0; t0 < T; t0 += CHUNK)
+    if ((rc = do_block(s, w, norm_w, norm_mode, eps, (const char *)resid_in + t0 * row,
+                       (char *)resid_out + t0 * row, chunk_of(T - t0), ws, (hipStream_t)stream)))
+      return rc;
+  return AINFER_OK;
 }
 
 int ainfer_moe_block_forward_noalloc(const ainfer_moe_shape *s, const ainfer_moe_weights *w,
@@ -606,7 +661,8 @@ int ainfer_moe_block_forward_noalloc(const ainfer_moe_shape *s, const ainfer_moe
                                      void *stream) {
   int rc = check_block_args(s, w, norm_mode, eps, resid_in, resid_out, T);
   if (rc || T == 0) return rc;
-  if (layout_of(*s, T).total > AINFER_MOE_NOALLOC_SCRATCH_BYTES) return AINFER_ERR_SCRATCH;
+  if (layout_of(*s, chunk_of(T)).total > AINFER_MOE_NOALLOC_SCRATCH_BYTES)
+    return AINFER_ERR_SCRATCH;
   void *ws = nullptr;
   if ((rc = noalloc_scratch(&ws))) return rc;
   hipStream_t st = (hipStream_t)stream;
@@ -615,7 +671,12 @@ int ainfer_moe_block_forward_noalloc(const ainfer_moe_shape *s, const ainfer_moe
   // an earlier call (that call's outputs are NaN) leaves nothing behind
   const Layout L0 = layout_of(*s, 0);
   HIP_TRY(launch_zero_i32(at<int32_t>(ws, L0.sync), (int)L0.sync_words, st));
-  return do_block(s, w, norm_w, norm_mode, eps, resid_in, resid_out, T, ws, st);
+  const size_t row = (size_t)s->hidden * 2;
+  for (int t0 = 0; t0 < T; t0 += CHUNK)
+    if ((rc = do_block(s, w, norm_w, norm_mode, eps, (const char *)resid_in + t0 * row,
+                       (char *)resid_out + t0 * row, chunk_of(T - t0), ws, st)))
+      return rc;
+  return AINFER_OK;
 }
 
 size_t ainfer_moe_stack_table_bytes(int32_t n_layers) {
@@ -695,36 +756,13 @@ int ainfer_moe_route(const ainfer_moe_shape *s, const ainfer_moe_weights *w, con
   if (!w || !w->router_w) return AINFER_ERR_NULL;
   if (T == 0) return AINFER_OK;
   if (!x || !topk_idx || !topk_w || !shared_gate) return AINFER_ERR_NULL;
-  if ((rc = check_ws(s, T, ws, ws_bytes))) return rc;
-  const Layout L = layout_of(*s, T);
-  hipStream_t st = (hipStream_t)stream;
-  DecodeGeom dg;
-  if (T <= DECODE_MAX_T && decode_geometry(*s, &dg)) {
-    // the decode routing kernel, without its dispatch
-    HIP_TRY(launch_route_decode(x, w->router_w, w->router_bias, w->shared_gate_w,
-                                logits ? logits : at<float>(ws, L.logits),
-                                at<float>(ws, L.sg_logit), topk_idx, topk_w, shared_gate, nullptr,
-                                T, s->hidden, s->n_experts, s->top_k, s->shared_inter > 0,
-                                nullptr, at<int32_t>(ws, L.sync),
-                                at<uint32_t>(ws, L.sync) + L.slots, nullptr, st));
-    return AINFER_OK;
-  }
-  if (T <= EXACT_ROUTER_MAX_T) {
-    HIP_TRY(launch_router_exact(x, w->router_w, w->router_bias, w->shared_gate_w,
-                                logits ? logits : at<float>(ws, L.logits),
-                                at<float>(ws, L.sg_logit), topk_idx, topk_w, shared_gate, nullptr,
-                                T, s->hidden, s->n_experts, s->top_k, s->shared_inter > 0,
-                                nullptr, st));
-    return AINFER_OK;
-  }
-  HIP_TRY(launch_router_fast(x, w->router_w, w->router_bias, w->shared_gate_w,
-                             at<float>(ws, L.logits), at<float>(ws, L.wnorm), topk_idx, topk_w,
-                             shared_gate, nullptr, nullptr, T, s->hidden, s->n_experts,
-                             s->top_k, s->shared_inter > 0, nullptr, st));
-  // the full canonical logits, on request (lane-strided chunk order, VALU)
-  if (logits)
-    HIP_TRY(launch_router(x, w->router_w, w->router_bias, w->shared_gate_w, logits,
-                          at<float>(ws, L.sg_logit), nullptr, T, s->hidden, s->n_experts, st));
+  if ((rc = check_ws(s, chunk_of(T), ws, ws_bytes))) return rc;
+  const int H = s->hidden, E = s->n_experts, k = s->top_k;
+  for (int t0 = 0; t0 < T; t0 += CHUNK)
+    if ((rc = do_route(s, w, (const char *)x + (size_t)t0 * H * 2, chunk_of(T - t0),
+                       topk_idx + (size_t)t0 * k, topk_w + (size_t)t0 * k, shared_gate + t0,
+                       logits ? logits + (size_t)t0 * E : nullptr, ws, (hipStream_t)stream)))
+      return rc;
   return AINFER_OK;
 }
 
@@ -733,7 +771,7 @@ int ainfer_moe_dispatch(const ainfer_moe_shape *s, const int32_t *topk_idx, int3
                         void *ws, size_t ws_bytes, void *stream) {
   int rc = ainfer_moe_validate(s);
   if (rc) return rc;
-  if (T < 0 || T > AINFER_MOE_MAX_TOKENS) return AINFER_ERR_TOKENS;
+  if (T < 0 || T > AINFER_MOE_CHUNK_TOKENS) return AINFER_ERR_TOKENS;
   if (!counts || !offsets) return AINFER_ERR_NULL;
   if (T > 0 && (!topk_idx || !perm)) return AINFER_ERR_NULL;
   if ((rc = check_ws(s, T, ws, ws_bytes))) return rc;

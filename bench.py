@@ -506,6 +506,14 @@ def main():
             "gate_up_tflops": gu_flops / (st["gate_up"] * 1e-6) / 1e12 if st["gate_up"] else 0,
         }
         log(f"[bench]   {json.dumps(prefill)}")
+        # chunked prefill: 16384 tokens as four 4096-token chunks on one workspace
+        T2 = 16384
+        ms2, st2, _ = run_prefill(layer2, c2, T2, max(2, args.prefill_steps // 2), 1, stream)
+        fl2 = algorithmic_flops(c2, T2)
+        prefill["chunked_T16384"] = {
+            "tokens_per_s": T2 / (ms2 * 1e-3), "ms_per_step": ms2,
+            "layer_mfma_frac": fl2 / (ms2 * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFS}
+        log(f"[bench]   chunked T=16384: {json.dumps(prefill['chunked_T16384'])}")
         del layer2
         torch.cuda.empty_cache()
 

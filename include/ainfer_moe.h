@@ -76,8 +76,15 @@ enum { AINFER_SCALE_BF16 = 0, AINFER_SCALE_FP16 = 1 };
  * (reference/operators_t14.npz rmsnorm_*) uses y = x*inv*w. */
 enum { AINFER_NORM_PLAIN = 0, AINFER_NORM_ONE_PLUS = 1 };
 
-/* Largest token count one call accepts (prefill chunk). */
+/* Largest token count one call accepts. */
 #define AINFER_MOE_MAX_TOKENS 65536
+/* Calls with more tokens than this run as consecutive chunks of at most this
+ * many tokens on one workspace (chunked prefill; the reference records its
+ * prefill GEMMs per chunk, tools/cmdlist/chunkgemm_replay.cpp): the
+ * workspace is the chunk's size (ainfer_moe_workspace_bytes stops growing
+ * here) and each token is routed and computed within its chunk.  The
+ * stage-level dispatch entry is not chunked (its permutation spans all T). */
+#define AINFER_MOE_CHUNK_TOKENS 4096
 
 typedef struct ainfer_moe_shape {
   int32_t hidden;       /* H, multiple of 128                               */
@@ -231,7 +238,7 @@ int ainfer_moe_route(const ainfer_moe_shape *shape,
                      float *shared_gate, float *logits, void *workspace,
                      size_t workspace_bytes, void *stream);
 
-/* Dispatch: counts[E], offsets[E+1] (exclusive scan of counts),
+/* Dispatch (T <= AINFER_MOE_CHUNK_TOKENS): counts[E], offsets[E+1] (exclusive scan of counts),
  * perm[T*k] (position p holds t*k + j, expert-contiguous, token ascending
  * within an expert) and inv_perm[T*k] (inverse of perm). */
 int ainfer_moe_dispatch(const ainfer_moe_shape *shape,
