@@ -10,6 +10,8 @@ LIB_PATH = Path(__file__).resolve().parent / "libainfer_moe.so"
 OK = 0
 ERR_SHAPE, ERR_NULL, ERR_WORKSPACE, ERR_TOKENS, ERR_HIP, ERR_ARG, ERR_SYNC, ERR_SCRATCH = (
     -1, -2, -3, -4, -5, -6, -7, -8)
+ERR_FORMAT, ERR_IO = -9, -10
+BINFER_LAYOUT_EXPERTS = 32
 NOALLOC_SCRATCH_BYTES = 16 << 20
 SCALE_BF16, SCALE_FP16 = 0, 1
 NORM_PLAIN, NORM_ONE_PLUS = 0, 1
@@ -28,6 +30,8 @@ EXPORTS = (
     "ainfer_moe_dispatch", "ainfer_moe_rmsnorm", "ainfer_moe_fill",
     "ainfer_moe_act_quant_i8", "ainfer_moe_int4_gemv_i8",
     "ainfer_moe_profile_enable", "ainfer_moe_profile_read", "ainfer_moe_debug_spin_limit",
+    "ainfer_binfer_open", "ainfer_binfer_close", "ainfer_binfer_error", "ainfer_binfer_moe_info",
+    "ainfer_binfer_moe_layer_bytes", "ainfer_binfer_load_moe_layer",
 )
 N_STAGES = 7
 STAGES = ("rmsnorm", "router", "topk", "dispatch", "gate_up", "down", "combine")
@@ -85,10 +89,20 @@ def lib():
         L.ainfer_moe_act_quant_i8.argtypes = [P, I32, I32, I32, P, P, P]
         L.ainfer_moe_int4_gemv_i8.argtypes = [P, P, I32, P, P, I32, I32, I32, P, P]
         L.ainfer_moe_profile_enable.argtypes = [I32]
+        L.ainfer_binfer_open.argtypes = [C.c_char_p, C.POINTER(P), C.c_char_p, SZ]
+        L.ainfer_binfer_close.restype = None
+        L.ainfer_binfer_close.argtypes = [P]
+        L.ainfer_binfer_error.restype = C.c_char_p
+        L.ainfer_binfer_error.argtypes = [P]
+        L.ainfer_binfer_moe_info.argtypes = [P, sp, C.POINTER(I32), C.POINTER(F)]
+        L.ainfer_binfer_moe_layer_bytes.restype = SZ
+        L.ainfer_binfer_moe_layer_bytes.argtypes = [P, I32]
+        L.ainfer_binfer_load_moe_layer.argtypes = [P, I32, P, SZ, wp, C.POINTER(P), P]
         L.ainfer_moe_debug_spin_limit.argtypes = [I32]
         L.ainfer_moe_profile_read.argtypes = [C.POINTER(C.c_float), I32, C.POINTER(I32)]
         for name in EXPORTS:
-            getattr(L, name).restype = getattr(L, name).restype or C.c_int
+            if name != "ainfer_binfer_close":
+                getattr(L, name).restype = getattr(L, name).restype or C.c_int
         _lib = L
     return _lib
 
@@ -109,3 +123,36 @@ def profile_read():
     n = C.c_int32(0)
     check(lib().ainfer_moe_profile_read(arr, N_STAGES, C.byref(n)))
     return dict(zip(STAGES, list(arr))), n.value
+
+
+class BinferFile:
+    """An opened, fully validated .binfer container (ainfer_binfer_open)."""
+
+    def __init__(self, path):
+        h = C.c_void_p()
+        err = C.create_string_buffer(512)
+        rc = lib().ainfer_binfer_open(str(path).encode(), C.byref(h), err, len(err))
+        if rc != OK:
+            raise MoeError(f"ainfer_binfer_open status {rc}: {err.value.decode()}")
+        self.h = h
+
+    def close(self):
+        if self.h:
+            lib().ainfer_binfer_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def moe_info(self):
+        s = Shape()
+        n = C.c_int32(0)
+        eps = C.c_float(0.0)
+        check(lib().ainfer_binfer_moe_info(self.h, C.byref(s), C.byref(n), C.byref(eps)))
+        return s, n.value, eps.value
+
+    def layer_bytes(self, layer):
+        return lib().ainfer_binfer_moe_layer_bytes(self.h, layer)

@@ -139,6 +139,32 @@ class MoeLayer:
         return counts, offsets, perm[:T * k], inv[:T * k]
 
 
+def load_binfer_layer(bf, layer, device="cuda"):
+    """Layer `layer` of an opened BinferFile, copied into a device arena: a
+    MoeLayer whose weights are the file's (no synthetic fill); its norm
+    weight (or None) is returned beside it."""
+    shape, n_layers, eps = bf.moe_info()
+    nbytes = bf.layer_bytes(layer)
+    arena = torch.empty(nbytes + 256, dtype=torch.uint8, device=device)
+    off = (-arena.data_ptr()) % 256
+    arena = arena[off:off + nbytes]
+    w = L.Weights()
+    nw = C.c_void_p()
+    L.check(L.lib().ainfer_binfer_load_moe_layer(bf.h, layer, _ptr(arena), nbytes, C.byref(w),
+                                                 C.byref(nw), _stream(None)))
+    ly = MoeLayer.__new__(MoeLayer)
+    ly.cfg = None
+    ly.device = device
+    ly.shape = shape
+    ly.weights = w
+    ly.t = {"arena": arena}
+    norm = None
+    if nw.value:
+        # a view of the arena at the norm weight's offset
+        norm = arena[nw.value - arena.data_ptr():][:shape.hidden * 2].view(torch.bfloat16)
+    return ly, norm
+
+
 class MoeStack:
     """L decoder-block MLP halves run as one persistent launch
     (ainfer_moe_stack_forward, T <= 4): the layers' weights and per-layer

@@ -65,8 +65,10 @@ enum {
   AINFER_ERR_HIP = -5,        /* a HIP runtime call failed                  */
   AINFER_ERR_ARG = -6,        /* another argument is out of range           */
   AINFER_ERR_SYNC = -7,       /* a device-side wait ran out (decode path)   */
-  AINFER_ERR_SCRATCH = -8     /* the call needs more than the static scratch
+  AINFER_ERR_SCRATCH = -8,    /* the call needs more than the static scratch
                                  of ainfer_moe_block_forward_noalloc holds    */
+  AINFER_ERR_FORMAT = -9,     /* a .binfer file fails validation            */
+  AINFER_ERR_IO = -10         /* a file cannot be opened or read            */
 };
 
 enum { AINFER_SCALE_BF16 = 0, AINFER_SCALE_FP16 = 1 };
@@ -251,6 +253,51 @@ int ainfer_moe_dispatch(const ainfer_moe_shape *shape,
  * Sum of squares in fp64, as RMSNormW (kernels.cpp:73-116). */
 int ainfer_moe_rmsnorm(const void *x, const void *w, int32_t norm_mode,
                        float eps, void *y, int32_t T, int32_t H, void *stream);
+
+/* ---- .binfer containers ---------------------------------------------------
+ * The reference's v1 container (docs/binfer_spec.md): header, section table,
+ * identity / architecture / tokenizer / policy sections, tensor directory,
+ * scale pool, 64-byte aligned payloads, trailing SHA-256.  An MoE layer l is
+ * the tensors model.layers.<l>.mlp.{gate.weight [E][H] bf16, gate.bias [E]
+ * fp32 (optional), shared_expert_gate.weight [1][H] bf16 (optional),
+ * experts.{gate,up}_proj.weight [E][I][H] and experts.down_proj.weight
+ * [E][H][I] (INT4, layout_id AINFER_BINFER_LAYOUT_EXPERTS),
+ * shared_expert.{gate,up,down}_proj.weight (INT4, row-major)} and
+ * model.layers.<l>.post_attention_layernorm.weight [H] bf16 (optional); the
+ * architecture section (JSON) holds hidden, n_experts, top_k, inter,
+ * shared_inter, layers, scale_fp16 and rms_eps.  ainfer_amd/binfer.py writes
+ * such files.
+ * Additions in fields v1 reserves: layout_id AINFER_BINFER_LAYOUT_EXPERTS (in
+ * the experimental range, which v1 reference loaders reject) = E stacked
+ * row-major [rows][K] matrices, the weight layout of this ABI; byte 180 of a
+ * directory entry = scale dtype of an INT4 tensor (0 bf16, the v1 default;
+ * 1 fp16). */
+#define AINFER_BINFER_LAYOUT_EXPERTS 32
+typedef struct ainfer_binfer ainfer_binfer;
+/* Open and validate the whole file before anything is allocated: magic,
+ * version, flags, section CRCs, directory size and CRC, unique names, no
+ * visual tensors, known dtypes and layout ids, quantization sizes, bounds,
+ * overlaps, payload CRCs and the trailing SHA-256 (the reference loader's
+ * rules, docs/binfer_spec.md:112-116, tools/binfer.py:383-499).  On failure
+ * returns AINFER_ERR_FORMAT (or AINFER_ERR_IO) and writes the first failure,
+ * with the tensor name and expected/actual values, into err. */
+int ainfer_binfer_open(const char *path, ainfer_binfer **file, char *err, size_t err_len);
+void ainfer_binfer_close(ainfer_binfer *file);
+/* Text of the last load failure on the file. */
+const char *ainfer_binfer_error(const ainfer_binfer *file);
+/* The MoE shape, layer count and RMSNorm eps of the architecture section. */
+int ainfer_binfer_moe_info(const ainfer_binfer *file, ainfer_moe_shape *shape,
+                           int32_t *n_layers, float *eps);
+/* Device bytes one layer's tensors take in an arena (each 256-byte aligned). */
+size_t ainfer_binfer_moe_layer_bytes(const ainfer_binfer *file, int32_t layer);
+/* Check layer `layer`'s tensors against the MoE shape (names, dtypes,
+ * layouts, shapes, scale dtype), copy them into the caller's device arena
+ * (256-byte aligned, ainfer_binfer_moe_layer_bytes) and fill the weight pointers
+ * (and *norm_w, NULL when the file has no norm weight).  Blocks until the
+ * copies are done (an init-time call). */
+int ainfer_binfer_load_moe_layer(const ainfer_binfer *file, int32_t layer, void *arena,
+                                 size_t arena_bytes, ainfer_moe_weights *weights,
+                                 const void **norm_w, void *stream);
 
 /* ---- W4A8: the reference's production GEMV numerics ---------------------
  * Activations quantised per group of 128 to int8, INT4 weights, int32 group

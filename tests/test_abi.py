@@ -18,7 +18,7 @@ def L():
 
 def declared_symbols():
     txt = (ROOT / "include" / "ainfer_moe.h").read_text()
-    return sorted(set(re.findall(r"\b(ainfer_moe_\w+)\s*\(", txt)))
+    return sorted(set(re.findall(r"\b(ainfer_(?:moe|binfer)_\w+)\s*\(", txt)))
 
 
 def test_exports_every_declared_symbol(L):
