@@ -14,6 +14,7 @@ ERR_FORMAT, ERR_IO = -9, -10
 BINFER_LAYOUT_EXPERTS = 32
 NOALLOC_SCRATCH_BYTES = 16 << 20
 SCALE_BF16, SCALE_FP16 = 0, 1
+PRECISION_W4A16, PRECISION_W4A8 = 0, 1
 NORM_PLAIN, NORM_ONE_PLUS = 0, 1
 ACT_F32, ACT_BF16 = 0, 1
 FILL_BYTES, FILL_BF16_NORMAL, FILL_FP16_ABSNORMAL, FILL_BF16_ABSNORMAL = 0, 1, 2, 3
@@ -40,7 +41,7 @@ STAGES = ("rmsnorm", "router", "topk", "dispatch", "gate_up", "down", "combine")
 class Shape(C.Structure):
     _fields_ = [("hidden", C.c_int32), ("n_experts", C.c_int32), ("top_k", C.c_int32),
                 ("inter", C.c_int32), ("shared_inter", C.c_int32), ("group", C.c_int32),
-                ("scale_dtype", C.c_int32), ("reserved", C.c_int32)]
+                ("scale_dtype", C.c_int32), ("precision", C.c_int32)]
 
 
 class Weights(C.Structure):

@@ -67,6 +67,7 @@ struct ProfCall {
 };
 
 struct Layout {
+  size_t w8_xq, w8_xs, w8_act, w8_acts, w8_aq, w8_as, w8_aqs, w8_ass, w8_o;
   size_t stack_flags, stack_cap, stack_end;
   size_t sync, sync_words, slots, tiles2, n_tiles2, logits, sg_logit, idx, w, sg, xperm, chunk_counts, rank, counts, offsets, perm, inv,
       ptok, tiles, n_tiles, ticket, act, act_s, o, h, wnorm, xsum, asum, asum_s, total;
@@ -135,6 +136,19 @@ Layout layout_of(const ainfer_moe_shape &s, int Tm) {
   L.xsum = take(T * (H / 128) * 4);
   L.asum = take(T * k * (s.inter / 32) * 4);
   L.asum_s = take(T * (size_t)(s.shared_inter > 0 ? s.shared_inter / 32 : 1) * 4);
+  L.w8_xq = L.w8_xs = L.w8_act = L.w8_acts = L.w8_aq = L.w8_as = L.w8_aqs = L.w8_ass = L.w8_o = 0;
+  if (s.precision == AINFER_PRECISION_W4A8) {
+    const size_t Is = s.shared_inter > 0 ? s.shared_inter : 128, I = s.inter;
+    L.w8_xq = take(T * H);
+    L.w8_xs = take(T * (H / 128) * 4);
+    L.w8_act = take(T * k * I * 4);
+    L.w8_acts = take(T * Is * 4);
+    L.w8_aq = take(T * k * I);
+    L.w8_as = take(T * k * (I / 128) * 4);
+    L.w8_aqs = take(T * Is);
+    L.w8_ass = take(T * (Is / 128) * 4);
+    L.w8_o = take(T * (k + 1) * H * 4);
+  }
   L.total = off;
   return L;
 }
@@ -254,9 +268,89 @@ ExpertArgs expert_args(const ainfer_moe_shape *s, const ainfer_moe_weights *w, c
 // the routing kernel applies the RMSNorm itself
 int down_kbw(const ainfer_moe_shape &s) { return down_kbw_of(s); }
 
+// The layer in W4A8 (AINFER_PRECISION_W4A8): the routing and dispatch of
+// the W4A16 path (16-token tiles), then x quantized, the grouped gate/up
+// GEMVs with SiLU, act quantized, the grouped down GEMVs and the fp32
+// combine (moe_w4a8.hip).
+int do_forward_w4a8(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const void *x,
+                    const void *resid, void *y, int T, void *ws, hipStream_t st, ProfCall *pc) {
+  const Layout L = layout_of(*s, T);
+  const int E = s->n_experts, k = s->top_k, H = s->hidden, I = s->inter, Is = s->shared_inter;
+  const int has_shared = Is > 0;
+  DispatchOut d = dispatch_out(s, L, ws, T);
+  d.mt = W8_MT;
+  if (T <= EXACT_ROUTER_MAX_T)
+    HIP_TRY(launch_router_exact(x, w->router_w, w->router_bias, w->shared_gate_w,
+                                at<float>(ws, L.logits), at<float>(ws, L.sg_logit),
+                                at<int32_t>(ws, L.idx), at<float>(ws, L.w), at<float>(ws, L.sg),
+                                at<uint16_t>(ws, L.xperm), T, H, E, k, has_shared, nullptr, st));
+  else
+    HIP_TRY(launch_router_fast(x, w->router_w, w->router_bias, w->shared_gate_w,
+                               at<float>(ws, L.logits), at<float>(ws, L.wnorm),
+                               at<int32_t>(ws, L.idx), at<float>(ws, L.w), at<float>(ws, L.sg),
+                               at<uint16_t>(ws, L.xperm), nullptr, T, H, E, k, has_shared,
+                               nullptr, st));
+  pc->end(2);
+  HIP_TRY(launch_dispatch(at<int32_t>(ws, L.idx), T, k, E, W8_MT, has_shared,
+                          at<int32_t>(ws, L.chunk_counts), at<int32_t>(ws, L.rank), d, st));
+  pc->end(3);
+  W4A8Args a;
+  memset(&a, 0, sizeof a);
+  a.xq = at<int8_t>(ws, L.w8_xq);
+  a.xs = at<float>(ws, L.w8_xs);
+  a.act = at<float>(ws, L.w8_act);
+  a.act_s = at<float>(ws, L.w8_acts);
+  a.aq = at<int8_t>(ws, L.w8_aq);
+  a.as = at<float>(ws, L.w8_as);
+  a.aq_s = at<int8_t>(ws, L.w8_aqs);
+  a.as_s = at<float>(ws, L.w8_ass);
+  a.o = at<float>(ws, L.w8_o);
+  a.ptok = d.ptok;
+  a.tiles = d.tiles;
+  a.n_tiles = d.n_tiles;
+  a.T = T;
+  a.k = k;
+  a.E = E;
+  a.H = H;
+  a.I = I;
+  a.Is = Is;
+  const int mtb = max_tiles_bound(*s, T, W8_MT);
+  HIP_TRY(launch_act_quant_i8(x, AINFER_ACT_BF16, T, H, at<int8_t>(ws, L.w8_xq),
+                              at<float>(ws, L.w8_xs), st));
+  a.w0 = w->w_gate;
+  a.w1 = w->w_up;
+  a.s0 = (const uint16_t *)w->s_gate;
+  a.s1 = (const uint16_t *)w->s_up;
+  a.ws0 = w->ws_gate;
+  a.ws1 = w->ws_up;
+  a.ss0 = (const uint16_t *)w->ss_gate;
+  a.ss1 = (const uint16_t *)w->ss_up;
+  HIP_TRY(launch_w4a8_expert(0, s->scale_dtype, a, mtb, st));
+  HIP_TRY(launch_act_quant_i8(a.act, AINFER_ACT_F32, T * k, I, at<int8_t>(ws, L.w8_aq),
+                              at<float>(ws, L.w8_as), st));
+  if (has_shared)
+    HIP_TRY(launch_act_quant_i8(a.act_s, AINFER_ACT_F32, T, Is, at<int8_t>(ws, L.w8_aqs),
+                                at<float>(ws, L.w8_ass), st));
+  pc->end(4);
+  a.w0 = w->w_down;
+  a.s0 = (const uint16_t *)w->s_down;
+  a.ws0 = w->ws_down;
+  a.ss0 = (const uint16_t *)w->ss_down;
+  a.w1 = a.ws1 = nullptr;
+  a.s1 = a.ss1 = nullptr;
+  HIP_TRY(launch_w4a8_expert(1, s->scale_dtype, a, mtb, st));
+  pc->end(5);
+  HIP_TRY(launch_combine_f32(a.o, d.inv, at<float>(ws, L.w), at<float>(ws, L.sg), has_shared,
+                             resid, y, T, k, H, at<int32_t>(ws, L.sync) + SY_ERR, st));
+  pc->end(6);
+  return AINFER_OK;
+}
+
 int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const void *x,
                const void *resid, void *y, int T, void *ws, hipStream_t st,
                ProfCall *pc, const NormIn *norm = nullptr) {
+  if (s->precision == AINFER_PRECISION_W4A8)
+    return do_forward_w4a8(s, w, x, resid, y, T, ws, st, pc);
   const Layout L = layout_of(*s, T);
   const int E = s->n_experts, k = s->top_k, H = s->hidden;
   const int has_shared = s->shared_inter > 0;
@@ -468,7 +562,8 @@ int do_block(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const void 
   ProfCall pc(st);
   pc.start();
   DecodeGeom dg;
-  if (T <= DECODE_NORM_MAX_T && decode_geometry(*s, &dg)) {
+  if (T <= DECODE_NORM_MAX_T && s->precision == AINFER_PRECISION_W4A16 &&
+      decode_geometry(*s, &dg)) {
     // decode at up to 4 tokens: the routing kernel normalizes x itself (one
     // launch fewer per block: c4 T=1 about 2470 -> 2235 us per 60-block
     // step); the values are those k_rmsnorm writes
@@ -569,7 +664,9 @@ const char *ainfer_moe_strerror(int status) {
 
 int ainfer_moe_validate(const ainfer_moe_shape *s) {
   if (!s) return AINFER_ERR_NULL;
-  if (s->group != 128 || s->reserved != 0) return AINFER_ERR_SHAPE;
+  if (s->group != 128) return AINFER_ERR_SHAPE;
+  if (s->precision != AINFER_PRECISION_W4A16 && s->precision != AINFER_PRECISION_W4A8)
+    return AINFER_ERR_SHAPE;
   // K of every expert product <= 4096 (the prefill GEMM's tables hold 32 groups)
   if (s->hidden < 128 || s->hidden % 128 || s->hidden > 4096) return AINFER_ERR_SHAPE;
   if (s->inter < 128 || s->inter % 128 || s->inter > 4096) return AINFER_ERR_SHAPE;

@@ -184,6 +184,28 @@ struct DecodeGeom {
   size_t lds;              // dynamic LDS bytes
 };
 // W4A8 GEMV numerics (moe_w4a8.hip)
+// The MoE layer in W4A8: the grouped expert GEMVs over dispatch tiles of at
+// most W8_MT tokens and the fp32 combine.
+constexpr int W8_MT = 16;
+struct W4A8Args {
+  const uint8_t *w0, *w1, *ws0, *ws1;     // MODE 0: gate, up; MODE 1: down (w0/ws0)
+  const uint16_t *s0, *s1, *ss0, *ss1;
+  const int8_t *xq;                      // [T][H] x quantized
+  const float *xs;                       // [T][H/128]
+  float *act, *act_s;                    // MODE 0 out: [T*k][I], [T][Is]
+  const int8_t *aq, *aq_s;               // MODE 1 in: act quantized
+  const float *as, *as_s;                // their group scales
+  float *o;                              // MODE 1 out: [T*k + T][H]
+  const int32_t *ptok;
+  const int4 *tiles;
+  const int32_t *n_tiles;
+  int T, k, E, H, I, Is;
+};
+hipError_t launch_w4a8_expert(int mode, int scale_dtype, const W4A8Args &a, int max_tiles,
+                              hipStream_t s);
+hipError_t launch_combine_f32(const float *o, const int32_t *inv, const float *w,
+                              const float *sg, int has_shared, const void *resid, void *y, int T,
+                              int k, int H, const int32_t *err, hipStream_t s);
 hipError_t launch_act_quant_i8(const void *x, int x_dtype, int T, int K, int8_t *q, float *sq,
                                hipStream_t s);
 hipError_t launch_int4_gemv_i8(const uint8_t *P, const void *S, int scale_dtype, const int8_t *xq,

@@ -642,6 +642,7 @@ std::mutex g_stack_mu;
 }  // namespace
 
 bool stack_geometry(const ainfer_moe_shape &s, int T, StackGeom *g) {
+  if (s.precision != AINFER_PRECISION_W4A16) return false;  // the W4A16 items only
   DecodeGeom dg;
   if (!decode_geometry(s, &dg)) return false;
   int kbw, wk, wr;

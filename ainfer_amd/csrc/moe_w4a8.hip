@@ -81,28 +81,29 @@ __device__ __forceinline__ i32x4 mfma_i8(i32x4 a, i32x4 b, i32x4 c) {
 constexpr int GV_CHUNK = GV_WAVES * GV_GPW;  // groups whose terms one LDS pass holds
 static_assert(GV_WAVES >= 4, "the ordered sum uses one thread per (row, token) of a 16 x 16 tile");
 
-// grid (ceil(M / 16), ceil(T / 16)), GV_WAVES waves: the block owns rows
-// [16 * bx, +16) and tokens [16 * by, +16).  Wave w computes the terms
+// One 16-row x 16-token block of the INT4 x int8 GEMV, GV_WAVES waves: rows
+// [m0, +16) of P / S (M rows, K columns) against 16 activation rows, lane
+// column c reading row xrow of xq / sq.  Wave w computes the terms
 // float(gs) * s * sq of groups w, w + GV_WAVES, ... of each chunk into LDS;
-// then 256 threads, one per (row, token), add them in group order.  y is
-// [T][M] fp32.
+// then 256 threads, one per (row, token), add them in group order.  Returns
+// the sum of thread (row 4 * (lp / 16) + i, token lp % 16), lp = tid / 4,
+// i = tid % 4.
 // STG: the block's weight scales [16][G] and activation scales [16][G] are
-// staged in LDS once (per-lane 2-byte gathers in every pass cost 3 of 18 us
-// at 17408 x 5120); else they are gathered per group.
+// staged in LDS (gv_lds) once (per-lane 2-byte gathers in every pass cost 3
+// of 18 us at 17408 x 5120); else they are gathered per group.
 template <int SD, bool STG>
-__global__ __launch_bounds__(GV_WAVES * 64) void k_int4_gemv_i8(
-    const uint8_t *__restrict__ P, const uint16_t *__restrict__ S, const int8_t *__restrict__ xq,
-    const float *__restrict__ sq, int M, int K, int T, float *__restrict__ y) {
-  __shared__ float term[GV_CHUNK][256];
-  extern __shared__ __attribute__((aligned(16))) uint8_t gv_lds[];  // STG: [16][G] f32, [16][G] u16
+__device__ __forceinline__ float gemv_i8_block(const uint8_t *__restrict__ P,
+                                               const uint16_t *__restrict__ S, int m0, int M,
+                                               int K, const int8_t *__restrict__ xq,
+                                               const float *__restrict__ sq, int xrow,
+                                               float (*term)[256], uint8_t *gv_lds,
+                                               const int *xrows_lds) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int m0 = blockIdx.x * 16, t0 = blockIdx.y * 16;
   const int G = K / 128, qd = lane >> 4, c = lane & 15;
-  // A operand: row m0 + c; B operand and D column: token t0 + c
+  // A operand: row m0 + c; B operand and D column: token column c
   const uint8_t *wp = P + (size_t)min(m0 + c, M - 1) * (K / 2) + qd * 16;
-  const int tb = min(t0 + c, T - 1);
-  const int8_t *xp = xq + (size_t)tb * K + qd * 32;
-  const float *sqp = sq + (size_t)tb * G;
+  const int8_t *xp = xq + (size_t)xrow * K + qd * 32;
+  const float *sqp = sq + (size_t)xrow * G;
   // D rows of this lane: m0 + 4 * qd + i
   const uint16_t *sp[4];
 #pragma unroll
@@ -113,7 +114,7 @@ __global__ __launch_bounds__(GV_WAVES * 64) void k_int4_gemv_i8(
     for (int i = threadIdx.x; i < 16 * G; i += GV_WAVES * 64) {
       const int r = i / G, g = i - r * G;
       sc_l[i] = S[(size_t)min(m0 + r, M - 1) * G + g];
-      sq_l[i] = sq[(size_t)min(t0 + r, T - 1) * G + g];
+      sq_l[i] = sq[(size_t)xrows_lds[r] * G + g];
     }
     __syncthreads();
   }
@@ -190,11 +191,105 @@ __global__ __launch_bounds__(GV_WAVES * 64) void k_int4_gemv_i8(
     }
     __syncthreads();
   }
+  return acc;
+}
+
+// grid (ceil(M / 16), ceil(T / 16)): the block owns rows [16 * bx, +16) and
+// tokens [16 * by, +16).  y is [T][M] fp32.
+template <int SD, bool STG>
+__global__ __launch_bounds__(GV_WAVES * 64) void k_int4_gemv_i8(
+    const uint8_t *__restrict__ P, const uint16_t *__restrict__ S, const int8_t *__restrict__ xq,
+    const float *__restrict__ sq, int M, int K, int T, float *__restrict__ y) {
+  __shared__ float term[GV_CHUNK][256];
+  __shared__ int xrows[16];
+  extern __shared__ __attribute__((aligned(16))) uint8_t gv_lds[];  // STG: [16][G] f32, [16][G] u16
+  const int m0 = blockIdx.x * 16, t0 = blockIdx.y * 16;
+  if (threadIdx.x < 16) xrows[threadIdx.x] = min(t0 + (int)threadIdx.x, T - 1);
+  __syncthreads();
+  const int c = threadIdx.x & 15;
+  const float acc = gemv_i8_block<SD, STG>(P, S, m0, M, K, xq, sq, min(t0 + c, T - 1), term,
+                                           gv_lds, xrows);
   // element e = lane' * 4 + i of the producing lane': row 4 * (lane' / 16) + i,
   // token lane' % 16
   const int lp = threadIdx.x >> 2, i = threadIdx.x & 3;
   const int m = m0 + 4 * (lp >> 4) + i, t = t0 + (lp & 15);
   if (m < M && t < T) y[(size_t)t * M + m] = acc;
+}
+
+// ---- the MoE layer in W4A8 (AINFER_PRECISION_W4A8) --------------------------
+// The decoder MLP of tools/decode/decode_l0.cpp:663-674 per (token, expert):
+// xq -> Int4Gemv gate, Int4Gemv up -> SiluMul -> quantize -> Int4Gemv down,
+// here grouped by expert: one block = 16 weight rows x one dispatch tile of
+// at most 16 tokens of one expert (the shared expert's tiles carry expert id
+// E), the GEMV block arithmetic above.
+//   MODE 0: act[pos][n] = silu(gate . x) * (up . x), fp32, for the tile's
+//           tokens (x quantized per 128-group, rows xq[token]);
+//   MODE 1: o[pos][h] = down . act, fp32, act quantized per 128-group
+//           (rows actq[pos]; the shared expert's outputs at rows T * k + t).
+template <int SD, int MODE>
+__global__ __launch_bounds__(GV_WAVES * 64) void k_w4a8_expert(W4A8Args a) {
+  __shared__ float term[GV_CHUNK][256];
+  __shared__ int xrows[16];
+  extern __shared__ __attribute__((aligned(16))) uint8_t gv_lds[];
+  if ((int)blockIdx.y >= *a.n_tiles) return;
+  const int4 t = a.tiles[blockIdx.y];
+  const int e = t.x, pos0 = t.y, mcnt = t.z;
+  const bool shared = e == a.E;
+  const int N = MODE == 0 ? (shared ? a.Is : a.I) : a.H;
+  const int K = MODE == 0 ? a.H : (shared ? a.Is : a.I);
+  const int m0 = blockIdx.x * 16;
+  if (m0 >= N) return;
+  // the tile's activation rows (columns past mcnt repeat the last one)
+  if (threadIdx.x < 16) {
+    const int r = min((int)threadIdx.x, mcnt - 1);
+    xrows[threadIdx.x] = MODE == 0 ? (shared ? pos0 + r : a.ptok[pos0 + r]) : pos0 + r;
+  }
+  __syncthreads();
+  const int c = threadIdx.x & 15;
+  const int xr = xrows[c];
+  const size_t rowb = (size_t)K / 2, G = K / 128;
+  float v;
+  if constexpr (MODE == 0) {
+    const uint8_t *wg = shared ? a.ws0 : a.w0 + (size_t)e * N * rowb;
+    const uint8_t *wu = shared ? a.ws1 : a.w1 + (size_t)e * N * rowb;
+    const uint16_t *sgp = shared ? a.ss0 : a.s0 + (size_t)e * N * G;
+    const uint16_t *sup = shared ? a.ss1 : a.s1 + (size_t)e * N * G;
+    const float g = gemv_i8_block<SD, true>(wg, sgp, m0, N, K, a.xq, a.xs, xr, term, gv_lds, xrows);
+    const float u = gemv_i8_block<SD, true>(wu, sup, m0, N, K, a.xq, a.xs, xr, term, gv_lds, xrows);
+    v = g / (1.0f + expf(-g)) * u;  // SiluMul, tools/cmdlist/kernels.cpp:29-37
+  } else {
+    const uint8_t *wd = shared ? a.ws0 : a.w0 + (size_t)e * N * rowb;
+    const uint16_t *sdp = shared ? a.ss0 : a.s0 + (size_t)e * N * G;
+    v = gemv_i8_block<SD, true>(wd, sdp, m0, N, K, shared ? a.aq_s : a.aq,
+                                shared ? a.as_s : a.as, xr, term, gv_lds, xrows);
+  }
+  const int lp = threadIdx.x >> 2, i = threadIdx.x & 3;
+  const int m = m0 + 4 * (lp >> 4) + i, tc = lp & 15;
+  if (m >= N || tc >= mcnt) return;
+  if constexpr (MODE == 0)
+    (shared ? a.act_s : a.act)[(size_t)(pos0 + tc) * N + m] = v;
+  else
+    a.o[(size_t)((shared ? a.T * a.k : 0) + pos0 + tc) * N + m] = v;
+}
+
+// y[t][h] = bf16(sum_j w_j o[pos(t, j)][h] + g_s o[T * k + t][h] (+ resid)),
+// fp32 fma in slot order (k_combine's order on the fp32 expert outputs).
+__global__ __launch_bounds__(256) void k_combine_f32(const float *__restrict__ o,
+                                                     const int32_t *__restrict__ inv,
+                                                     const float *__restrict__ w,
+                                                     const float *__restrict__ sg,
+                                                     int has_shared,
+                                                     const uint16_t *__restrict__ resid,
+                                                     uint16_t *__restrict__ y, int T, int k, int H,
+                                                     const int32_t *__restrict__ err) {
+  const int t = blockIdx.y, h = blockIdx.x * 256 + threadIdx.x;
+  if (h >= H) return;
+  float acc = 0.0f;
+  for (int j = 0; j < k; ++j)
+    acc = __builtin_fmaf(w[(size_t)t * k + j], o[(size_t)inv[(size_t)t * k + j] * H + h], acc);
+  if (has_shared) acc = __builtin_fmaf(sg[t], o[((size_t)T * k + t) * H + h], acc);
+  if (resid) acc += bf16_to_f32(resid[(size_t)t * H + h]);
+  y[(size_t)t * H + h] = (err && *err) ? (uint16_t)0x7FC0u : f32_to_bf16(acc);
 }
 
 }  // namespace
@@ -207,6 +302,36 @@ hipError_t launch_act_quant_i8(const void *x, int x_dtype, int T, int K, int8_t 
     k_act_quant_i8<float><<<grid, 256, 0, s>>>((const float *)x, T, K, q, sq);
   else
     k_act_quant_i8<uint16_t><<<grid, 256, 0, s>>>((const uint16_t *)x, T, K, q, sq);
+  return hipGetLastError();
+}
+
+hipError_t launch_w4a8_expert(int mode, int scale_dtype, const W4A8Args &a, int max_tiles,
+                              hipStream_t s) {
+  if (max_tiles <= 0) return hipSuccess;
+  const int N = mode == 0 ? (a.I > a.Is ? a.I : a.Is) : a.H;
+  const int K = mode == 0 ? a.H : (a.I > a.Is ? a.I : a.Is);
+  const dim3 grid((N + 15) / 16, max_tiles);
+  const size_t stg = (size_t)16 * (K / 128) * 6;  // staged scales
+  auto go = [&](auto sd_c) {
+    constexpr int SDc = decltype(sd_c)::value;
+    if (mode == 0)
+      k_w4a8_expert<SDc, 0><<<grid, GV_WAVES * 64, stg, s>>>(a);
+    else
+      k_w4a8_expert<SDc, 1><<<grid, GV_WAVES * 64, stg, s>>>(a);
+  };
+  if (scale_dtype == AINFER_SCALE_FP16)
+    go(std::integral_constant<int, AINFER_SCALE_FP16>());
+  else
+    go(std::integral_constant<int, AINFER_SCALE_BF16>());
+  return hipGetLastError();
+}
+
+hipError_t launch_combine_f32(const float *o, const int32_t *inv, const float *w,
+                              const float *sg, int has_shared, const void *resid, void *y, int T,
+                              int k, int H, const int32_t *err, hipStream_t s) {
+  if (T == 0) return hipSuccess;
+  k_combine_f32<<<dim3((H + 255) / 256, T), 256, 0, s>>>(
+      o, inv, w, sg, has_shared, (const uint16_t *)resid, (uint16_t *)y, T, k, H, err);
   return hipGetLastError();
 }
 

@@ -36,10 +36,11 @@ class MoeLayer:
     """One INT4 MoE layer resident in HBM (synthetic seeded weights)."""
 
     def __init__(self, cfg: MoeConfig, layer: int = 0, device="cuda",
-                 scale_dtype: int = L.SCALE_FP16, stream=None):
+                 scale_dtype: int = L.SCALE_FP16, stream=None,
+                 precision: int = L.PRECISION_W4A16):
         self.cfg, self.layer, self.device = cfg, layer, device
         H, E, I, Is = cfg.hidden, cfg.n_experts, cfg.inter, cfg.shared_inter
-        self.shape = L.Shape(H, E, cfg.top_k, I, Is, 128, scale_dtype, 0)
+        self.shape = L.Shape(H, E, cfg.top_k, I, Is, 128, scale_dtype, precision)
         L.check(L.lib().ainfer_moe_validate(C.byref(self.shape)))
         ls = layer_seed(cfg.seed, layer)
         sdt = torch.float16 if scale_dtype == L.SCALE_FP16 else torch.bfloat16
@@ -163,6 +164,16 @@ def load_binfer_layer(bf, layer, device="cuda"):
         # a view of the arena at the norm weight's offset
         norm = arena[nw.value - arena.data_ptr():][:shape.hidden * 2].view(torch.bfloat16)
     return ly, norm
+
+
+def with_precision(layer, precision):
+    """The same resident layer (shared weights) run in another precision."""
+    twin = MoeLayer.__new__(MoeLayer)
+    twin.__dict__.update(layer.__dict__)
+    twin.shape = L.Shape.from_buffer_copy(layer.shape)
+    twin.shape.precision = precision
+    L.check(L.lib().ainfer_moe_validate(C.byref(twin.shape)))
+    return twin
 
 
 class MoeStack:

@@ -73,6 +73,19 @@ enum {
 
 enum { AINFER_SCALE_BF16 = 0, AINFER_SCALE_FP16 = 1 };
 
+/* Expert arithmetic of the layer entries.
+ * W4A16: bf16 activations against dequantised INT4 weights, fp32 sums
+ *   (bf16 MFMA), act and expert outputs rounded to bf16.
+ * W4A8: the reference's production decode numerics (the MLP sequence of
+ *   tools/decode/decode_l0.cpp:663-674): x quantised per group of 128 to int8
+ *   (ScalesMax + Quantize, tools/cmdlist/kernels.cpp:551-579), gate and up
+ *   as Int4Gemv (kernels.cpp:148-201: exact int32 group dots, fp32 terms
+ *   float(gs) * s_w * s_x added in group order without contraction), act =
+ *   SiluMul in fp32, quantised again, down as Int4Gemv, and the combine in
+ *   fp32 (fma in slot order) before the bf16 output.  Each GEMV gives the
+ *   reference formula's bits on the same inputs (ainfer_moe_int4_gemv_i8). */
+enum { AINFER_PRECISION_W4A16 = 0, AINFER_PRECISION_W4A8 = 1 };
+
 /* RMSNorm weight forms: reference RMSNormW uses y = x*inv*(1+w)
  * (tools/cmdlist/kernels.cpp:73-116); the operator fixture
  * (reference/operators_t14.npz rmsnorm_*) uses y = x*inv*w. */
@@ -96,7 +109,7 @@ typedef struct ainfer_moe_shape {
   int32_t shared_inter; /* I of the shared expert, multiple of 128; 0 = none */
   int32_t group;        /* quantisation group along K; must be 128          */
   int32_t scale_dtype;  /* AINFER_SCALE_FP16 or AINFER_SCALE_BF16           */
-  int32_t reserved;     /* must be 0                                        */
+  int32_t precision;    /* AINFER_PRECISION_W4A16 (0) or _W4A8              */
 } ainfer_moe_shape;
 
 /* Device pointers.  Weight and router tensors must be 16-byte aligned, scale

@@ -581,6 +581,80 @@ int mo_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *wts,
   return 0;
 }
 
+/* The layer in W4A8 (AINFER_PRECISION_W4A8): per (token, expert) the MLP
+ * sequence of tools/decode/decode_l0.cpp:663-674 -- xq (ScalesMax +
+ * Quantize, mo_act_quant_i8), Int4Gemv gate and up (mo_int4_gemv_i8),
+ * SiluMul in fp32 (kernels.cpp:29-37: g / (1 + exp(-g)) * u), quantize,
+ * Int4Gemv down -- then the combine in fp32: fmaf(w_j, o_j, acc) in slot
+ * order, fmaf(g_s, o_shared, acc).  Routing as mo_route.  y_f32 [T][H]. */
+typedef struct {
+  const ainfer_moe_shape *s;
+  const ainfer_moe_weights *w;
+  const uint16_t *x;
+  const int32_t *idx;
+  const float *tw, *sg;
+  float *y;
+} w8_ctx;
+
+static void w8_expert(const uint8_t *wg, const void *sg_, const uint8_t *wu, const void *su,
+                      const uint8_t *wd, const void *sd, int dt, int H, int I, const int8_t *xq,
+                      const float *xs, float *g, float *u, int8_t *aq, float *as, float *o) {
+  mo_int4_gemv_i8(wg, sg_, dt, xq, xs, I, H, 1, g);
+  mo_int4_gemv_i8(wu, su, dt, xq, xs, I, H, 1, u);
+  for (int n = 0; n < I; ++n) g[n] = g[n] / (1.0f + expf(-g[n])) * u[n];
+  mo_act_quant_i8(g, NULL, 1, I, aq, as);
+  mo_int4_gemv_i8(wd, sd, dt, aq, as, H, I, 1, o);
+}
+
+static void w8_range(void *p, long lo, long hi) {
+  w8_ctx *c = (w8_ctx *)p;
+  const ainfer_moe_shape *s = c->s;
+  const ainfer_moe_weights *w = c->w;
+  int H = s->hidden, I = s->inter, Is = s->shared_inter, k = s->top_k, dt = s->scale_dtype;
+  int Im = I > Is ? I : Is;
+  int8_t *xq = (int8_t *)malloc((size_t)H);
+  float *xs = (float *)malloc(sizeof(float) * (H / 128));
+  float *g = (float *)malloc(sizeof(float) * Im), *u = (float *)malloc(sizeof(float) * Im);
+  int8_t *aq = (int8_t *)malloc((size_t)Im);
+  float *as = (float *)malloc(sizeof(float) * (Im / 128));
+  float *o = (float *)malloc(sizeof(float) * (size_t)(k + 1) * H);
+  for (long t = lo; t < hi; ++t) {
+    mo_act_quant_i8(NULL, c->x + (size_t)t * H, 1, H, xq, xs);
+    for (int j = 0; j < k; ++j) {
+      int e = c->idx[(size_t)t * k + j];
+      size_t pg = (size_t)e * I * (H / 2), sgo = (size_t)e * I * (H / 128);
+      size_t pd = (size_t)e * H * (I / 2), sdo = (size_t)e * H * (I / 128);
+      w8_expert(w->w_gate + pg, (const uint16_t *)w->s_gate + sgo, w->w_up + pg,
+                (const uint16_t *)w->s_up + sgo, w->w_down + pd, (const uint16_t *)w->s_down + sdo,
+                dt, H, I, xq, xs, g, u, aq, as, o + (size_t)j * H);
+    }
+    if (Is > 0)
+      w8_expert(w->ws_gate, w->ss_gate, w->ws_up, w->ss_up, w->ws_down, w->ss_down, dt, H, Is,
+                xq, xs, g, u, aq, as, o + (size_t)k * H);
+    for (int h = 0; h < H; ++h) {
+      float acc = 0.0f;
+      for (int j = 0; j < k; ++j) acc = fmaf(c->tw[(size_t)t * k + j], o[(size_t)j * H + h], acc);
+      if (Is > 0) acc = fmaf(c->sg[t], o[(size_t)k * H + h], acc);
+      c->y[(size_t)t * H + h] = acc;
+    }
+  }
+  free(xq); free(xs); free(g); free(u); free(aq); free(as); free(o);
+}
+
+int mo_forward_w4a8(const ainfer_moe_shape *s, const ainfer_moe_weights *wts, const uint16_t *x,
+                    int T, float *y_f32, int nthreads) {
+  int k = s->top_k;
+  if (T <= 0) return 0;
+  int32_t *idx = (int32_t *)malloc(sizeof(int32_t) * (size_t)T * k);
+  float *tw = (float *)malloc(sizeof(float) * (size_t)T * k);
+  float *sg = (float *)malloc(sizeof(float) * (size_t)T);
+  mo_route(s, wts, x, T, idx, tw, sg, NULL, nthreads);
+  w8_ctx c = {s, wts, x, idx, tw, sg, y_f32};
+  parallel_for(T, nthreads, w8_range, &c);
+  free(idx); free(tw); free(sg);
+  return 0;
+}
+
 int mo_block_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *wts,
                      const uint16_t *norm_w, int norm_mode, float eps,
                      const uint16_t *resid_in, uint16_t *resid_out, int T,

@@ -109,6 +109,11 @@ int mo_forward_dense(const ainfer_moe_shape *s, const ainfer_moe_weights *wts,
                      const uint16_t *x, int T, const int32_t *idx,
                      const float *w, const float *sg, double *y);
 
+/* The layer in W4A8 (per-group int8 activations, Int4Gemv products, fp32
+ * SiluMul and combine): y_f32 [T][H]. */
+int mo_forward_w4a8(const ainfer_moe_shape *s, const ainfer_moe_weights *wts, const uint16_t *x,
+                    int T, float *y_f32, int nthreads);
+
 #ifdef __cplusplus
 }
 #endif

@@ -22,7 +22,7 @@ NORM_PLAIN, NORM_ONE_PLUS = 0, 1
 class Shape(C.Structure):
     _fields_ = [("hidden", C.c_int32), ("n_experts", C.c_int32), ("top_k", C.c_int32),
                 ("inter", C.c_int32), ("shared_inter", C.c_int32), ("group", C.c_int32),
-                ("scale_dtype", C.c_int32), ("reserved", C.c_int32)]
+                ("scale_dtype", C.c_int32), ("precision", C.c_int32)]
 
 
 class Weights(C.Structure):
@@ -74,6 +74,7 @@ def lib():
         L.mo_forward.argtypes = [P, P, P, I, P, P, I]
         L.mo_block_forward.argtypes = [P, P, P, I, F, P, P, I, I]
         L.mo_forward_dense.argtypes = [P, P, P, I, P, P, P, P]
+        L.mo_forward_w4a8.argtypes = [P, P, P, I, P, I]
         L.mo_act_quant_i8.argtypes = [P, P, I, I, P, P]
         L.mo_int4_gemv_i8.argtypes = [P, P, I, P, P, I, I, I, P]
         L.mo_ref_gemv_inputs.argtypes = [I, I, I, P, P, P]
@@ -165,6 +166,13 @@ class HostLayer:
         y = np.empty((T, self.H), np.float32)
         lib().mo_forward(C.byref(self.shape), C.byref(self.weights), ptr(x), T, ptr(y), None,
                          threads or nthreads())
+        return y
+
+    def forward_w4a8(self, x: np.ndarray, T: int, threads=None):
+        """The layer in W4A8 numerics (fp32 output)."""
+        y = np.empty((T, self.H), np.float32)
+        lib().mo_forward_w4a8(C.byref(self.shape), C.byref(self.weights), ptr(x), T, ptr(y),
+                              threads or nthreads())
         return y
 
     def block_forward(self, resid: np.ndarray, T: int, norm_w=None, mode=NORM_PLAIN, eps=1e-6,

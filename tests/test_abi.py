@@ -31,7 +31,7 @@ def test_exports_every_declared_symbol(L):
 
 def shape(L, **kw):
     d = dict(hidden=2048, n_experts=512, top_k=10, inter=512, shared_inter=512, group=128,
-             scale_dtype=L.SCALE_FP16, reserved=0)
+             scale_dtype=L.SCALE_FP16, precision=0)
     d.update(kw)
     return L.Shape(**d)
 
@@ -41,7 +41,7 @@ def test_validate(L):
     assert lib.ainfer_moe_validate(C.byref(shape(L))) == L.OK
     for bad in (dict(group=64), dict(hidden=1000), dict(top_k=0), dict(top_k=600),
                 dict(n_experts=2048), dict(inter=100), dict(shared_inter=-128),
-                dict(scale_dtype=7), dict(reserved=1), dict(hidden=16384)):
+                dict(scale_dtype=7), dict(precision=2), dict(precision=-1), dict(hidden=16384)):
         assert lib.ainfer_moe_validate(C.byref(shape(L, **bad))) == L.ERR_SHAPE, bad
     assert lib.ainfer_moe_validate(None) == L.ERR_NULL
 
