@@ -14,11 +14,12 @@
 // v_mfma_f32_16x16x32_bf16.  Token subtiles past the tile's count skip
 // their MFMAs and A reads.
 //
-// Data movement: a 2-stage LDS ring per block, one barrier per group.  Each
+// Data movement: a 3-stage LDS ring per block (2 stages where K > 2048
+// leaves no room), one barrier per group.  Each
 // stage holds one group of the token rows (128 x 256 B, already in MFMA
 // order) and of the raw INT4 weight rows (64 B each).  Both arrive by
 // global->LDS DMA (global_load_lds_dwordx4: lane i of a wave lands at
-// M0 + 16 i), one group ahead of the math, with no staging registers.  The
+// M0 + 16 i), two groups ahead of the math, with no staging registers.  The
 // DMA is issued from inline asm and its completion tracked with explicit
 // vmcnt waits, so the compiler's conservative waits do not serialise the
 // ring.  Rows are swizzled in 16-byte chunks (A: chunk c of row r at
@@ -55,6 +56,19 @@ __device__ __forceinline__ void dma16(const void *g, uint32_t lds_addr) {
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
                :
                : "v"(g), "s"(lds_addr)
+               : "memory", "m0");
+}
+
+// The same with a scalar base address and a 32-bit per-lane offset.  The
+// base must be wave-uniform; it is moved to SGPRs explicitly, since the
+// compiler cannot always prove the uniformity of values loaded per item.
+__device__ __forceinline__ void dma16s(uint32_t off, const void *base, uint32_t lds_addr) {
+  const uint64_t b = (uint64_t)(uintptr_t)base;
+  const uint64_t sb = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b) |
+                      ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) << 32);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(off), "s"(sb), "s"(lds_addr)
                : "memory", "m0");
 }
 
@@ -95,22 +109,41 @@ __device__ __forceinline__ u32x4 nib_slice3(u32x4 b, int j, uint32_t magic) {
                ((b[2] >> (4 * j)) & mask) | magic, ((b[3] >> (4 * j)) & mask) | magic};
 }
 
-__device__ __forceinline__ float silu_mul(float g, float u) {
-  return g / (1.0f + expf(-g)) * u;
+// silu(g) * u for the prefill epilogue: the hardware exp2 and reciprocal
+// (about 1 ulp each) instead of expf and an IEEE division, which made the
+// epilogue several times longer than a group of the main loop.  The result is
+// rounded to bf16 (2^-9 relative) right after.  Large |g| behaves: exp2 -> inf
+// gives rcp 0 and g * 0; exp2 -> 0 gives g.
+__device__ __forceinline__ float silu_mul_fast(float g, float u) {
+  const float e = __builtin_amdgcn_exp2f(g * -1.44269504088896341f);
+  return g * __builtin_amdgcn_rcpf(1.0f + e) * u;
 }
 
+// round to nearest even bf16 (v_cvt_pk_bf16_f32)
+__device__ __forceinline__ uint32_t bf16_bits(float f) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f);
+}
+
+// sum over the 16 lanes of a DPP row (lane & 15), in every lane of the row
+__device__ __forceinline__ float row16_sum(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));   // quad [1,0,3,2]
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));   // quad [2,3,0,1]
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));  // half mirror
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));  // row mirror
+  return v;
+}
+
+// One item: expert tile lb / n_nblk, column block lb % n_nblk.
 template <int SD, int MODE, int WN, int STAGES_>
-__global__ __launch_bounds__(128 * WN) void k_expert_gemm(GemmArgs a) {
+__device__ __forceinline__ void gemm_item(const GemmArgs &a, const int lb) {
   using Gm = Geo<WN, STAGES_>;
   constexpr int BN = Gm::BN, STAGES = Gm::STAGES, A_STAGE = Gm::A_STAGE, STAGE = Gm::STAGE;
   constexpr int NW = Gm::NW, THREADS = Gm::THREADS, COLS = Gm::COLS;
   // dynamic LDS: STAGES x (A | B) ring, scales[G][BN] fp16, xs[G][BM] fp32
-  // (group-major: a lane's 4 rows are one 16-byte read), red_sum[2][BM] fp32
+  // (group-major: a lane's 4 rows are one 16-byte read); the epilogue's
+  // staging and row sums reuse the idle ring
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int n_nb = a.n_nblk;
-  const int n_items = *a.n_tiles * n_nb;  // the grid is an upper bound
-  if ((int)blockIdx.x >= n_items) return;
-  const int lb = xcd_remap(blockIdx.x, n_items);
   const int tile_id = lb / n_nb, nb = lb % n_nb;
   const int4 t = a.tiles[tile_id];
   const int e = t.x, pos0 = t.y, mcnt = t.z;
@@ -124,9 +157,8 @@ __global__ __launch_bounds__(128 * WN) void k_expert_gemm(GemmArgs a) {
   const uint32_t lds0 = (uint32_t)(uintptr_t)lds;
   uint16_t *sc_lds = (uint16_t *)(lds + STAGES * STAGE);
   float *xs_lds = (float *)(lds + STAGES * STAGE + ((BN * G * 2 + 15) & ~15));
-  float *red_sum = xs_lds + BM * G;
 
-  const int tid = threadIdx.x;
+  const int tid = tid_opaque();  // per item: nothing lane-dependent is hoisted across items
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   // 2 token waves x WN row waves; wave w runs on SIMD w % 4, so each SIMD
@@ -136,53 +168,60 @@ __global__ __launch_bounds__(128 * WN) void k_expert_gemm(GemmArgs a) {
   const int m16 = lane & 15, q = lane >> 4;
 
   // ---- per-thread DMA sources: A_DMA A slots and B_DMA B slots per stage ---
-  // slot s = (i*NW + wave)*64 + lane, 16 bytes each
-  const uint8_t *asrc[Gm::A_DMA];
+  // slot s = (i*NW + wave)*64 + lane, 16 bytes each.  The block-uniform part
+  // of each address is a scalar base (advanced per group); a lane keeps one
+  // 32-bit offset per slot.
+  const uint8_t *abase;
+  uint32_t aoff[Gm::A_DMA];
+  if (MODE == 0)
+    abase = (const uint8_t *)(a.a_routed + (shared ? (size_t)pos0 * a.H : 0));
+  else
+    abase = (const uint8_t *)((shared ? a.a_shared : a.a_routed) + (size_t)pos0 * K);
 #pragma unroll
   for (int i = 0; i < Gm::A_DMA; ++i) {
     const int s = (i * NW + wave) * 64 + lane;
     const int r = s >> 4, c = (s & 15) ^ aswz(r);
     const int rr = min(r, mcnt - 1);
-    const uint16_t *row;
-    if (MODE == 0) {
-      const int tok = shared ? pos0 + rr : a.ptok[pos0 + rr];
-      row = a.a_routed + (size_t)tok * a.H;
-    } else {
-      row = (shared ? a.a_shared : a.a_routed) + (size_t)(pos0 + rr) * K;
-    }
-    asrc[i] = (const uint8_t *)row + c * 16;
+    // MODE 0 routed: a gathered token row, tok < T <= 4096 and H <= 4096
+    const uint32_t row = MODE == 0 && !shared ? (uint32_t)a.ptok[pos0 + rr] : (uint32_t)rr;
+    aoff[i] = row * (uint32_t)(MODE == 0 ? a.H : K) * 2u + (uint32_t)c * 16u;
   }
   const size_t rowb = (size_t)K / 2;
-  const uint8_t *bsrc[Gm::B_DMA];
+  const uint8_t *bbase[Gm::B_DMA];
+  uint32_t boff[Gm::B_DMA];
 #pragma unroll
   for (int i = 0; i < Gm::B_DMA; ++i) {
     const int s = (i * NW + wave) * 64 + lane;
     const int r = s >> 2, qq = (s & 3) ^ bswz(r);
-    const uint8_t *w;
+    // the 16 B-rows of one (i, wave) lie on one side of COLS (16 | COLS)
+    const int r0 = (i * NW + wave) * 16;
     int row;
     if (MODE == 0) {  // B-rows [0, COLS) gate, [COLS, 2 COLS) up
-      w = r < COLS ? (shared ? a.ws0 : a.w0 + (size_t)e * N * rowb)
-                   : (shared ? a.ws1 : a.w1 + (size_t)e * N * rowb);
+      bbase[i] = r0 < COLS ? (shared ? a.ws0 : a.w0 + (size_t)e * N * rowb)
+                           : (shared ? a.ws1 : a.w1 + (size_t)e * N * rowb);
       row = nb * COLS + (r % COLS);
     } else {
-      w = shared ? a.ws0 : a.w0 + (size_t)e * N * rowb;
+      bbase[i] = shared ? a.ws0 : a.w0 + (size_t)e * N * rowb;
       row = nb * BN + r;
     }
     row = min(row, N - 1);
-    bsrc[i] = w + (size_t)row * rowb + qq * 16;
+    boff[i] = (uint32_t)row * (uint32_t)rowb + (uint32_t)qq * 16u;
   }
-  auto issue = [&](int g) {  // DMA of group g into stage g % STAGES
-    const uint32_t base = lds0 + (uint32_t)(g % STAGES) * STAGE;
+  // DMA of group g into stage st (normally g % STAGES)
+  auto issue_to = [&](int g, int st) {
+    const uint32_t base = lds0 + (uint32_t)st * STAGE;
 #pragma unroll
     for (int i = 0; i < Gm::A_DMA; ++i)
-      dma16(asrc[i] + g * 256, base + (uint32_t)((i * NW + wave) * 1024));
+      dma16s(aoff[i], abase + g * 256, base + (uint32_t)((i * NW + wave) * 1024));
 #pragma unroll
     for (int i = 0; i < Gm::B_DMA; ++i)
-      dma16(bsrc[i] + g * 64, base + A_STAGE + (uint32_t)((i * NW + wave) * 1024));
+      dma16s(boff[i], bbase[i] + g * 64, base + A_STAGE + (uint32_t)((i * NW + wave) * 1024));
   };
+  auto issue = [&](int g) { issue_to(g, g % STAGES); };
 
-  // ---- prologue: group 0 in flight; tables to LDS ---------------------------
+  // ---- prologue: groups 0 .. STAGES-2 in flight; tables to LDS -------------
   issue(0);
+  if (STAGES > 2) issue_to(min(1, G - 1), 1);  // group 1, or a dummy into idle stage 1
   // Tables: every load is issued before the first use (unrolled, clamped
   // indices, no per-lane branches), so the block pays one latency, not one
   // per element.  G <= 32.  Entry idx is (g = idx / rows, row = idx % rows):
@@ -262,65 +301,112 @@ __global__ __launch_bounds__(128 * WN) void k_expert_gemm(GemmArgs a) {
     for (int ns = 0; ns < 4; ++ns) tot[ms][ns] = f32x4{0.f, 0.f, 0.f, 0.f};
   auto main_loop = [&](auto nms_c) {
     constexpr int NMS = decltype(nms_c)::value;
-  uint32_t magic;
-  asm volatile("v_mov_b32 %0, 0x43004300" : "=v"(magic));
-
-  // One barrier per group.  At the top of iteration g every wave has issued
-  // all its MFMAs of group g-1 (they may still be executing) and has read
-  // its last fragment of stage g-1, so after the barrier the DMA of group g+1
-  // may overwrite that stage.  The scale step of group g-1 runs after the
-  // first LDS reads of group g are issued, so the MFMA drain and the LDS
-  // latency overlap instead of adding up.
-  static_assert(STAGES == 2, "one barrier per group needs a 2-stage ring");
-  f32x4 acc[4][4];
-  float sprev[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int g = 0; g < G; ++g) {
-    wait_vm<0>();  // this thread's DMA of group g (issued one group ago)
-    // stage g complete for every thread (and, at g = 0, the LDS tables)
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    block_barrier();
-    if (g + 1 < G) issue(g + 1);
-    const uint8_t *sa = lds + (g % STAGES) * STAGE;
-    const uint8_t *sb = sa + A_STAGE;
-    f32x4 c0[4];
+    uint32_t magic;
+    asm volatile("v_mov_b32 %0, 0x43004300" : "=v"(magic));
+    // acc and sprev start at zero, so the scale step of "group -1" adds
+    // +0 * +0 to tot's +0 and leaves it unchanged (no branch in the loop)
+    f32x4 acc[4][4];
 #pragma unroll
-    for (int ms = 0; ms < NMS; ++ms) c0[ms] = *(const f32x4 *)(xs_lds + g * BM + wm * 64 + ms * 16 + 4 * q);
-    u32x4 bx[4];
-    float sg[4];
+    for (int ms = 0; ms < 4; ++ms)
 #pragma unroll
-    for (int ns = 0; ns < 4; ++ns) {
-      bx[ns] = *(const u32x4 *)(sb + brow[ns] * 64 + ((q ^ bswz(brow[ns])) << 4)) ^ 0x88888888u;
-      sg[ns] = scale_to_f32<SD>(sc_lds[g * BN + brow[ns]]);
-    }
-    if (g > 0) {
+      for (int ns = 0; ns < 4; ++ns) acc[ms][ns] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float sg[4], sprev[4] = {0.f, 0.f, 0.f, 0.f};
+    // Group g, part 1: the scale step of group g-1 (VALU only) and the
+    // scales of group g.
+    auto part_v = [&](int g) {
+#pragma unroll
+      for (int ns = 0; ns < 4; ++ns) sg[ns] = scale_to_f32<SD>(sc_lds[g * BN + brow[ns]]);
 #pragma unroll
       for (int ns = 0; ns < 4; ++ns)
 #pragma unroll
         for (int ms = 0; ms < NMS; ++ms) tot[ms][ns] += sprev[ns] * acc[ms][ns];
-    }
-    const uint8_t *arow = sa + (wm * 64 + m16) * 256;
+    };
+    // Group g, part 2: group sums and A fragments from LDS, B unpacked per
+    // k-slice, and the 4 x NMS MFMAs of each of the 4 k-slices.
+    // this wave's raw B chunks of group g (sign bits flipped: 8 + q)
+    auto load_bx = [&](int g, u32x4 (&bx)[4]) {
+      const uint8_t *sb = lds + (g % STAGES) * STAGE + A_STAGE;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      u32x4 af[4], bf[4];
-      const int chunk = ((4 * q + j) ^ aswz(m16)) << 4;
-#pragma unroll
-      for (int ms = 0; ms < NMS; ++ms) af[ms] = *(const u32x4 *)(arow + ms * 16 * 256 + chunk);
-#pragma unroll
-      for (int ns = 0; ns < 4; ++ns) bf[ns] = nib_slice3(bx[ns], j, magic);
-      // the first k-slice accumulates onto c0 directly (no copies of c0)
+      for (int ns = 0; ns < 4; ++ns)
+        bx[ns] = *(const u32x4 *)(sb + brow[ns] * 64 + ((q ^ bswz(brow[ns])) << 4)) ^ 0x88888888u;
+    };
+    auto part_m = [&](int g, const u32x4 (&bx)[4]) {
+      const uint8_t *sa = lds + (g % STAGES) * STAGE;
+      const uint8_t *arow = sa + (wm * 64 + m16) * 256;
+      // group sums (-136 sum_k a): the first k-slice accumulates onto them
+      f32x4 c0[4];
 #pragma unroll
       for (int ms = 0; ms < NMS; ++ms)
+        c0[ms] = *(const f32x4 *)(xs_lds + g * BM + wm * 64 + ms * 16 + 4 * q);
+      // A fragments one k-slice ahead; the scheduling barrier after each
+      // slice keeps the compiler from hoisting all 16 reads (64 VGPRs) to
+      // the top, which spills at this register budget
+      u32x4 af[2][4];
 #pragma unroll
-        for (int ns = 0; ns < 4; ++ns)
-          acc[ms][ns] = mfma_bf16_16x16x32(af[ms], bf[ns], j == 0 ? c0[ms] : acc[ms][ns]);
+      for (int ms = 0; ms < NMS; ++ms)
+        af[0][ms] = *(const u32x4 *)(arow + ms * 16 * 256 + (((4 * q) ^ aswz(m16)) << 4));
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (j < 3) {
+          const int chunk = ((4 * q + j + 1) ^ aswz(m16)) << 4;
+#pragma unroll
+          for (int ms = 0; ms < NMS; ++ms)
+            af[(j + 1) & 1][ms] = *(const u32x4 *)(arow + ms * 16 * 256 + chunk);
+        }
+        u32x4 bf[4];
+#pragma unroll
+        for (int ns = 0; ns < 4; ++ns) bf[ns] = nib_slice3(bx[ns], j, magic);
+#pragma unroll
+        for (int ms = 0; ms < NMS; ++ms)
+#pragma unroll
+          for (int ns = 0; ns < 4; ++ns)
+            acc[ms][ns] = mfma_bf16_16x16x32(af[j & 1][ms], bf[ns], j == 0 ? c0[ms] : acc[ms][ns]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int ns = 0; ns < 4; ++ns) sprev[ns] = sg[ns];
+    };
+
+    u32x4 bx[4];
+    if constexpr (STAGES == 2) {
+      // One barrier per group.  At the top of iteration g every wave has
+      // issued all its MFMAs of group g-1 (they may still be executing) and
+      // has read its last fragment of stage g-1, so after the barrier the DMA
+      // of group g+1 may overwrite that stage.
+      for (int g = 0; g < G; ++g) {
+        wait_vm<0>();  // this thread's DMA of group g (issued one group ago)
+        // stage g complete for every thread (and, at g = 0, the LDS tables)
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        block_barrier();
+        if (g + 1 < G) issue(g + 1);
+        load_bx(g, bx);
+        part_v(g);
+        part_m(g, bx);
+      }
+    } else {
+      // Three stages; the barrier that ends iteration g-1 also makes group
+      // g+1 visible, so each wave reads its B chunks of the next group into
+      // registers at the end of a group, and a group starts with the scale
+      // step (VALU) that hides its first LDS reads, then unpacks at once.
+      // The DMA of group g+2 is issued after that barrier into stage
+      // (g+2) % 3, which held group g-1, and every thread waits for it
+      // before the next barrier: one iteration of latency per DMA.
+      asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)" ::: "memory");
+      block_barrier();  // groups 0 and 1 and the LDS tables complete
+      for (int g = 0; g < G; ++g) {
+        if (g + 2 < G) issue(g + 2);
+        load_bx(g, bx);
+        part_v(g);
+        part_m(g, bx);
+        wait_vm<0>();
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        block_barrier();
+      }
     }
 #pragma unroll
-    for (int ns = 0; ns < 4; ++ns) sprev[ns] = sg[ns];
-  }
+    for (int ns = 0; ns < 4; ++ns)
 #pragma unroll
-  for (int ns = 0; ns < 4; ++ns)
-#pragma unroll
-    for (int ms = 0; ms < NMS; ++ms) tot[ms][ns] += sprev[ns] * acc[ms][ns];
+      for (int ms = 0; ms < NMS; ++ms) tot[ms][ns] += sprev[ns] * acc[ms][ns];
   };
   // token subtiles of this wave holding tokens of the tile (wave-uniform)
   const int nms = __builtin_amdgcn_readfirstlane(max(0, min(4, (mcnt - wm * 64 + 15) >> 4)));
@@ -330,6 +416,7 @@ __global__ __launch_bounds__(128 * WN) void k_expert_gemm(GemmArgs a) {
     main_loop(std::integral_constant<int, 2>());
   else
     main_loop(std::integral_constant<int, 0>());
+  wait_vm<0>();  // no DMA into the ring remains in flight
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   block_barrier();  // every wave's last read of the ring precedes the staging below
 
@@ -339,7 +426,9 @@ __global__ __launch_bounds__(128 * WN) void k_expert_gemm(GemmArgs a) {
   // row chunks.
   if (MODE == 0) {
     constexpr int OST = COLS * 2 + 16;  // staged row stride, bytes
-    static_assert(BM * OST <= STAGES * STAGE, "staging exceeds the ring");
+    // staged rows, then red_sum[WN][BM] fp32 (per row-wave row sums)
+    float *red_sum = (float *)(lds + BM * OST);
+    static_assert(BM * OST + WN * BM * 4 <= STAGES * STAGE, "staging exceeds the ring");
     float rowsum[4][4];
 #pragma unroll
     for (int ms = 0; ms < 4; ++ms)
@@ -360,8 +449,8 @@ __global__ __launch_bounds__(128 * WN) void k_expert_gemm(GemmArgs a) {
         uint32_t v[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          v[r] = f32_to_bf16(silu_mul(tot[ms][h][r], tot[ms][h + 2][r]));
-          rowsum[ms][r] += bf16_to_f32((uint16_t)v[r]);
+          v[r] = bf16_bits(silu_mul_fast(tot[ms][h][r], tot[ms][h + 2][r]));
+          rowsum[ms][r] += __uint_as_float(v[r] << 16);
         }
         const uint32_t send = hi4 ? (v[0] | (v[1] << 16)) : (v[2] | (v[3] << 16));
         // lane ^ 4 inside each group of 32 lanes (ds_swizzle bit mode)
@@ -377,14 +466,7 @@ __global__ __launch_bounds__(128 * WN) void k_expert_gemm(GemmArgs a) {
 #pragma unroll
     for (int ms = 0; ms < 4; ++ms)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float v = rowsum[ms][r];
-        v += __shfl_xor(v, 1, 64);
-        v += __shfl_xor(v, 2, 64);
-        v += __shfl_xor(v, 4, 64);
-        v += __shfl_xor(v, 8, 64);
-        rowsum[ms][r] = v;
-      }
+      for (int r = 0; r < 4; ++r) rowsum[ms][r] = row16_sum(rowsum[ms][r]);
     if (m16 == 0)
 #pragma unroll
       for (int ms = 0; ms < 4; ++ms)
@@ -423,7 +505,7 @@ __global__ __launch_bounds__(128 * WN) void k_expert_gemm(GemmArgs a) {
       for (int ms = 0; ms < 4; ++ms) {
         uint32_t v[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) v[r] = f32_to_bf16(tot[ms][ns][r]);
+        for (int r = 0; r < 4; ++r) v[r] = bf16_bits(tot[ms][ns][r]);
         const uint32_t send = odd ? (v[0] | (v[1] << 16)) : (v[2] | (v[3] << 16));
         const uint32_t recv =
             (uint32_t)__builtin_amdgcn_update_dpp(0, (int)send, 0xB1, 0xF, 0xF, false);  // lane ^ 1
@@ -445,6 +527,24 @@ __global__ __launch_bounds__(128 * WN) void k_expert_gemm(GemmArgs a) {
         *(u32x4 *)(a.o + orow * a.H + col) = *(const u32x4 *)(lds + row * OST + c * 16);
       }
     }
+  }
+}
+
+// Persistent grid: one block per resident slot (occupancy x CUs) walks the
+// items in rounds of gridDim.x.  Within a round the items a block takes are
+// XCD-contiguous (xcd_remap), so the column blocks of one expert tile run on
+// one XCD at the same time and share its A rows through that L2.  The item
+// count comes from the dispatch on the device; the host sizes the grid from
+// its upper bound.
+template <int SD, int MODE, int WN, int STAGES_>
+__global__ __launch_bounds__(128 * WN) void k_expert_gemm(GemmArgs a) {
+  const int n_items = *a.n_tiles * a.n_nblk;
+  const int P = gridDim.x;
+  for (int base = 0; base < n_items; base += P) {
+    const int lb = base + xcd_remap(blockIdx.x, P);
+    if (lb >= n_items) break;  // later rounds only hold larger items
+    gemm_item<SD, MODE, WN, STAGES_>(a, lb);
+    __syncthreads();  // the epilogue's LDS reads precede the next item's DMA
   }
 }
 
@@ -580,6 +680,15 @@ __global__ __launch_bounds__(256) void k_router_gemm(const uint16_t *__restrict_
   }
 }
 
+constexpr size_t GEMM_LDS_MAX = 160 * 1024;  // LDS per workgroup on gfx950
+
+template <int WN>
+size_t gemm_lds_bytes(int stages, int Gmax) {
+  using Gm = Geo<WN, 2>;
+  return (size_t)stages * Gm::STAGE + (((size_t)Gm::BN * Gmax * 2 + 15) & ~(size_t)15) +
+         sizeof(float) * (size_t)BM * Gmax;
+}
+
 template <int WN, int STAGES_>
 hipError_t launch_geo(int mode, int scale_dtype, GemmArgs a, int max_tiles, hipStream_t s) {
   using Gm = Geo<WN, STAGES_>;
@@ -590,21 +699,25 @@ hipError_t launch_geo(int mode, int scale_dtype, GemmArgs a, int max_tiles, hipS
   if (grid > 0x7FFFFFFF) return hipErrorInvalidValue;
   const int Gmax = (mode == 0 ? a.H : (a.I > a.Is ? a.I : a.Is)) / 128;
   if (Gmax > 32) return hipErrorInvalidValue;  // table loads assume K <= 4096
-  const size_t lds = (size_t)Gm::STAGES * Gm::STAGE +
-                     (((size_t)Gm::BN * Gmax * 2 + 15) & ~(size_t)15) +
-                     sizeof(float) * ((size_t)BM * Gmax + (size_t)WN * BM);
-  if (lds > 160 * 1024) return hipErrorInvalidValue;
-  if (mode == 0) {
-    if (scale_dtype == AINFER_SCALE_FP16)
-      k_expert_gemm<AINFER_SCALE_FP16, 0, WN, STAGES_><<<(unsigned)grid, Gm::THREADS, lds, s>>>(a);
-    else
-      k_expert_gemm<AINFER_SCALE_BF16, 0, WN, STAGES_><<<(unsigned)grid, Gm::THREADS, lds, s>>>(a);
-  } else {
-    if (scale_dtype == AINFER_SCALE_FP16)
-      k_expert_gemm<AINFER_SCALE_FP16, 1, WN, STAGES_><<<(unsigned)grid, Gm::THREADS, lds, s>>>(a);
-    else
-      k_expert_gemm<AINFER_SCALE_BF16, 1, WN, STAGES_><<<(unsigned)grid, Gm::THREADS, lds, s>>>(a);
-  }
+  const size_t lds = gemm_lds_bytes<WN>(Gm::STAGES, Gmax);
+  if (lds > GEMM_LDS_MAX) return hipErrorInvalidValue;
+  void (*kern)(GemmArgs);
+  if (mode == 0)
+    kern = scale_dtype == AINFER_SCALE_FP16 ? k_expert_gemm<AINFER_SCALE_FP16, 0, WN, STAGES_>
+                                            : k_expert_gemm<AINFER_SCALE_BF16, 0, WN, STAGES_>;
+  else
+    kern = scale_dtype == AINFER_SCALE_FP16 ? k_expert_gemm<AINFER_SCALE_FP16, 1, WN, STAGES_>
+                                            : k_expert_gemm<AINFER_SCALE_BF16, 1, WN, STAGES_>;
+  // resident blocks per CU for this kernel and LDS size, times the CUs
+  int dev = 0, cus = 0, per_cu = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e == hipSuccess)
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, Gm::THREADS, lds);
+  if (e != hipSuccess) return e;
+  if (per_cu < 1) return hipErrorInvalidConfiguration;
+  const long resident = (long)per_cu * cus;
+  kern<<<(unsigned)(grid < resident ? grid : resident), Gm::THREADS, lds, s>>>(a);
   return hipGetLastError();
 }
 
@@ -628,5 +741,9 @@ hipError_t launch_router_gemm(const void *x, const void *rw, const float *bias, 
 hipError_t launch_expert_gemm(int mode, int scale_dtype, GemmArgs a, int max_tiles,
                               hipStream_t s) {
   if (max_tiles <= 0) return hipSuccess;
-  return launch_geo<GEMM_WN, GEMM_STAGES>(mode, scale_dtype, a, max_tiles, s);
+  // the 3-stage ring where its LDS fits (K <= 2048 at GEMM_WN = 4)
+  const int Gmax = (mode == 0 ? a.H : (a.I > a.Is ? a.I : a.Is)) / 128;
+  if (gemm_lds_bytes<GEMM_WN>(3, Gmax) <= GEMM_LDS_MAX)
+    return launch_geo<GEMM_WN, 3>(mode, scale_dtype, a, max_tiles, s);
+  return launch_geo<GEMM_WN, 2>(mode, scale_dtype, a, max_tiles, s);
 }

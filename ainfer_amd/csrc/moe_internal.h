@@ -58,9 +58,6 @@ constexpr int GEMM_MT = 128;
 #ifndef GEMM_WN
 #define GEMM_WN 4       // row waves per GEMM block (2 x GEMM_WN waves)
 #endif
-#ifndef GEMM_STAGES
-#define GEMM_STAGES 2   // LDS ring depth
-#endif
 constexpr int GEMM_MIN_T = 256;
 
 // Outputs of the dispatch stage.  tiles: (expert, first position, rows,
