@@ -119,9 +119,20 @@ __device__ __forceinline__ float silu_mul_fast(float g, float u) {
   return g * __builtin_amdgcn_rcpf(1.0f + e) * u;
 }
 
-// round to nearest even bf16 (v_cvt_pk_bf16_f32)
-__device__ __forceinline__ uint32_t bf16_bits(float f) {
-  return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f);
+// two floats as packed bf16 (low half: lo), round to nearest even
+__device__ __forceinline__ uint32_t bf16x2_bits(float lo, float hi) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)lo, (__bf16)hi});
+}
+
+// Byte selectors for v_perm_b32(recv, own, sel) in the epilogues' pair
+// exchange: a lane holds rows (0, 1) of its column as own = r0 | r1 << 16
+// (lower lane of the pair) or rows (2, 3) (upper lane), sends the other two
+// rows to its partner and builds two dwords, each one row of the column
+// pair (lower column in the low half).  Selector bytes 0-3 take own, 4-7
+// recv.
+__device__ __forceinline__ uint32_t pair_sel(bool upper, int d) {
+  return upper ? (d == 0 ? 0x01000504u : 0x03020706u) : (d == 0 ? 0x05040100u : 0x07060302u);
 }
 
 // sum over the 16 lanes of a DPP row (lane & 15), in every lane of the row
@@ -133,9 +144,10 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v;
 }
 
-// One item: expert tile lb / n_nblk, column block lb % n_nblk.
+// One item: expert tile lb / n_nblk (its entry t, loaded by the caller one
+// item ahead), column block lb % n_nblk.
 template <int SD, int MODE, int WN, int STAGES_>
-__device__ __forceinline__ void gemm_item(const GemmArgs &a, const int lb) {
+__device__ __forceinline__ void gemm_item(const GemmArgs &a, const int lb, const int4 t) {
   using Gm = Geo<WN, STAGES_>;
   constexpr int BN = Gm::BN, STAGES = Gm::STAGES, A_STAGE = Gm::A_STAGE, STAGE = Gm::STAGE;
   constexpr int NW = Gm::NW, THREADS = Gm::THREADS, COLS = Gm::COLS;
@@ -144,8 +156,7 @@ __device__ __forceinline__ void gemm_item(const GemmArgs &a, const int lb) {
   // staging and row sums reuse the idle ring
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int n_nb = a.n_nblk;
-  const int tile_id = lb / n_nb, nb = lb % n_nb;
-  const int4 t = a.tiles[tile_id];
+  const int nb = lb % n_nb;
   const int e = t.x, pos0 = t.y, mcnt = t.z;
   const bool shared = e == a.E;
   // MODE 0: N = act columns (I or Is), block covers 64 of them; MODE 1: N = H, 128 rows
@@ -219,14 +230,14 @@ __device__ __forceinline__ void gemm_item(const GemmArgs &a, const int lb) {
   };
   auto issue = [&](int g) { issue_to(g, g % STAGES); };
 
-  // ---- prologue: groups 0 .. STAGES-2 in flight; tables to LDS -------------
-  issue(0);
-  if (STAGES > 2) issue_to(min(1, G - 1), 1);  // group 1, or a dummy into idle stage 1
+  // ---- prologue: tables to LDS; groups 0 .. STAGES-2 in flight -------------
   // Tables: every load is issued before the first use (unrolled, clamped
   // indices, no per-lane branches), so the block pays one latency, not one
   // per element.  G <= 32.  Entry idx is (g = idx / rows, row = idx % rows):
   // consecutive threads write consecutive LDS words (the global reads
-  // gather instead), so the LDS stores are free of bank conflicts.
+  // gather instead), so the LDS stores are free of bank conflicts.  The
+  // first groups' DMA is issued after the table loads: loads complete in
+  // issue order, so a wait for a table value never waits for the DMA.
   {
     constexpr int SC_IT = BN * 32 / THREADS;
     uint16_t scv[SC_IT];
@@ -273,6 +284,8 @@ __device__ __forceinline__ void gemm_item(const GemmArgs &a, const int lb) {
         xv[i] = v;
       }
     }
+    issue(0);
+    if (STAGES > 2) issue_to(min(1, G - 1), 1);  // group 1, or a dummy into idle stage 1
 #pragma unroll
     for (int i = 0; i < SC_IT; ++i) {
       const int idx = tid + i * THREADS;
@@ -439,27 +452,31 @@ __device__ __forceinline__ void gemm_item(const GemmArgs &a, const int lb) {
     // halves so that each lane stores whole dwords (lane bit 2 clear: rows
     // r = 0, 1; set: rows 2, 3).  2-byte LDS stores cost several times a
     // dword store.
+    // Branch-free: the selects below are plain values and v_perm_b32 takes
+    // a per-lane selector (ternaries over expressions became divergent
+    // branches around every store).
     const bool hi4 = (m16 & 4) != 0;
+    const uint32_t sel0 = pair_sel(hi4, 0), sel1 = pair_sel(hi4, 1);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       // within a 32-aligned block of columns, MFMA order is block-local
       const int p = perm32_pos(wn * 32 + h * 16 + (m16 & ~4));  // the pair's even position
 #pragma unroll
       for (int ms = 0; ms < 4; ++ms) {
-        uint32_t v[4];
+        float f[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          v[r] = bf16_bits(silu_mul_fast(tot[ms][h][r], tot[ms][h + 2][r]));
-          rowsum[ms][r] += __uint_as_float(v[r] << 16);
-        }
-        const uint32_t send = hi4 ? (v[0] | (v[1] << 16)) : (v[2] | (v[3] << 16));
+        for (int r = 0; r < 4; ++r) f[r] = silu_mul_fast(tot[ms][h][r], tot[ms][h + 2][r]);
+        const uint32_t p01 = bf16x2_bits(f[0], f[1]), p23 = bf16x2_bits(f[2], f[3]);
+        rowsum[ms][0] += __uint_as_float(p01 << 16);
+        rowsum[ms][1] += __uint_as_float(p01 & 0xFFFF0000u);
+        rowsum[ms][2] += __uint_as_float(p23 << 16);
+        rowsum[ms][3] += __uint_as_float(p23 & 0xFFFF0000u);
+        const uint32_t send = hi4 ? p01 : p23, own = hi4 ? p23 : p01;
         // lane ^ 4 inside each group of 32 lanes (ds_swizzle bit mode)
         const uint32_t recv = (uint32_t)__builtin_amdgcn_ds_swizzle((int)send, 0x101F);
         const int row0 = wm * 64 + ms * 16 + 4 * q + (hi4 ? 2 : 0);
-        const uint32_t d0 = hi4 ? ((recv & 0xFFFFu) | (v[2] << 16)) : (v[0] | (recv << 16));
-        const uint32_t d1 = hi4 ? ((recv >> 16) | (v[3] << 16)) : (v[1] | (recv & 0xFFFF0000u));
-        *(uint32_t *)(lds + row0 * OST + p * 2) = d0;
-        *(uint32_t *)(lds + (row0 + 1) * OST + p * 2) = d1;
+        *(uint32_t *)(lds + row0 * OST + p * 2) = __builtin_amdgcn_perm(recv, own, sel0);
+        *(uint32_t *)(lds + (row0 + 1) * OST + p * 2) = __builtin_amdgcn_perm(recv, own, sel1);
       }
     }
     // per-row sum over this wave's 32 columns: reduce over the 16 lanes m16
@@ -475,12 +492,17 @@ __device__ __forceinline__ void gemm_item(const GemmArgs &a, const int lb) {
     __syncthreads();
     uint16_t *dst = shared ? a.act_s : a.act;
     constexpr int CPR = COLS / 8;  // 16-byte chunks per row
+    constexpr int NST = BM * CPR / THREADS;
+    u32x4 out[NST];  // every LDS read before the (predicated) stores
 #pragma unroll
-    for (int i = 0; i < BM * CPR / THREADS; ++i) {
+    for (int i = 0; i < NST; ++i) {
+      const int idx = tid + i * THREADS;
+      out[i] = *(const u32x4 *)(lds + (idx / CPR) * OST + (idx % CPR) * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < NST; ++i) {
       const int idx = tid + i * THREADS, row = idx / CPR, c = idx % CPR;
-      if (row < mcnt)
-        *(u32x4 *)(dst + (size_t)(pos0 + row) * N + nb * COLS + c * 8) =
-            *(const u32x4 *)(lds + row * OST + c * 16);
+      if (row < mcnt) *(u32x4 *)(dst + (size_t)(pos0 + row) * N + nb * COLS + c * 8) = out[i];
     }
     if (tid < BM && tid < mcnt) {
       float *as = shared ? a.asum_s : a.asum;
@@ -498,33 +520,38 @@ __device__ __forceinline__ void gemm_item(const GemmArgs &a, const int lb) {
     // 1; odd lane: rows 2, 3).  With the 528-byte row stride the 32 lanes of
     // one store hit 32 distinct banks.
     const bool odd = (m16 & 1) != 0;
+    const uint32_t sel0 = pair_sel(odd, 0), sel1 = pair_sel(odd, 1);
 #pragma unroll
     for (int ns = 0; ns < 4; ++ns) {
       const int cl = wn * 64 + 16 * ns + (m16 & ~1);
 #pragma unroll
       for (int ms = 0; ms < 4; ++ms) {
-        uint32_t v[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) v[r] = bf16_bits(tot[ms][ns][r]);
-        const uint32_t send = odd ? (v[0] | (v[1] << 16)) : (v[2] | (v[3] << 16));
+        const uint32_t p01 = bf16x2_bits(tot[ms][ns][0], tot[ms][ns][1]);
+        const uint32_t p23 = bf16x2_bits(tot[ms][ns][2], tot[ms][ns][3]);
+        const uint32_t send = odd ? p01 : p23, own = odd ? p23 : p01;
         const uint32_t recv =
             (uint32_t)__builtin_amdgcn_update_dpp(0, (int)send, 0xB1, 0xF, 0xF, false);  // lane ^ 1
         const int row0 = wm * 64 + ms * 16 + 4 * q + (odd ? 2 : 0);
-        const uint32_t d0 = odd ? ((recv & 0xFFFFu) | (v[2] << 16)) : (v[0] | (recv << 16));
-        const uint32_t d1 = odd ? ((recv >> 16) | (v[3] << 16)) : (v[1] | (recv & 0xFFFF0000u));
-        *(uint32_t *)(lds + row0 * OST + cl * 2) = d0;
-        *(uint32_t *)(lds + (row0 + 1) * OST + cl * 2) = d1;
+        *(uint32_t *)(lds + row0 * OST + cl * 2) = __builtin_amdgcn_perm(recv, own, sel0);
+        *(uint32_t *)(lds + (row0 + 1) * OST + cl * 2) = __builtin_amdgcn_perm(recv, own, sel1);
       }
     }
     __syncthreads();
     constexpr int CPR = BN / 8;
+    constexpr int NST = BM * CPR / THREADS;
+    u32x4 out[NST];  // every LDS read before the (predicated) stores
 #pragma unroll
-    for (int i = 0; i < BM * CPR / THREADS; ++i) {
+    for (int i = 0; i < NST; ++i) {
+      const int idx = tid + i * THREADS;
+      out[i] = *(const u32x4 *)(lds + (idx / CPR) * OST + (idx % CPR) * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < NST; ++i) {
       const int idx = tid + i * THREADS, row = idx / CPR, c = idx % CPR;
       const int col = nb * BN + c * 8;
       if (row < mcnt && col < N) {
         const size_t orow = shared ? (size_t)a.T * a.k + pos0 + row : (size_t)(pos0 + row);
-        *(u32x4 *)(a.o + orow * a.H + col) = *(const u32x4 *)(lds + row * OST + c * 16);
+        *(u32x4 *)(a.o + orow * a.H + col) = out[i];
       }
     }
   }
@@ -539,11 +566,17 @@ __device__ __forceinline__ void gemm_item(const GemmArgs &a, const int lb) {
 template <int SD, int MODE, int WN, int STAGES_>
 __global__ __launch_bounds__(128 * WN) void k_expert_gemm(GemmArgs a) {
   const int n_items = *a.n_tiles * a.n_nblk;
-  const int P = gridDim.x;
+  const int P = gridDim.x, me = xcd_remap(blockIdx.x, P);
+  // the tile entry of the next item is loaded while this one runs (it is a
+  // global load the item's whole prologue would otherwise wait on)
+  int4 t = me < n_items ? a.tiles[me / a.n_nblk] : int4{0, 0, 0, 0};
   for (int base = 0; base < n_items; base += P) {
-    const int lb = base + xcd_remap(blockIdx.x, P);
+    const int lb = base + me;
     if (lb >= n_items) break;  // later rounds only hold larger items
-    gemm_item<SD, MODE, WN, STAGES_>(a, lb);
+    const int ln = lb + P;
+    const int4 tn = ln < n_items ? a.tiles[ln / a.n_nblk] : t;
+    gemm_item<SD, MODE, WN, STAGES_>(a, lb, t);
+    t = tn;
     __syncthreads();  // the epilogue's LDS reads precede the next item's DMA
   }
 }
