@@ -1,6 +1,7 @@
 // moe_common.h - device helpers shared by the gfx950 MoE kernels.
 #pragma once
 #include <hip/hip_runtime.h>
+#include <type_traits>
 #include <stdint.h>
 
 #include "../../include/ainfer_moe.h"
@@ -119,6 +120,29 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 }
 __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
   return wave_reduce_u32(v, [](uint32_t a, uint32_t b) { return a < b ? a : b; });
+}
+// sum over the 64 lanes of an fp64 value, in every lane, on the DPP path
+// (the same steps as wave_reduce_u32; masked-off rows add 0).  The order of
+// the additions is fixed but is not the xor butterfly's: only for sums whose
+// result does not depend on the order (rms_mean_f's exact cases).
+__device__ __forceinline__ double wave_sum_f64(double v) {
+  auto step = [&](auto ctrl_c, auto rmask_c) {
+    constexpr int CTRL = decltype(ctrl_c)::value, RMASK = decltype(rmask_c)::value;
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, RMASK, 0xF, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, RMASK, 0xF, false);
+    v += __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+  };
+  step(std::integral_constant<int, 0xB1>(), std::integral_constant<int, 0xF>());
+  step(std::integral_constant<int, 0x4E>(), std::integral_constant<int, 0xF>());
+  step(std::integral_constant<int, 0x141>(), std::integral_constant<int, 0xF>());
+  step(std::integral_constant<int, 0x140>(), std::integral_constant<int, 0xF>());
+  step(std::integral_constant<int, 0x142>(), std::integral_constant<int, 0xA>());
+  step(std::integral_constant<int, 0x143>(), std::integral_constant<int, 0xC>());
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, 63);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), 63);
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
 }
 // inclusive prefix sum over the 64 lanes (all active): Hillis-Steele inside
 // each row of 16 lanes by DPP row shifts, then the row totals carried across

@@ -13,13 +13,14 @@
 //                   (one row x 1 or 2 tokens) unit per wave, each stored
 //                   with an sc1 store as ~bits into a key slot of the sync
 //                   region (never 0: ~bits == 0 only for one NaN pattern no
-//                   bf16 product or sum yields); the last workgroup (one wave
-//                   per token) writes x in MFMA order, polls its token's slots
+//                   bf16 product or sum yields); workgroup NR (one wave per
+//                   token) polls its token's slots
 //                   until none is 0, clears them, takes the exact top-k, the
 //                   weights and the shared gate, and builds the dispatch
 //                   (tiles of at most DEC_MT tokens) from LDS.  A slot that is
 //                   its own ready flag saves the store wait, barrier and
-//                   counter round trip of an arrival.
+//                   counter round trip of an arrival.  Workgroup NR + 1
+//                   writes x in MFMA order meanwhile.
 //  k_experts_decode one workgroup per item: first every gate/up + SiLU item
 //                   (tile-major, slab-minor), one arrival each on
 //                   gu_done[tile]; then every down item, which requests its
@@ -199,13 +200,10 @@ __global__ __launch_bounds__(W * 64) void k_route_decode(RouteDecodeArgs a) {
                   emin = min(emin, bf16_qexp(u));
                 }
             }
-            double tot = (p4[0] + p4[1]) + (p4[2] + p4[3]);
-#pragma unroll
-            for (int st = 32; st >= 1; st >>= 1) {
-              tot += __shfl_xor(tot, st, 64);
-              emin = min(emin, __shfl_xor(emin, st, 64));
-            }
-            tot = __shfl(tot, 0, 64);  // lanes may round differently: one value
+            // wave reductions on the DPP path (no LDS round trips on this
+            // critical path); one value in every lane
+            const double tot = wave_sum_f64((p4[0] + p4[1]) + (p4[2] + p4[3]));
+            emin = (int)wave_min_u32((uint32_t)emin);
             inv[j] = rms_inv_finish(tot, emin, a.x + (size_t)min(t0 + j, T - 1) * H, H,
                                     a.norm.eps, lane);
           }
@@ -257,13 +255,18 @@ __global__ __launch_bounds__(W * 64) void k_route_decode(RouteDecodeArgs a) {
     DTRACE(0, 1);
     return;
   }
-  // ---- the selection workgroup: one wave per token (T <= W) ---------------
   const int t = wave;
-  // the MFMA-order copy of x does not depend on the routing
-  if (t < T && a.xperm) {
-    const float inv = NORM ? row_rms_inv(a.x + (size_t)t * H, H, a.norm.eps, lane) : 1.0f;
-    write_xperm(a.x + (size_t)t * H, a.xperm, nullptr, t, H, lane, NORM ? &a.norm : nullptr, inv);
+  if ((int)blockIdx.x > a.NR) {
+    // ---- workgroup NR + 1: the MFMA-order copy of x, one wave per token.
+    // It does not depend on the routing; a workgroup of its own keeps it off
+    // the selection's path (the selection polls as soon as it starts).
+    if (t < T && a.xperm) {
+      const float inv = NORM ? row_rms_inv(a.x + (size_t)t * H, H, a.norm.eps, lane) : 1.0f;
+      write_xperm(a.x + (size_t)t * H, a.xperm, nullptr, t, H, lane, NORM ? &a.norm : nullptr, inv);
+    }
+    return;
   }
+  // ---- the selection workgroup (NR): one wave per token (T <= W) ----------
   DTRACE(0, 1);
   uint32_t raw[NV], graw = 0u;
   if (t < T) {
@@ -513,7 +516,7 @@ hipError_t launch_route_decode(const void *x, const void *rw, const float *bias,
   const int units = (nrows + RD_R - 1) / RD_R * ((T + tt - 1) / tt);
   const int wg = tt == 1 ? RD_W1 : RD_WAVES;
   a.NR = (units + wg - 1) / wg;
-  const unsigned grid = a.NR + 1;
+  const unsigned grid = a.NR + 2;  // router units, the selection, the x copy
   const int nv = (E + 63) / 64;
   auto go = [&](auto nv_c) {
     constexpr int NVc = decltype(nv_c)::value;
