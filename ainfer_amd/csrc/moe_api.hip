@@ -365,10 +365,15 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
   if (T <= DECODE_MAX_T && decode_geometry(*s, &dg)) {
     // decode: two launches (moe_decode.hip)
     int32_t *sync = at<int32_t>(ws, L.sync);
+    // the expert kernels read the tiles and positions only: no per-expert
+    // counts or offsets on this path
+    DispatchOut dr = d;
+    dr.counts = nullptr;
+    dr.offsets = nullptr;
     HIP_TRY(launch_route_decode(x, w->router_w, w->router_bias, w->shared_gate_w,
                                 at<float>(ws, L.logits), at<float>(ws, L.sg_logit),
                                 at<int32_t>(ws, L.idx), at<float>(ws, L.w), at<float>(ws, L.sg),
-                                at<uint16_t>(ws, L.xperm), T, H, E, k, has_shared, &d, sync,
+                                at<uint16_t>(ws, L.xperm), T, H, E, k, has_shared, &dr, sync,
                                 (uint32_t *)(sync + L.slots), norm, st));
     pc->end(2);
     ExpertArgs gu = expert_args(s, w, L, ws, d, T, 0), dn = expert_args(s, w, L, ws, d, T, 1);

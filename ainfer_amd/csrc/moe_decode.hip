@@ -213,6 +213,7 @@ __global__ __launch_bounds__(W * 64) void k_route_decode(RouteDecodeArgs a) {
             for (int j = 0; j < RD_TT; ++j)
 #pragma unroll
               for (int q = 0; q < 4; ++q) xv[b][j][q] = norm_pair(xv[b][j][q], nv[b][q], inv[j], a.norm);
+          DTRACE(0, 2);
         }
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
@@ -240,6 +241,7 @@ __global__ __launch_bounds__(W * 64) void k_route_decode(RouteDecodeArgs a) {
         for (int i = 0; i < RD_R; ++i)
 #pragma unroll
           for (int j = 0; j < RD_TT; ++j) acc[i][j] = acc[i][j] + __shfl_xor(acc[i][j], m, 64);
+      DTRACE(0, 3);
       if (lane == 0) {
 #pragma unroll
         for (int i = 0; i < RD_R; ++i)

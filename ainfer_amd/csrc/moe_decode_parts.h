@@ -44,6 +44,39 @@ __device__ __forceinline__ void dispatch_decode(const int32_t *__restrict__ idx,
   __shared__ int offl[1024];
   __shared__ int wsum[W];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  if (T == 1 && k <= 64) {
+    // One token: the k picks are distinct experts, each a one-token tile.
+    // Pick j's position is its rank among the picks by expert index (the
+    // general path's expert-order scan); wave 0 alone, no barrier.
+    if (wv != 0) return;
+    const int e = lane < k ? idx[lane] : 0x7FFFFFFF;
+    int r = 0;
+    for (int j = 0; j < k; ++j) r += __builtin_amdgcn_readlane(e, j) < e ? 1 : 0;
+    if (lane < k) {
+      ds.tiles[r] = make_int4(e, r, 1, 0);
+      ds.perm[r] = lane;
+      ds.inv[lane] = r;
+      ds.ptok[r] = 0;
+    }
+    if (lane == 0) {
+      if (has_shared) ds.tiles[k] = make_int4(E, 0, 1, 0);
+      *ds.n_tiles = k + (has_shared ? 1 : 0);
+      if (ds.offsets) ds.offsets[E] = k;
+    }
+    if (ds.counts) {
+      for (int ee = lane; ee < E; ee += 64) {
+        int below = 0, hit = 0;
+        for (int j = 0; j < k; ++j) {
+          const int ej = __builtin_amdgcn_readlane(e, j);
+          below += ej < ee ? 1 : 0;
+          hit |= ej == ee ? 1 : 0;
+        }
+        ds.counts[ee] = hit;
+        ds.offsets[ee] = below;
+      }
+    }
+    return;
+  }
   constexpr int NT = W * 64;
   for (int e = tid; e < E; e += NT) msk[e] = 0u;
   __syncthreads();
