@@ -169,16 +169,23 @@ __global__ __launch_bounds__(W * 64) void k_route_decode(RouteDecodeArgs a) {
       // chunks l, l + 64, ... in order
       for (int cb = lane; cb < nch; cb += 64 * NB) {
         u32x4 wv[NB][RD_R], xv[NB][RD_TT], nv[NB];
+        // x and the norm weight first: loads complete in issue order, so the
+        // RMSNorm (which needs only them) runs while the router row, a cold
+        // read from HBM, is still in flight
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
           const int c = min(cb + 64 * b, nch - 1);
-#pragma unroll
-          for (int i = 0; i < RD_R; ++i) wv[b][i] = *(const u32x4 *)(wr[i] + (size_t)c * 8);
 #pragma unroll
           for (int j = 0; j < RD_TT; ++j)
             xv[b][j] = *(const u32x4 *)(a.x + (size_t)min(t0 + j, T - 1) * H + (size_t)c * 8);
           nv[b] = NORM && a.norm.w ? *(const u32x4 *)(a.norm.w + (size_t)c * 8)
                                    : u32x4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          const int c = min(cb + 64 * b, nch - 1);
+#pragma unroll
+          for (int i = 0; i < RD_R; ++i) wv[b][i] = *(const u32x4 *)(wr[i] + (size_t)c * 8);
         }
         if constexpr (NORM) {
           // sum of squares in any order (rms_mean_f's tests hold for every
@@ -269,7 +276,6 @@ __global__ __launch_bounds__(W * 64) void k_route_decode(RouteDecodeArgs a) {
     return;
   }
   // ---- the selection workgroup (NR): one wave per token (T <= W) ----------
-  DTRACE(0, 1);
   uint32_t raw[NV], graw = 0u;
   if (t < T) {
     uint32_t *sl = a.slots + (size_t)t * (E + 1);
@@ -296,6 +302,7 @@ __global__ __launch_bounds__(W * 64) void k_route_decode(RouteDecodeArgs a) {
     int seli;
     uint32_t selk;
     wave_topk_fast<NV>(key, E, k, lane, seli, selk, s_cand[wave], s_sel[wave]);
+    DTRACE(0, 1);
     const float selv = lane < k ? key_to_float(selk) : 0.0f;
     const float vmax = __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(selv)));
     const float p = lane < k ? expf(selv - vmax) : 0.0f;
