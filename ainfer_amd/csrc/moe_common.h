@@ -269,7 +269,7 @@ __device__ __forceinline__ int bf16_qexp(uint16_t u) {
 // Sequential fp64 sum of squares of a bf16 row (the reference order for
 // N != 5120): the rare fallback of rms_mean_f, run by one lane.  Loads are
 // issued 16 elements at a time; the additions stay in element order.
-__device__ __attribute__((noinline)) double row_sumsq_seq(const uint16_t *__restrict__ xr,
+__device__ __forceinline__ double row_sumsq_seq(const uint16_t *__restrict__ xr,
                                                           int H) {
   double ss = 0.0;
   int j = 0;
@@ -350,21 +350,28 @@ __device__ __forceinline__ float row_rms_inv(const uint16_t *__restrict__ xr, in
   return rms_inv_finish(tot, emin, xr, H, eps, lane);
 }
 
-// one packed bf16 pair of x normalized as k_rmsnorm writes it
+// two floats as packed bf16 (low half: lo), round to nearest even
+// (v_cvt_pk_bf16_f32; for finite values the same bits as f32_to_bf16)
+__device__ __forceinline__ uint32_t bf16x2_bits(float lo, float hi) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)lo, (__bf16)hi});
+}
+
+// one packed bf16 pair of x normalized as k_rmsnorm writes it: (x * inv) * wt
+// in fp32, rounded to nearest even
 __device__ __forceinline__ uint32_t norm_pair(uint32_t xp, uint32_t wp, float inv,
                                               const NormIn &n) {
-  uint32_t out = 0u;
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const float v = bf16_to_f32((uint16_t)(xp >> (16 * h))) * inv;
-    float wt = 1.0f;
-    if (n.w) {
-      const float wv = bf16_to_f32((uint16_t)(wp >> (16 * h)));
-      wt = n.mode == AINFER_NORM_ONE_PLUS ? 1.0f + wv : wv;
+  const float v0 = __uint_as_float(xp << 16) * inv, v1 = __uint_as_float(xp & 0xFFFF0000u) * inv;
+  float w0 = 1.0f, w1 = 1.0f;
+  if (n.w) {
+    w0 = __uint_as_float(wp << 16);
+    w1 = __uint_as_float(wp & 0xFFFF0000u);
+    if (n.mode == AINFER_NORM_ONE_PLUS) {
+      w0 = 1.0f + w0;
+      w1 = 1.0f + w1;
     }
-    out |= (uint32_t)f32_to_bf16(v * wt) << (16 * h);
   }
-  return out;
+  return bf16x2_bits(v0 * w0, v1 * w1);
 }
 
 __device__ __forceinline__ void write_xperm(const uint16_t *__restrict__ xrow,

@@ -119,12 +119,6 @@ __device__ __forceinline__ float silu_mul_fast(float g, float u) {
   return g * __builtin_amdgcn_rcpf(1.0f + e) * u;
 }
 
-// two floats as packed bf16 (low half: lo), round to nearest even
-__device__ __forceinline__ uint32_t bf16x2_bits(float lo, float hi) {
-  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-  return __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)lo, (__bf16)hi});
-}
-
 // Byte selectors for v_perm_b32(recv, own, sel) in the epilogues' pair
 // exchange: a lane holds rows (0, 1) of its column as own = r0 | r1 << 16
 // (lower lane of the pair) or rows (2, 3) (upper lane), sends the other two
