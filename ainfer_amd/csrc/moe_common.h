@@ -308,45 +308,44 @@ __device__ __forceinline__ float rms_inv_finish(double tot, int emin,
   return 1.0f / sqrtf(mean + eps);
 }
 
-// inv = 1 / sqrt(mean + eps) (H <= 4096) with the mean from rms_mean_f over ss in
-// fp64 in k_rmsnorm's order: 256
-// partial sums (partial l over j = l, l + 256, ...), then the pairwise tree
-// st = 128 .. 1.  One wave: lane l holds partials l, l + 64, l + 128,
-// l + 192; st = 128 and 64 stay in the lane, st = 32 .. 1 are shuffles (for
-// the lanes below st, l ^ st = l + st).
+// Partial fp64 sum of squares and packed exponent key of one 16-byte chunk
+// of bf16 (8 elements): squares of bf16 values are exact in fp64 (fma ==
+// add of the square); the key is max(exponent field, 1) << 7 per element,
+// zeros included as exponent 1 (a smaller emin only makes rms_mean_f's
+// exactness test stricter, so it stays a sufficient test).
+typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void sumsq_chunk(const u32x4 &v, double (&p4)[4], u16x2_t &ek) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const uint32_t d = v[q];
+    const double lo = (double)__uint_as_float(d << 16);
+    const double hi = (double)__uint_as_float(d & 0xFFFF0000u);
+    p4[q] = __builtin_fma(lo, lo, p4[q]);
+    p4[q] = __builtin_fma(hi, hi, p4[q]);
+    const u16x2_t e2 = __builtin_bit_cast(u16x2_t, d & 0x7F807F80u);
+    ek = __builtin_elementwise_min(ek, __builtin_elementwise_max(e2, u16x2_t{0x80, 0x80}));
+  }
+}
+__device__ __forceinline__ int ek_emin(u16x2_t ek) { return (int)(min(ek[0], ek[1]) >> 7); }
+
+// inv = 1 / sqrt(mean + eps) of row xr (H <= 4096, H % 8 == 0, 16-byte
+// aligned) with the mean from rms_mean_f: one wave; lane l sums the 16-byte
+// chunks l, l + 64, ... (all loads issued at once), then wave reductions on
+// the DPP path.
 __device__ __forceinline__ float row_rms_inv(const uint16_t *__restrict__ xr, int H, float eps,
                                              int lane) {
-  // loads in two batches of 8 blocks of 256 (H <= 4096), each issued before
-  // its sums; the partial sums still run over m in order
-  double p[4] = {0.0, 0.0, 0.0, 0.0};
-  int emin = 0x7FFF;
+  const int nch = H >> 3;
+  u32x4 v[8];
 #pragma unroll
-  for (int m0 = 0; m0 < 16; m0 += 8) {
-    if (256 * m0 >= H) break;
-    uint16_t v[8][4];
+  for (int c = 0; c < 8; ++c)
+    v[c] = *(const u32x4 *)(xr + 8 * min(lane + 64 * c, nch - 1));
+  double p4[4] = {0.0, 0.0, 0.0, 0.0};
+  u16x2_t ek = {0x7F80, 0x7F80};
 #pragma unroll
-    for (int m = 0; m < 8; ++m)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) v[m][i] = xr[min(256 * (m0 + m) + 64 * i + lane, H - 1)];
-#pragma unroll
-    for (int m = 0; m < 8; ++m)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (256 * (m0 + m) + 64 * i + lane < H) {
-          const double d = (double)bf16_to_f32(v[m][i]);
-          p[i] += d * d;
-          emin = min(emin, bf16_qexp(v[m][i]));
-        }
-      }
-  }
-  p[0] += p[2];
-  p[1] += p[3];
-  p[0] += p[1];
-#pragma unroll
-  for (int st = 32; st >= 1; st >>= 1) p[0] += __shfl_xor(p[0], st, 64);
-  const double tot = __shfl(p[0], 0, 64);
-#pragma unroll
-  for (int st = 32; st >= 1; st >>= 1) emin = min(emin, __shfl_xor(emin, st, 64));
+  for (int c = 0; c < 8; ++c)
+    if (lane + 64 * c < nch) sumsq_chunk(v[c], p4, ek);
+  const double tot = wave_sum_f64((p4[0] + p4[1]) + (p4[2] + p4[3]));
+  const int emin = (int)wave_min_u32((uint32_t)ek_emin(ek));
   return rms_inv_finish(tot, emin, xr, H, eps, lane);
 }
 

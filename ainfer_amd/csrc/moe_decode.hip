@@ -192,29 +192,12 @@ __global__ __launch_bounds__(W * 64) void k_route_decode(RouteDecodeArgs a) {
           // order), four independent fp64 chains per lane
 #pragma unroll
           for (int j = 0; j < RD_TT; ++j) {
-            // squares of bf16 values are exact in fp64 (fma == add of the
-            // square); the exponent minimum runs on packed halves: the key
-            // max(exponent field, 1) << 7 per element, zeros included as
-            // exponent 1 (a smaller emin only makes the exactness test
-            // stricter, so it stays a sufficient test)
-            typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
             double p4[4] = {0.0, 0.0, 0.0, 0.0};
-            u16x2 ek = {0x7F80, 0x7F80};
+            u16x2_t ek = {0x7F80, 0x7F80};
 #pragma unroll
-            for (int b = 0; b < NB; ++b) {
-              if (cb + 64 * b >= nch) continue;
-#pragma unroll
-              for (int q = 0; q < 4; ++q) {
-                const uint32_t d = xv[b][j][q];
-                const double lo = (double)__uint_as_float(d << 16);
-                const double hi = (double)__uint_as_float(d & 0xFFFF0000u);
-                p4[q] = __builtin_fma(lo, lo, p4[q]);
-                p4[q] = __builtin_fma(hi, hi, p4[q]);
-                const u16x2 e2 = __builtin_bit_cast(u16x2, d & 0x7F807F80u);
-                ek = __builtin_elementwise_min(ek, __builtin_elementwise_max(e2, u16x2{0x80, 0x80}));
-              }
-            }
-            int emin = (int)(min(ek[0], ek[1]) >> 7);
+            for (int b = 0; b < NB; ++b)
+              if (cb + 64 * b < nch) sumsq_chunk(xv[b][j], p4, ek);
+            int emin = ek_emin(ek);
             // wave reductions on the DPP path (no LDS round trips on this
             // critical path); one value in every lane
             const double tot = wave_sum_f64((p4[0] + p4[1]) + (p4[2] + p4[3]));

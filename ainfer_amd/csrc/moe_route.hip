@@ -138,11 +138,82 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const uint16_t *__restrict__ x,
   }
 }
 
+// The same for rows of 16-byte chunks (H % 8 == 0, H <= 2048 * NC, rows
+// 16-byte aligned): thread l holds chunks l, l + 256, ... in registers from
+// one load to the store; sums as row_rms_inv (DPP wave reductions, then the
+// four waves' partials); normalized pairs as norm_pair.  Bit-identical to
+// k_rmsnorm (the mean is order-free whenever rms_mean_f accepts it, else
+// re-summed in the reference order).
+template <int NC>
+__global__ __launch_bounds__(256) void k_rmsnorm_v(const uint16_t *__restrict__ x,
+                                                   const uint16_t *__restrict__ w, int mode,
+                                                   float eps, uint16_t *__restrict__ y, int H) {
+  __shared__ double ps[4];
+  __shared__ int pe[4];
+  const int t = blockIdx.x, lid = threadIdx.x, lane = lid & 63, wv = lid >> 6;
+  const uint16_t *xr = x + (size_t)t * H;
+  const int nch = H >> 3;
+  u32x4 xv[NC], nv[NC];
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int c = min(lid + 256 * i, nch - 1);
+    xv[i] = *(const u32x4 *)(xr + 8 * c);
+    nv[i] = w ? *(const u32x4 *)(w + 8 * c) : u32x4{0u, 0u, 0u, 0u};
+  }
+  double p4[4] = {0.0, 0.0, 0.0, 0.0};
+  u16x2_t ek = {0x7F80, 0x7F80};
+#pragma unroll
+  for (int i = 0; i < NC; ++i)
+    if (lid + 256 * i < nch) sumsq_chunk(xv[i], p4, ek);
+  const double wtot = wave_sum_f64((p4[0] + p4[1]) + (p4[2] + p4[3]));
+  const int wemin = (int)wave_min_u32((uint32_t)ek_emin(ek));
+  if (lane == 0) {
+    ps[wv] = wtot;
+    pe[wv] = wemin;
+  }
+  __syncthreads();
+  const double tot = (ps[0] + ps[1]) + (ps[2] + ps[3]);
+  const int emin = min(min(pe[0], pe[1]), min(pe[2], pe[3]));
+  float mean;
+  if (!rms_mean_f(tot, emin, H, mean)) {  // block-uniform; see rms_mean_f
+    __syncthreads();
+    if (lid == 0) ps[0] = row_sumsq_seq(xr, H);
+    __syncthreads();
+    mean = (float)(ps[0] / H);
+  }
+  const float inv = 1.0f / sqrtf(mean + eps);
+  NormIn n;
+  n.w = w;
+  n.mode = mode;
+  n.eps = eps;
+  n.on = 1;
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int c = lid + 256 * i;
+    if (c < nch) {
+      u32x4 o;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) o[q] = norm_pair(xv[i][q], nv[i][q], inv, n);
+      *(u32x4 *)(y + (size_t)t * H + 8 * c) = o;
+    }
+  }
+}
+
 hipError_t launch_rmsnorm(const void *x, const void *w, int mode, float eps, void *y,
                           int T, int H, hipStream_t s) {
   if (T == 0) return hipSuccess;
-  k_rmsnorm<<<T, 256, 0, s>>>((const uint16_t *)x, (const uint16_t *)w, mode, eps,
-                              (uint16_t *)y, H);
+  const bool vec = (H & 7) == 0 && H <= 8192 && ((uintptr_t)x & 15) == 0 &&
+                   ((uintptr_t)y & 15) == 0 && ((uintptr_t)w & 15) == 0;
+  const uint16_t *xp = (const uint16_t *)x, *wp = (const uint16_t *)w;
+  uint16_t *yp = (uint16_t *)y;
+  if (vec && H <= 2048)
+    k_rmsnorm_v<1><<<T, 256, 0, s>>>(xp, wp, mode, eps, yp, H);
+  else if (vec && H <= 4096)
+    k_rmsnorm_v<2><<<T, 256, 0, s>>>(xp, wp, mode, eps, yp, H);
+  else if (vec)
+    k_rmsnorm_v<4><<<T, 256, 0, s>>>(xp, wp, mode, eps, yp, H);
+  else
+    k_rmsnorm<<<T, 256, 0, s>>>(xp, wp, mode, eps, yp, H);
   return hipGetLastError();
 }
 
