@@ -207,27 +207,12 @@ template <int N>
 __device__ __forceinline__ float wave_rms_inv(const u32x4 (&v)[N], const bool (&ok)[N],
                                               const uint16_t *xr, int H, float eps, int lane) {
   double p4[4] = {0.0, 0.0, 0.0, 0.0};
-  int emin = 0x7FFF;
+  u16x2_t ek = {0x7F80, 0x7F80};
 #pragma unroll
-  for (int b = 0; b < N; ++b) {
-    if (!ok[b]) continue;
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const uint16_t u = (uint16_t)(v[b][q] >> (16 * h));
-        const double d = (double)bf16_to_f32(u);
-        p4[q] += d * d;
-        emin = min(emin, bf16_qexp(u));
-      }
-  }
-  double tot = (p4[0] + p4[1]) + (p4[2] + p4[3]);
-#pragma unroll
-  for (int st = 32; st >= 1; st >>= 1) {
-    tot += __shfl_xor(tot, st, 64);
-    emin = min(emin, __shfl_xor(emin, st, 64));
-  }
-  tot = __shfl(tot, 0, 64);  // lanes may round differently: one value
+  for (int b = 0; b < N; ++b)
+    if (ok[b]) sumsq_chunk(v[b], p4, ek);
+  const double tot = wave_sum_f64((p4[0] + p4[1]) + (p4[2] + p4[3]));
+  const int emin = (int)wave_min_u32((uint32_t)ek_emin(ek));
   return rms_inv_finish(tot, emin, xr, H, eps, lane);
 }
 
