@@ -22,6 +22,12 @@ struct Prof {
   int slot = 0, calls = 0;
   double sum_us[NSTAGE];
   int cnt[NSTAGE];
+  // the decode gate/up kernel's own start and end (hipExtLaunchKernel events,
+  // stamped by the dispatch: no barrier packets of their own)
+  hipEvent_t kev[PROF_SLOTS][2];
+  bool kused[PROF_SLOTS];
+  double ksum_us;
+  int kcnt;
 } g_prof;
 
 void prof_flush_slot(int s) {
@@ -39,6 +45,15 @@ void prof_flush_slot(int s) {
     }
     prev = i;
     g_prof.used[s][i] = false;
+  }
+  if (g_prof.kused[s]) {
+    float ms = 0.f;
+    if (hipEventSynchronize(g_prof.kev[s][1]) == hipSuccess &&
+        hipEventElapsedTime(&ms, g_prof.kev[s][0], g_prof.kev[s][1]) == hipSuccess) {
+      g_prof.ksum_us += ms * 1000.0;
+      g_prof.kcnt += 1;
+    }
+    g_prof.kused[s] = false;
   }
 }
 
@@ -63,6 +78,12 @@ struct ProfCall {
   void rec(int i) {
     (void)hipEventRecord(g_prof.ev[s][i], st);
     g_prof.used[s][i] = true;
+  }
+  // the next gate/up expert launch records its own start and end
+  void kernel_events() {
+    if (s < 0) return;
+    set_expert_launch_events(g_prof.kev[s][0], g_prof.kev[s][1]);
+    g_prof.kused[s] = true;
   }
 };
 
@@ -381,6 +402,7 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
       // latency-bound: gate/up, down and combine in one launch (T = 1: the
       // gate/up items in a launch of their own first)
       if (T == 1) {
+        pc->kernel_events();
         HIP_TRY(launch_expert_stream(0, s->scale_dtype, gu, max_tiles_bound(*s, T, DEC_MT), 4,
                                      DEC_RG_GATE_UP, DEC_MT, st));
         pc->end(4);
@@ -392,6 +414,7 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
     } else {
       // bandwidth-bound: three launches whose items hold no waits
       const int mtb = max_tiles_bound(*s, T, DEC_MT);
+      pc->kernel_events();
       HIP_TRY(launch_expert_stream(0, s->scale_dtype, gu, mtb, 4, DEC_RG_GATE_UP, DEC_MT, st));
       pc->end(4);
       HIP_TRY(launch_expert_stream(1, s->scale_dtype, dn, mtb, down_kbw(*s), DEC_RG_DOWN, DEC_MT, st));
@@ -935,15 +958,24 @@ int ainfer_moe_profile_enable(int32_t enable) {
         if (hipEventCreate(&g_prof.ev[i][j]) != hipSuccess) return AINFER_ERR_HIP;
         g_prof.used[i][j] = false;
       }
+    for (int i = 0; i < PROF_SLOTS; ++i) {
+      for (int j = 0; j < 2; ++j)
+        if (hipEventCreate(&g_prof.kev[i][j]) != hipSuccess) return AINFER_ERR_HIP;
+      g_prof.kused[i] = false;
+    }
     g_prof.created = true;
   }
   if (enable) {
     for (int i = 0; i < NSTAGE; ++i) g_prof.sum_us[i] = 0.0, g_prof.cnt[i] = 0;
     g_prof.calls = 0;
     g_prof.slot = 0;
+    g_prof.ksum_us = 0.0;
+    g_prof.kcnt = 0;
     if (g_prof.created)
-      for (int i = 0; i < PROF_SLOTS; ++i)
+      for (int i = 0; i < PROF_SLOTS; ++i) {
         for (int j = 0; j <= NSTAGE; ++j) g_prof.used[i][j] = false;
+        g_prof.kused[i] = false;
+      }
   }
   g_prof.on = enable != 0;
   return AINFER_OK;
@@ -956,6 +988,15 @@ int ainfer_moe_profile_read(float *stage_us, int32_t n_stages, int32_t *n_calls)
   for (int i = 0; i < n_stages && i < NSTAGE; ++i)
     stage_us[i] = g_prof.cnt[i] ? (float)(g_prof.sum_us[i] / g_prof.cnt[i]) : 0.0f;
   if (n_calls) *n_calls = g_prof.calls;
+  return AINFER_OK;
+}
+
+int ainfer_moe_profile_kernel(float *gate_up_us, int32_t *n_launches) {
+  if (!gate_up_us) return AINFER_ERR_NULL;
+  if (g_prof.created)
+    for (int i = 0; i < PROF_SLOTS; ++i) prof_flush_slot(i);
+  *gate_up_us = g_prof.kcnt ? (float)(g_prof.ksum_us / g_prof.kcnt) : 0.0f;
+  if (n_launches) *n_launches = g_prof.kcnt;
   return AINFER_OK;
 }
 

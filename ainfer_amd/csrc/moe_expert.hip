@@ -28,6 +28,8 @@
 //         order).
 // MODE 1: down, epilogue o (bf16) per dispatch position; the combine kernel
 //         sums a token's k + 1 rows in slot order.
+#include <hip/hip_ext.h>
+
 #include "moe_common.h"
 #include "moe_internal.h"
 #include "moe_expert_item.h"
@@ -221,16 +223,27 @@ bool expert_geometry(int mode, int H, int I, int Is, int pref_kbw, int *KBW, int
 }
 
 
+hipEvent_t g_kev_start = nullptr, g_kev_stop = nullptr;
+
 template <int SD, int MODE, int RG>
 void launch_kbw(int kbw, int mt, unsigned grid, int threads, size_t lds, const ExpertArgs &a,
                 hipStream_t s) {
   if (mt == DEC_MT) {
+    auto go = [&](auto kern) {
+      if (g_kev_start) {  // profiling: the kernel's own start and end
+        hipExtLaunchKernelGGL(kern, dim3(grid), dim3(threads), (uint32_t)lds, s, g_kev_start,
+                              g_kev_stop, 0u, a);
+        g_kev_start = g_kev_stop = nullptr;
+      } else {
+        kern<<<grid, threads, lds, s>>>(a);
+      }
+    };
     if (kbw == 1)
-      k_expert_lds<SD, 1, RG, DEC_MT, MODE><<<grid, threads, lds, s>>>(a);
+      go(k_expert_lds<SD, 1, RG, DEC_MT, MODE>);
     else if (kbw == 2)
-      k_expert_lds<SD, 2, RG, DEC_MT, MODE><<<grid, threads, lds, s>>>(a);
+      go(k_expert_lds<SD, 2, RG, DEC_MT, MODE>);
     else
-      k_expert_lds<SD, 4, RG, DEC_MT, MODE><<<grid, threads, lds, s>>>(a);
+      go(k_expert_lds<SD, 4, RG, DEC_MT, MODE>);
     return;
   }
   if (kbw == 1)
@@ -250,6 +263,11 @@ void launch_rg(int rg, int kbw, int mt, unsigned grid, int threads, size_t lds,
     launch_kbw<SD, MODE, 2>(kbw, mt, grid, threads, lds, a, s);
   else
     launch_kbw<SD, MODE, 4>(kbw, mt, grid, threads, lds, a, s);
+}
+
+void set_expert_launch_events(hipEvent_t start, hipEvent_t stop) {
+  g_kev_start = start;
+  g_kev_stop = stop;
 }
 
 hipError_t launch_expert_stream(int mode, int scale_dtype, ExpertArgs a, int max_tiles,

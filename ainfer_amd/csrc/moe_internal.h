@@ -138,6 +138,9 @@ bool expert_geometry(int mode, int H, int I, int Is, int pref_kbw, int *KBW, int
 #endif
 // rg: 16-row groups per wave (1, 2 or 4) sharing one load of the token rows;
 // mt: tokens per tile the dispatch produced (DEC_MT: A staged in LDS, or SMALL_MT)
+// The next decode gate/up launch of launch_expert_stream (the DEC_MT items)
+// goes through hipExtLaunchKernel with these start/stop events (one shot).
+void set_expert_launch_events(hipEvent_t start, hipEvent_t stop);
 hipError_t launch_expert_stream(int mode, int scale_dtype, ExpertArgs a, int max_tiles,
                                 int pref_kbw, int rg, int mt, hipStream_t s);
 

@@ -281,6 +281,7 @@ def run_c4(steps, tokens=(1, 8), warmup=3, keep_layer0=False, stack=True):
             step(s)
         torch.cuda.synchronize()
         st, _ = L.profile_read()
+        k_us, _ = L.profile_kernel()  # the gate/up kernel's own duration
         L.profile_enable(False)
         Ul = U / len(layers)
         nbytes = sum(algorithmic_bytes(cfg, T, 0) for _ in layers) + round(U) * cfg.expert_bytes()
@@ -289,7 +290,8 @@ def run_c4(steps, tokens=(1, 8), warmup=3, keep_layer0=False, stack=True):
         if st["gate_up"] > 0:
             dom = {"kernel": "k_expert_lds<fp16, gate/up> (gate/up + SiLU of the routed and "
                              "shared experts)", "file": "k_expert_gate_up",
-                   "alg_bytes": gateup_bytes(cfg, Ul), "us": st["gate_up"]}
+                   "alg_bytes": gateup_bytes(cfg, Ul), "us": k_us if k_us > 0 else st["gate_up"],
+                   "us_stage_events": st["gate_up"]}
         else:
             dom = {"kernel": "k_experts_decode (gate/up + down + combine)",
                    "file": "k_experts_decode",

@@ -377,6 +377,13 @@ int ainfer_moe_fill(int32_t kind, uint64_t seed, float std_, size_t n,
 #define AINFER_MOE_N_STAGES 7
 int ainfer_moe_profile_enable(int32_t enable);
 int ainfer_moe_profile_read(float *stage_us, int32_t n_stages, int32_t *n_calls);
+/* Mean duration of the decode gate/up kernel itself over the calls since
+ * enable (T <= 16 paths with a gate/up launch of its own): while profiling,
+ * that launch goes through hipExtLaunchKernel with start/stop events stamped
+ * by the dispatch, so the figure carries no event-packet overhead and is
+ * what a kernel trace reports.  No counterpart in the reference: a
+ * measurement aid for roofline figures. */
+int ainfer_moe_profile_kernel(float *gate_up_us, int32_t *n_launches);
 
 #ifdef __cplusplus
 }
