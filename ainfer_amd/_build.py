@@ -21,17 +21,21 @@ FLAGS = [
 ]
 
 
-def build_library(verbose: bool = False) -> Path:
-    """Compile every HIP source into ainfer_amd/libainfer_moe.so."""
+def build_library(verbose: bool = False, out: Path = None) -> Path:
+    """Compile every HIP source into ainfer_amd/libainfer_moe.so (or `out`).
+    AINFER_HIPFLAGS adds compiler flags, e.g. "-DAINFER_GEMM_TRACE" for the
+    prefill GEMM's per-item timestamps (a diagnostic build)."""
     from concurrent.futures import ThreadPoolExecutor
     objs = [str(CSRC / (src + ".o")) for src in SOURCES]
-    cmds = [[HIPCC, *[f for f in FLAGS if f != "-shared"], "-c", str(CSRC / src), "-o", obj]
+    extra = os.environ.get("AINFER_HIPFLAGS", "").split()
+    cmds = [[HIPCC, *[f for f in FLAGS if f != "-shared"], *extra, "-c", str(CSRC / src), "-o", obj]
             for src, obj in zip(SOURCES, objs)]
     jobs = max(1, min(len(cmds), (os.cpu_count() or 1) // 2, 8))
     with ThreadPoolExecutor(jobs) as pool:
         list(pool.map(lambda c: _run(c, verbose), cmds))
-    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(LIB), *objs], verbose)
-    return LIB
+    lib = Path(out) if out else LIB
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(lib), *objs], verbose)
+    return lib
 
 
 def _run(cmd, verbose):
@@ -44,4 +48,5 @@ def _run(cmd, verbose):
 
 
 if __name__ == "__main__":
-    print(build_library(verbose=True))
+    import sys
+    print(build_library(verbose=True, out=Path(sys.argv[1]).resolve() if len(sys.argv) > 1 else None))

@@ -32,6 +32,19 @@
 #include "moe_common.h"
 #include "moe_internal.h"
 
+#ifdef AINFER_GEMM_TRACE
+// diagnostic builds only: per item (MODE * 16384 + item), the shader clock
+// (s_memtime) at the item's start, before its main loop, after the loop's
+// last barrier, and after its epilogue
+__device__ unsigned long long g_gtrace[2 * 16384 * 4];
+#define GTRACE(V) V
+extern "C" int ainfer_debug_gemm_trace(void *host) {
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_gtrace), sizeof(g_gtrace)) == hipSuccess ? 0 : -1;
+}
+#else
+#define GTRACE(V)
+#endif
+
 namespace {
 
 constexpr int BM = 128;  // tokens per tile
@@ -163,6 +176,7 @@ __device__ __forceinline__ void gemm_item(const GemmArgs &a, const int lb, const
   uint16_t *sc_lds = (uint16_t *)(lds + STAGES * STAGE);
   float *xs_lds = (float *)(lds + STAGES * STAGE + ((BN * G * 2 + 15) & ~15));
 
+  GTRACE(const unsigned long long t0 = __builtin_amdgcn_s_memtime());
   const int tid = tid_opaque();  // per item: nothing lane-dependent is hoisted across items
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
@@ -416,6 +430,7 @@ __device__ __forceinline__ void gemm_item(const GemmArgs &a, const int lb, const
       for (int ms = 0; ms < NMS; ++ms) tot[ms][ns] += sprev[ns] * acc[ms][ns];
   };
   // token subtiles of this wave holding tokens of the tile (wave-uniform)
+  GTRACE(const unsigned long long t1 = __builtin_amdgcn_s_memtime());
   const int nms = __builtin_amdgcn_readfirstlane(max(0, min(4, (mcnt - wm * 64 + 15) >> 4)));
   if (nms > 2)
     main_loop(std::integral_constant<int, 4>());
@@ -426,6 +441,12 @@ __device__ __forceinline__ void gemm_item(const GemmArgs &a, const int lb, const
   wait_vm<0>();  // no DMA into the ring remains in flight
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   block_barrier();  // every wave's last read of the ring precedes the staging below
+  GTRACE(if (tid == 0 && lb < 16384) {
+    const int o = (MODE * 16384 + lb) * 4;
+    g_gtrace[o] = t0;
+    g_gtrace[o + 1] = t1;
+    g_gtrace[o + 2] = __builtin_amdgcn_s_memtime();
+  });
 
   // ---- epilogue -------------------------------------------------------
   // lane (q, m16) of tile (ms, ns) holds rows wm*64 + ms*16 + 4q + r, column
@@ -572,6 +593,8 @@ __global__ __launch_bounds__(128 * WN) void k_expert_gemm(GemmArgs a) {
     gemm_item<SD, MODE, WN, STAGES_>(a, lb, t);
     t = tn;
     __syncthreads();  // the epilogue's LDS reads precede the next item's DMA
+    GTRACE(if (threadIdx.x == 0 && lb < 16384) g_gtrace[(MODE * 16384 + lb) * 4 + 3] =
+               __builtin_amdgcn_s_memtime());
   }
 }
 
