@@ -2,6 +2,15 @@
 
   AINFER_HIPFLAGS=-DAINFER_GEMM_TRACE python -m ainfer_amd._build /tmp/gemm_trace.so
   python -m ainfer_amd.diag gemm-phases /tmp/gemm_trace.so
+  AINFER_HIPFLAGS=-DAINFER_DECODE_TRACE python -m ainfer_amd._build /tmp/decode_trace.so
+  python -m ainfer_amd.diag decode-phases /tmp/decode_trace.so
+
+decode-phases runs 8 blocks of config 4 at T = 1 (block_forward, three steps)
+and prints the last block's timeline in microseconds from the routing
+kernel's first workgroup (s_memrealtime stamps per workgroup, moe_decode.hip
+and moe_expert_item.h): the router waves' RMSNorm and dot, the selection's
+poll, top-k and dispatch, and the gate/up and down items' start, weight
+arrival and stores.
 
 gemm-phases runs the c2 prefill layer (T = 4096, Zipf routing) a few times and
 prints, per grouped-GEMM kind, the mean shader-clock span of an item's
@@ -45,9 +54,58 @@ def gemm_phases(lib_path, steps=3):
     return out
 
 
+def decode_phases(lib_path, n_layers=8):
+    import numpy as np
+    from . import _lib as L
+    L.LIB_PATH = Path(lib_path).resolve()
+    import torch
+    from .moe import MoeLayer, make_input
+    from .synthetic import CONFIGS
+    cfg = CONFIGS["c4"]
+    layers = [MoeLayer(cfg, layer=i) for i in range(n_layers)]
+    T = 1
+    ws = layers[0].workspace(T)
+    x = make_input(cfg, T, tag=5000) * 4
+    y = torch.empty_like(x)
+    for _ in range(3):
+        layers[0].block_forward(x, y, ws)
+        for ly in layers[1:]:
+            ly.block_forward(y, y, ws)
+    torch.cuda.synchronize()
+    lib = L.lib()
+    tr = np.zeros((2, 1 << 15, 5), dtype=np.uint64)
+    ld = np.zeros((2, 1 << 14, 3), dtype=np.uint64)
+    if lib.ainfer_debug_trace(tr.ctypes.data_as(C.c_void_p)) != 0 or \
+            lib.ainfer_debug_land_expert(ld.ctypes.data_as(C.c_void_p)) != 0:
+        raise RuntimeError("not a -DAINFER_DECODE_TRACE build")
+    r = tr[0].astype(np.int64)
+    nr = int((r[:, 0] > 0).sum())  # router units, the selection (nr - 2), the x copy
+    t0 = r[:nr, 0].min()
+    us = lambda v: (v - t0) / 100.0
+    rr = r[:nr - 2]
+    sel = r[nr - 2]
+    print(f"router waves: RMSNorm done {us(np.median(rr[:, 2])):.2f} (max {us(rr[:, 2].max()):.2f}), "
+          f"dot done {us(np.median(rr[:, 3])):.2f}, logits stored {us(np.median(rr[:, 1])):.2f} "
+          f"(max {us(rr[:, 1].max()):.2f})")
+    print(f"selection: slots seen {us(sel[4]):.2f}, top-k {us(sel[1]):.2f}, weights {us(sel[2]):.2f}, "
+          f"dispatch {us(sel[3]):.2f}")
+    g = ld[0].astype(np.int64)
+    g = g[g[:, 0] > 0]
+    if len(g):
+        print(f"gate/up items ({len(g)}): start {us(np.median(g[:, 0])):.2f}, weights landed "
+              f"{us(np.median(g[:, 1])):.2f} (max {us(g[:, 1].max()):.2f}), written max {us(g[:, 2].max()):.2f}")
+    d = tr[1].astype(np.int64)
+    d = d[(d[:, 0] > 0) & (d[:, 4] == 0)]
+    if len(d):
+        print(f"down items ({len(d)}): start {us(np.median(d[:, 0])):.2f}, stores max {us(d[:, 2].max()):.2f}, "
+              f"last arrival {us(d[:, 3].max()):.2f}")
+
+
 if __name__ == "__main__":
     if len(sys.argv) >= 3 and sys.argv[1] == "gemm-phases":
         gemm_phases(sys.argv[2])
+    elif len(sys.argv) >= 3 and sys.argv[1] == "decode-phases":
+        decode_phases(sys.argv[2])
     else:
         print(__doc__)
         sys.exit(2)
