@@ -216,6 +216,103 @@ __global__ __launch_bounds__(GV_WAVES * 64) void k_int4_gemv_i8(
   if (m < M && t < T) y[(size_t)t * M + m] = acc;
 }
 
+// ---- T = 1: the GEMV proper -------------------------------------------------
+// One token, so no MFMA: a wave owns GV1_RW consecutive rows, lane l the
+// 16-byte chunks l, l + 64, ... of each (one load instruction = 1 KB of one
+// row, the wide pattern that streams fastest).  Chunk c is quarter c % 4 of
+// group c / 4, so the four lanes of a quad hold one group: the exact int32
+// dot of its nibbles and int8 activations is four v_dot4_i32_i8 per lane
+// (q + 8 in [0, 15] against x, less 8 * sum(x)) and a quad sum.  The terms
+// float(gs) * s * sq go to LDS and lane r adds row r's in group order.
+#ifndef GV1_RW
+#define GV1_RW 4  // rows per wave
+#endif
+constexpr int GV1_WAVES = 4;
+
+template <int SD, int NC>
+__global__ __launch_bounds__(GV1_WAVES * 64) void k_int4_gemv_i8_t1(
+    const uint8_t *__restrict__ P, const uint16_t *__restrict__ S, const int8_t *__restrict__ xq,
+    const float *__restrict__ sq, int M, int K, float *__restrict__ y) {
+  __shared__ float term[GV1_WAVES][GV1_RW][NC * 16];
+  const int tx = tid_opaque();
+  const int wave = __builtin_amdgcn_readfirstlane(tx >> 6), lane = tx & 63;
+  const int C = K >> 5, G = K >> 7;  // 16-byte chunks and groups per row
+  const int m0 = (blockIdx.x * GV1_WAVES + wave) * GV1_RW;
+  const size_t rowb = (size_t)K / 2;
+  // weights first: every row's chunks in flight at once
+  u32x4 wv[GV1_RW][NC];
+#pragma unroll
+  for (int r = 0; r < GV1_RW; ++r) {
+    const uint8_t *wp = P + (size_t)min(m0 + r, M - 1) * rowb;
+#pragma unroll
+    for (int i = 0; i < NC; ++i)
+      wv[r][i] = __builtin_nontemporal_load((const u32x4 *)(wp + (size_t)min(lane + 64 * i, C - 1) * 16));
+  }
+  // activations of this lane's chunks (32 bytes each, the same for every
+  // row), the group scales of its quad's groups, and the weight scales
+  u32x4 xa[NC], xb[NC];
+  float sqv[NC];
+  uint16_t sc[GV1_RW][NC];
+  const int qg = lane >> 2;  // group of chunk lane + 64 i is qg + 16 i
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int ch = min(lane + 64 * i, C - 1), g = min(qg + 16 * i, G - 1);
+    xa[i] = *(const u32x4 *)(xq + (size_t)ch * 32);
+    xb[i] = *(const u32x4 *)(xq + (size_t)ch * 32 + 16);
+    sqv[i] = sq[g];
+#pragma unroll
+    for (int r = 0; r < GV1_RW; ++r) sc[r][i] = S[(size_t)min(m0 + r, M - 1) * G + g];
+  }
+  // x in the nibbles' order: the low nibbles of weight dword d are elements
+  // 8 d + {0, 2, 4, 6}, the high ones 8 d + {1, 3, 5, 7}
+  int xe[NC][4], xo[NC][4], sx[NC];
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const uint32_t b[8] = {xa[i][0], xa[i][1], xa[i][2], xa[i][3],
+                           xb[i][0], xb[i][1], xb[i][2], xb[i][3]};
+    int s = 0;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      xe[i][d] = (int)__builtin_amdgcn_perm(b[2 * d + 1], b[2 * d], 0x06040200u);
+      xo[i][d] = (int)__builtin_amdgcn_perm(b[2 * d + 1], b[2 * d], 0x07050301u);
+      s = __builtin_amdgcn_sdot4(xe[i][d], 0x01010101, s, false);
+      s = __builtin_amdgcn_sdot4(xo[i][d], 0x01010101, s, false);
+    }
+    sx[i] = 8 * s;
+  }
+#pragma unroll
+  for (int r = 0; r < GV1_RW; ++r) {
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      int d = -sx[i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t u = wv[r][i][j] ^ 0x88888888u;  // nibble q -> q + 8
+        d = __builtin_amdgcn_sdot4((int)(u & 0x0F0F0F0Fu), xe[i][j], d, false);
+        d = __builtin_amdgcn_sdot4((int)((u >> 4) & 0x0F0F0F0Fu), xo[i][j], d, false);
+      }
+      if (lane + 64 * i >= C) d = 0;
+      d += __builtin_amdgcn_mov_dpp(d, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+      d += __builtin_amdgcn_mov_dpp(d, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+      const int g = qg + 16 * i;
+      if ((lane & 3) == 0 && g < G) {
+#pragma clang fp contract(off)
+        term[wave][r][g] = (float)d * scale_to_f32<SD>(sc[r][i]) * sqv[i];  // unfused
+      }
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  if (lane < GV1_RW && m0 + lane < M) {
+    float acc = 0.0f;
+    {
+#pragma clang fp contract(off)
+      for (int g = 0; g < G; ++g) acc = acc + term[wave][lane][g];  // group order
+    }
+    y[m0 + lane] = acc;
+  }
+}
+
 // ---- the MoE layer in W4A8 (AINFER_PRECISION_W4A8) --------------------------
 // The decoder MLP of tools/decode/decode_l0.cpp:663-674 per (token, expert):
 // xq -> Int4Gemv gate, Int4Gemv up -> SiluMul -> quantize -> Int4Gemv down,
@@ -337,6 +434,25 @@ hipError_t launch_combine_f32(const float *o, const int32_t *inv, const float *w
 
 hipError_t launch_int4_gemv_i8(const uint8_t *P, const void *S, int scale_dtype, const int8_t *xq,
                                const float *sq, int M, int K, int T, float *y, hipStream_t s) {
+  if (T == 1 && K % 128 == 0 && K <= 8192) {
+    const int nc = (K / 32 + 63) / 64;
+    const unsigned g1 = (unsigned)((M + GV1_WAVES * GV1_RW - 1) / (GV1_WAVES * GV1_RW));
+    auto go1 = [&](auto sd_c, auto nc_c) {
+      k_int4_gemv_i8_t1<decltype(sd_c)::value, decltype(nc_c)::value>
+          <<<g1, GV1_WAVES * 64, 0, s>>>(P, (const uint16_t *)S, xq, sq, M, K, y);
+    };
+    auto go_nc = [&](auto sd_c) {
+      if (nc == 1) go1(sd_c, std::integral_constant<int, 1>());
+      else if (nc == 2) go1(sd_c, std::integral_constant<int, 2>());
+      else if (nc == 3) go1(sd_c, std::integral_constant<int, 3>());
+      else go1(sd_c, std::integral_constant<int, 4>());
+    };
+    if (scale_dtype == AINFER_SCALE_FP16)
+      go_nc(std::integral_constant<int, AINFER_SCALE_FP16>());
+    else
+      go_nc(std::integral_constant<int, AINFER_SCALE_BF16>());
+    return hipGetLastError();
+  }
   const dim3 grid((M + 15) / 16, (T + 15) / 16);
   const size_t stg = (size_t)16 * (K / 128) * 6;  // staged scales
   const bool st = stg <= 48 * 1024;

@@ -67,7 +67,11 @@ def test_act_quant_bit_exact(torch, oracle, T, K):
 
 
 @pytest.mark.parametrize("M,K,T,sdt", [(16, 128, 1, 0), (100, 1024, 5, 1), (512, 2048, 16, 1),
-                                       (2048, 512, 17, 0), (77, 384, 40, 0)])
+                                       (2048, 512, 17, 0), (77, 384, 40, 0),
+                                       # T = 1: 1 to 4 chunks per lane, partial last
+                                       # chunk round, rows past a wave's end
+                                       (101, 1024, 1, 1), (333, 5120, 1, 1), (70, 8192, 1, 0),
+                                       (50, 2176, 1, 0), (19, 8320, 1, 1)])
 def test_int4_gemv_i8_bit_exact(torch, oracle, M, K, T, sdt):
     print(f"[case] gemv_i8 M={M} K={K} T={T} sdt={sdt}", flush=True)
     rng = np.random.default_rng(M + K + T)
