@@ -225,9 +225,11 @@ __global__ __launch_bounds__(GV_WAVES * 64) void k_int4_gemv_i8(
 // (q + 8 in [0, 15] against x, less 8 * sum(x)) and a quad sum.  The terms
 // float(gs) * s * sq go to LDS and lane r adds row r's in group order.
 #ifndef GV1_RW
-#define GV1_RW 4  // rows per wave
+#define GV1_RW 2  // rows per wave (2: 10.0 us at 17408 x 5120; 1: 12.1, 4: 10.9, 8: 13.0)
 #endif
-constexpr int GV1_WAVES = 4;
+#ifndef GV1_WAVES
+#define GV1_WAVES 4  // waves per block
+#endif
 
 template <int SD, int NC>
 __global__ __launch_bounds__(GV1_WAVES * 64) void k_int4_gemv_i8_t1(
