@@ -458,3 +458,52 @@ def test_forward_parity_random_shapes(torch, oracle, H, E, k, I, Is, T):
     check_close(to_np(y), hl.forward(to_np(x), T), f"random {H},{E},{k},{I},{Is} T={T}")
     assert layer.workspace_check(ws) == 0
     del layer
+
+
+def _heavy_tailed(torch, T, H, seed):
+    """Student-t (2 degrees of freedom: infinite variance) activations with a
+    few outliers 200x the bulk per row, rounded to bf16: the inputs the
+    Irwin-Hall synthetic fill never produces."""
+    rng = np.random.default_rng(seed)
+    x = rng.standard_t(2.0, size=(T, H)).astype(np.float32)
+    for t in range(T):
+        cols = rng.choice(H, size=3, replace=False)
+        x[t, cols] = rng.choice([-200.0, 200.0], size=3) * np.abs(rng.standard_normal(3)) + 1.0
+    return torch.from_numpy(x).to(torch.bfloat16).cuda()
+
+
+@pytest.mark.parametrize("name,T", [("c1", 1), ("c1", 4), ("c1", 16), ("c1", 300), ("c3", 64)])
+def test_forward_parity_heavy_tailed_activations(torch, oracle, name, T):
+    """Heavy-tailed activations through every decode form and the prefill
+    GEMM: routing bit-exact, outputs within the layer tolerance."""
+    print(f"[case] heavy-tailed forward {name} T={T}", flush=True)
+    layer = get_layer(torch, name)
+    x = _heavy_tailed(torch, T, layer.cfg.hidden, 1000 + T)
+    _route_check(torch, oracle, layer, x, f"heavy {name} T={T}")
+    ws = layer.workspace(T)
+    y = torch.full((T, layer.cfg.hidden), float("nan"), dtype=torch.bfloat16, device="cuda")
+    layer.forward(x, y, ws)
+    torch.cuda.synchronize()
+    assert not torch.isnan(y).any()
+    ref = host_copy(oracle, layer).forward(to_np(x), T)
+    check_close(to_np(y), ref, f"heavy {name} T={T}")
+
+
+def test_block_forward_heavy_tailed_residual(torch, oracle):
+    """The block (RMSNorm -> layer -> residual) on a heavy-tailed residual
+    stream, both the fused RMSNorm (T <= 4) and the separate kernel."""
+    from ainfer_amd import _lib as L
+    layer = get_layer(torch, "c1")
+    ws = layer.workspace(16)
+    g = torch.Generator().manual_seed(9)
+    nw = (torch.randn(layer.cfg.hidden, generator=g) * 0.5 + 1.0).to(torch.bfloat16).cuda()
+    hl = host_copy(oracle, layer)
+    for T in (1, 4, 16):
+        print(f"[case] heavy-tailed block T={T}", flush=True)
+        x = _heavy_tailed(torch, T, layer.cfg.hidden, 2000 + T)
+        out = torch.empty_like(x)
+        layer.block_forward(x, out, ws, norm_w=nw, norm_mode=L.NORM_PLAIN)
+        torch.cuda.synchronize()
+        want = hl.block_forward(to_np(x), T, norm_w=to_np(nw), mode=L.NORM_PLAIN)
+        check_close(to_np(out), oracle.bf16_to_f32(want), f"heavy block T={T}")
+    assert layer.workspace_check(ws) == 0
