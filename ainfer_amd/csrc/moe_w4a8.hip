@@ -231,21 +231,23 @@ __global__ __launch_bounds__(GV_WAVES * 64) void k_int4_gemv_i8(
 #define GV1_WAVES 4  // waves per block
 #endif
 
-template <int SD, int NC>
-__global__ __launch_bounds__(GV1_WAVES * 64) void k_int4_gemv_i8_t1(
-    const uint8_t *__restrict__ P, const uint16_t *__restrict__ S, const int8_t *__restrict__ xq,
-    const float *__restrict__ sq, int M, int K, float *__restrict__ y) {
-  __shared__ float term[GV1_WAVES][GV1_RW][NC * 16];
-  const int tx = tid_opaque();
-  const int wave = __builtin_amdgcn_readfirstlane(tx >> 6), lane = tx & 63;
+// Rows [m0, m0 + GV1_RW) of NMAT matrices P[j] / S[j] (M rows, K columns)
+// against one activation row xq / sq.  Lane j * GV1_RW + r returns row
+// m0 + r of matrix j (other lanes 0).  term: this wave's LDS, NMAT * GV1_RW
+// rows of NC * 16 floats.  Every weight load of every matrix is issued
+// before any is used.
+template <int SD, int NC, int NMAT>
+__device__ __forceinline__ float gemv1_rows(const uint8_t *const (&P)[NMAT],
+                                            const uint16_t *const (&S)[NMAT], int m0, int M,
+                                            int K, const int8_t *__restrict__ xq,
+                                            const float *__restrict__ sq, float *term, int lane) {
+  constexpr int R = NMAT * GV1_RW;
   const int C = K >> 5, G = K >> 7;  // 16-byte chunks and groups per row
-  const int m0 = (blockIdx.x * GV1_WAVES + wave) * GV1_RW;
   const size_t rowb = (size_t)K / 2;
-  // weights first: every row's chunks in flight at once
-  u32x4 wv[GV1_RW][NC];
+  u32x4 wv[R][NC];
 #pragma unroll
-  for (int r = 0; r < GV1_RW; ++r) {
-    const uint8_t *wp = P + (size_t)min(m0 + r, M - 1) * rowb;
+  for (int r = 0; r < R; ++r) {
+    const uint8_t *wp = P[r / GV1_RW] + (size_t)min(m0 + r % GV1_RW, M - 1) * rowb;
 #pragma unroll
     for (int i = 0; i < NC; ++i)
       wv[r][i] = __builtin_nontemporal_load((const u32x4 *)(wp + (size_t)min(lane + 64 * i, C - 1) * 16));
@@ -254,7 +256,7 @@ __global__ __launch_bounds__(GV1_WAVES * 64) void k_int4_gemv_i8_t1(
   // row), the group scales of its quad's groups, and the weight scales
   u32x4 xa[NC], xb[NC];
   float sqv[NC];
-  uint16_t sc[GV1_RW][NC];
+  uint16_t sc[R][NC];
   const int qg = lane >> 2;  // group of chunk lane + 64 i is qg + 16 i
 #pragma unroll
   for (int i = 0; i < NC; ++i) {
@@ -263,7 +265,8 @@ __global__ __launch_bounds__(GV1_WAVES * 64) void k_int4_gemv_i8_t1(
     xb[i] = *(const u32x4 *)(xq + (size_t)ch * 32 + 16);
     sqv[i] = sq[g];
 #pragma unroll
-    for (int r = 0; r < GV1_RW; ++r) sc[r][i] = S[(size_t)min(m0 + r, M - 1) * G + g];
+    for (int r = 0; r < R; ++r)
+      sc[r][i] = S[r / GV1_RW][(size_t)min(m0 + r % GV1_RW, M - 1) * G + g];
   }
   // x in the nibbles' order: the low nibbles of weight dword d are elements
   // 8 d + {0, 2, 4, 6}, the high ones 8 d + {1, 3, 5, 7}
@@ -283,7 +286,7 @@ __global__ __launch_bounds__(GV1_WAVES * 64) void k_int4_gemv_i8_t1(
     sx[i] = 8 * s;
   }
 #pragma unroll
-  for (int r = 0; r < GV1_RW; ++r) {
+  for (int r = 0; r < R; ++r) {
 #pragma unroll
     for (int i = 0; i < NC; ++i) {
       int d = -sx[i];
@@ -299,19 +302,74 @@ __global__ __launch_bounds__(GV1_WAVES * 64) void k_int4_gemv_i8_t1(
       const int g = qg + 16 * i;
       if ((lane & 3) == 0 && g < G) {
 #pragma clang fp contract(off)
-        term[wave][r][g] = (float)d * scale_to_f32<SD>(sc[r][i]) * sqv[i];  // unfused
+        term[r * NC * 16 + g] = (float)d * scale_to_f32<SD>(sc[r][i]) * sqv[i];  // unfused
       }
     }
   }
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-  if (lane < GV1_RW && m0 + lane < M) {
-    float acc = 0.0f;
-    {
+  float acc = 0.0f;
+  if (lane < R) {
 #pragma clang fp contract(off)
-      for (int g = 0; g < G; ++g) acc = acc + term[wave][lane][g];  // group order
-    }
-    y[m0 + lane] = acc;
+    for (int g = 0; g < G; ++g) acc = acc + term[lane * NC * 16 + g];  // group order
+  }
+  return acc;
+}
+
+template <int SD, int NC>
+__global__ __launch_bounds__(GV1_WAVES * 64) void k_int4_gemv_i8_t1(
+    const uint8_t *__restrict__ P, const uint16_t *__restrict__ S, const int8_t *__restrict__ xq,
+    const float *__restrict__ sq, int M, int K, float *__restrict__ y) {
+  __shared__ float term[GV1_WAVES][GV1_RW * NC * 16];
+  const int tx = tid_opaque();
+  const int wave = __builtin_amdgcn_readfirstlane(tx >> 6), lane = tx & 63;
+  const int m0 = (blockIdx.x * GV1_WAVES + wave) * GV1_RW;
+  const uint8_t *const Pm[1] = {P};
+  const uint16_t *const Sm[1] = {S};
+  const float acc = gemv1_rows<SD, NC, 1>(Pm, Sm, m0, M, K, xq, sq, term[wave], lane);
+  if (lane < GV1_RW && m0 + lane < M) y[m0 + lane] = acc;
+}
+
+// The layer's expert GEMVs at T = 1 (every dispatch tile holds one token):
+// grid (ceil(N / (GV1_WAVES * GV1_RW)), tiles), the rows of gemv1_rows.
+//   MODE 0: act[pos][n] = silu(gate . x) * (up . x), fp32 (SiluMul,
+//           tools/cmdlist/kernels.cpp:29-37);
+//   MODE 1: o[pos][h] = down . act.
+template <int SD, int MODE, int NC>
+__global__ __launch_bounds__(GV1_WAVES * 64) void k_w4a8_expert_t1(W4A8Args a) {
+  constexpr int NMAT = MODE == 0 ? 2 : 1;
+  __shared__ float term[GV1_WAVES][NMAT * GV1_RW * NC * 16];
+  if ((int)blockIdx.y >= *a.n_tiles) return;
+  const int4 t = a.tiles[blockIdx.y];
+  const int e = t.x, pos0 = t.y;
+  const bool shared = e == a.E;
+  const int N = MODE == 0 ? (shared ? a.Is : a.I) : a.H;
+  const int K = MODE == 0 ? a.H : (shared ? a.Is : a.I);
+  const int tx = tid_opaque();
+  const int wave = __builtin_amdgcn_readfirstlane(tx >> 6), lane = tx & 63;
+  const int m0 = (blockIdx.x * GV1_WAVES + wave) * GV1_RW;
+  if (m0 >= N) return;
+  const size_t rowb = (size_t)K / 2, G = K / 128;
+  if constexpr (MODE == 0) {
+    const int tok = shared ? pos0 : a.ptok[pos0];
+    const uint8_t *const Pm[2] = {shared ? a.ws0 : a.w0 + (size_t)e * N * rowb,
+                                  shared ? a.ws1 : a.w1 + (size_t)e * N * rowb};
+    const uint16_t *const Sm[2] = {shared ? a.ss0 : a.s0 + (size_t)e * N * G,
+                                   shared ? a.ss1 : a.s1 + (size_t)e * N * G};
+    const float v = gemv1_rows<SD, NC, 2>(Pm, Sm, m0, N, K, a.xq + (size_t)tok * K,
+                                          a.xs + (size_t)tok * G, term[wave], lane);
+    // lane r: gate row m0 + r; lane GV1_RW + r: up row m0 + r
+    const float u = __shfl(v, lane + GV1_RW, 64);
+    if (lane < GV1_RW && m0 + lane < N)
+      (shared ? a.act_s : a.act)[(size_t)pos0 * N + m0 + lane] = v / (1.0f + expf(-v)) * u;
+  } else {
+    const uint8_t *const Pm[1] = {shared ? a.ws0 : a.w0 + (size_t)e * N * rowb};
+    const uint16_t *const Sm[1] = {shared ? a.ss0 : a.s0 + (size_t)e * N * G};
+    const int8_t *aq = (shared ? a.aq_s : a.aq) + (size_t)pos0 * K;
+    const float *as = (shared ? a.as_s : a.as) + (size_t)pos0 * G;
+    const float v = gemv1_rows<SD, NC, 1>(Pm, Sm, m0, N, K, aq, as, term[wave], lane);
+    if (lane < GV1_RW && m0 + lane < N)
+      a.o[(size_t)((shared ? a.T * a.k : 0) + pos0) * N + m0 + lane] = v;
   }
 }
 
@@ -409,6 +467,30 @@ hipError_t launch_w4a8_expert(int mode, int scale_dtype, const W4A8Args &a, int 
   if (max_tiles <= 0) return hipSuccess;
   const int N = mode == 0 ? (a.I > a.Is ? a.I : a.Is) : a.H;
   const int K = mode == 0 ? a.H : (a.I > a.Is ? a.I : a.Is);
+  const int Kmin = mode == 0 ? a.H : (a.Is > 0 && a.Is < a.I ? a.Is : a.I);
+  if (a.T == 1 && K <= 8192 && Kmin % 128 == 0) {
+    // one token per tile: the wide one-token rows (gemv1_rows)
+    const int nc = (K / 32 + 63) / 64;
+    const dim3 g1((N + GV1_WAVES * GV1_RW - 1) / (GV1_WAVES * GV1_RW), max_tiles);
+    auto go1 = [&](auto sd_c, auto nc_c) {
+      constexpr int SDc = decltype(sd_c)::value, NCc = decltype(nc_c)::value;
+      if (mode == 0)
+        k_w4a8_expert_t1<SDc, 0, NCc><<<g1, GV1_WAVES * 64, 0, s>>>(a);
+      else
+        k_w4a8_expert_t1<SDc, 1, NCc><<<g1, GV1_WAVES * 64, 0, s>>>(a);
+    };
+    auto go_nc = [&](auto sd_c) {
+      if (nc == 1) go1(sd_c, std::integral_constant<int, 1>());
+      else if (nc == 2) go1(sd_c, std::integral_constant<int, 2>());
+      else if (nc == 3) go1(sd_c, std::integral_constant<int, 3>());
+      else go1(sd_c, std::integral_constant<int, 4>());
+    };
+    if (scale_dtype == AINFER_SCALE_FP16)
+      go_nc(std::integral_constant<int, AINFER_SCALE_FP16>());
+    else
+      go_nc(std::integral_constant<int, AINFER_SCALE_BF16>());
+    return hipGetLastError();
+  }
   const dim3 grid((N + 15) / 16, max_tiles);
   const size_t stg = (size_t)16 * (K / 128) * 6;  // staged scales
   auto go = [&](auto sd_c) {

@@ -313,6 +313,29 @@ def run_c4(steps, tokens=(1, 8), warmup=3, keep_layer0=False, stack=True):
             torch.cuda.synchronize()
             stack_us = round(t0.elapsed_time(t1) * 1e3 / steps, 1)
             del stk, sws
+        w8_us = None
+        if T == 1:
+            # the same step in the reference's W4A8 numerics (row f3: int8
+            # activations per group of 128, Int4Gemv products, fp32 SiluMul
+            # and combine), on the same resident weights
+            from ainfer_amd.moe import with_precision
+            w8 = [with_precision(L_, L.PRECISION_W4A8) for L_ in layers]
+            ws8 = w8[0].workspace(T)
+
+            def step8(s):
+                w8[0].block_forward(xs[s % len(xs)], y, ws8)
+                for L_ in w8[1:]:
+                    L_.block_forward(y, y, ws8)
+            for s in range(warmup):
+                step8(s)
+            torch.cuda.synchronize()
+            t0.record()
+            for s in range(steps):
+                step8(s)
+            t1.record()
+            torch.cuda.synchronize()
+            w8_us = round(t0.elapsed_time(t1) * 1e3 / steps, 1)
+            del w8, ws8
         out[str(T)] = {"us_per_step": round(us, 1), "us_per_token": round(us / T, 2),
                        "us_per_block": round(us / len(layers), 2),
                        "unique_experts_per_layer": round(Ul, 2),
@@ -321,7 +344,10 @@ def run_c4(steps, tokens=(1, 8), warmup=3, keep_layer0=False, stack=True):
                        "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                        "stage_us_per_block": {k: round(v, 3) for k, v in st.items() if v > 0},
                        "dominant": dom,
-                       "stack_launch_us_per_step": stack_us}
+                       "stack_launch_us_per_step": stack_us,
+                       "w4a8_us_per_step": w8_us,
+                       "w4a8_hbm_frac": (round(nbytes / (w8_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+                                         if w8_us else None)}
         log(f"[bench]   c4 T={T}: {json.dumps(out[str(T)])}")
         del ws
     keep = layers[0] if keep_layer0 else None

@@ -27,7 +27,7 @@ def torch():
 
 
 CASES = [("c0", 1), ("c0", 5), ("c1", 1), ("c1", 4), ("c1", 16), ("c1", 300), ("c2", 4096),
-         ("c3", 2)]
+         ("c3", 1), ("c3", 2)]
 
 
 @pytest.mark.parametrize("name,T", CASES)
@@ -67,6 +67,26 @@ def test_w4a8_layer_parity(torch, oracle, name, T):
     a, b = y.float(), y16.float()
     cos = float((a * b).sum() / (a.norm() * b.norm()))
     assert cos > 0.999, cos
+
+
+@pytest.mark.parametrize("Is", [1024, 256, 0])
+def test_w4a8_layer_one_token_shared_widths(torch, oracle, Is):
+    """T = 1 runs the one-token expert GEMVs (k_w4a8_expert_t1): a shared
+    expert wider, narrower than the routed ones, or none."""
+    from ainfer_amd import _lib as L
+    from ainfer_amd.moe import make_input, with_precision
+    print(f"[case] w4a8 c1 T=1 Is={Is}", flush=True)
+    base = get_layer(torch, "c1", shared_inter=Is)
+    layer = with_precision(base, L.PRECISION_W4A8)
+    x = make_input(base.cfg, 1, tag=7900 + Is)
+    ws = layer.workspace(1)
+    y = torch.full((1, base.cfg.hidden), float("nan"), dtype=torch.bfloat16, device="cuda")
+    layer.forward(x, y, ws)
+    torch.cuda.synchronize()
+    ref = host_copy(oracle, base).forward_w4a8(to_np(x), 1)
+    got = to_np(y)
+    check_close(got, ref, f"w4a8 c1 T=1 Is={Is}")
+    assert np.mean(got == oracle.f32_to_bf16(ref)) > 0.9
 
 
 def test_w4a8_block_forward(torch, oracle):
