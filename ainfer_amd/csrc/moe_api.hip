@@ -290,17 +290,34 @@ ExpertArgs expert_args(const ainfer_moe_shape *s, const ainfer_moe_weights *w, c
 int down_kbw(const ainfer_moe_shape &s) { return down_kbw_of(s); }
 
 // The layer in W4A8 (AINFER_PRECISION_W4A8): the routing and dispatch of
-// the W4A16 path (16-token tiles), then x quantized, the grouped gate/up
-// GEMVs with SiLU, act quantized, the grouped down GEMVs and the fp32
-// combine (moe_w4a8.hip).
+// the W4A16 path, then x quantized, the grouped gate/up GEMVs with SiLU, act
+// quantized, the grouped down GEMVs and the fp32 combine (moe_w4a8.hip).
+// Decode sizes take the W4A16 decode routing kernel (canonical logits,
+// top-k, weights, gate, the MFMA-order copy of x, the dispatch in tiles of
+// DEC_MT tokens, and with norm the block's RMSNorm) and quantize x from its
+// MFMA-order copy; larger T the staged router, 16-token tiles and the plain x.
 int do_forward_w4a8(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const void *x,
-                    const void *resid, void *y, int T, void *ws, hipStream_t st, ProfCall *pc) {
+                    const void *resid, void *y, int T, void *ws, hipStream_t st, ProfCall *pc,
+                    const NormIn *norm = nullptr) {
   const Layout L = layout_of(*s, T);
   const int E = s->n_experts, k = s->top_k, H = s->hidden, I = s->inter, Is = s->shared_inter;
   const int has_shared = Is > 0;
   DispatchOut d = dispatch_out(s, L, ws, T);
-  d.mt = W8_MT;
-  if (T <= EXACT_ROUTER_MAX_T)
+  const bool decode = T <= DECODE_MAX_T && E <= 1024 && (!norm || T <= DECODE_NORM_MAX_T);
+  if (norm && !decode) return AINFER_ERR_ARG;  // the caller normalizes above that
+  d.mt = decode ? DEC_MT : W8_MT;
+  if (decode) {
+    DispatchOut dr = d;  // nothing here reads the per-expert counts or offsets
+    dr.counts = nullptr;
+    dr.offsets = nullptr;
+    int32_t *sync = at<int32_t>(ws, L.sync);
+    HIP_TRY(launch_route_decode(x, w->router_w, w->router_bias, w->shared_gate_w,
+                                at<float>(ws, L.logits), at<float>(ws, L.sg_logit),
+                                at<int32_t>(ws, L.idx), at<float>(ws, L.w), at<float>(ws, L.sg),
+                                at<uint16_t>(ws, L.xperm), T, H, E, k, has_shared, &dr, sync,
+                                (uint32_t *)(sync + L.slots), norm, st));
+    pc->end(3);
+  } else if (T <= EXACT_ROUTER_MAX_T)
     HIP_TRY(launch_router_exact(x, w->router_w, w->router_bias, w->shared_gate_w,
                                 at<float>(ws, L.logits), at<float>(ws, L.sg_logit),
                                 at<int32_t>(ws, L.idx), at<float>(ws, L.w), at<float>(ws, L.sg),
@@ -311,10 +328,12 @@ int do_forward_w4a8(const ainfer_moe_shape *s, const ainfer_moe_weights *w, cons
                                at<int32_t>(ws, L.idx), at<float>(ws, L.w), at<float>(ws, L.sg),
                                at<uint16_t>(ws, L.xperm), nullptr, T, H, E, k, has_shared,
                                nullptr, st));
-  pc->end(2);
-  HIP_TRY(launch_dispatch(at<int32_t>(ws, L.idx), T, k, E, W8_MT, has_shared,
-                          at<int32_t>(ws, L.chunk_counts), at<int32_t>(ws, L.rank), d, st));
-  pc->end(3);
+  if (!decode) {
+    pc->end(2);
+    HIP_TRY(launch_dispatch(at<int32_t>(ws, L.idx), T, k, E, W8_MT, has_shared,
+                            at<int32_t>(ws, L.chunk_counts), at<int32_t>(ws, L.rank), d, st));
+    pc->end(3);
+  }
   W4A8Args a;
   memset(&a, 0, sizeof a);
   a.xq = at<int8_t>(ws, L.w8_xq);
@@ -335,9 +354,13 @@ int do_forward_w4a8(const ainfer_moe_shape *s, const ainfer_moe_weights *w, cons
   a.H = H;
   a.I = I;
   a.Is = Is;
-  const int mtb = max_tiles_bound(*s, T, W8_MT);
-  HIP_TRY(launch_act_quant_i8(x, AINFER_ACT_BF16, T, H, at<int8_t>(ws, L.w8_xq),
-                              at<float>(ws, L.w8_xs), st));
+  const int mtb = max_tiles_bound(*s, T, d.mt);
+  if (decode)
+    HIP_TRY(launch_act_quant_i8(at<uint16_t>(ws, L.xperm), AINFER_ACT_BF16, T, H,
+                                at<int8_t>(ws, L.w8_xq), at<float>(ws, L.w8_xs), st, true));
+  else
+    HIP_TRY(launch_act_quant_i8(x, AINFER_ACT_BF16, T, H, at<int8_t>(ws, L.w8_xq),
+                                at<float>(ws, L.w8_xs), st));
   a.w0 = w->w_gate;
   a.w1 = w->w_up;
   a.s0 = (const uint16_t *)w->s_gate;
@@ -347,11 +370,9 @@ int do_forward_w4a8(const ainfer_moe_shape *s, const ainfer_moe_weights *w, cons
   a.ss0 = (const uint16_t *)w->ss_gate;
   a.ss1 = (const uint16_t *)w->ss_up;
   HIP_TRY(launch_w4a8_expert(0, s->scale_dtype, a, mtb, st));
-  HIP_TRY(launch_act_quant_i8(a.act, AINFER_ACT_F32, T * k, I, at<int8_t>(ws, L.w8_aq),
-                              at<float>(ws, L.w8_as), st));
-  if (has_shared)
-    HIP_TRY(launch_act_quant_i8(a.act_s, AINFER_ACT_F32, T, Is, at<int8_t>(ws, L.w8_aqs),
-                                at<float>(ws, L.w8_ass), st));
+  HIP_TRY(launch_act_quant_f32_pair(a.act, T * k, I, at<int8_t>(ws, L.w8_aq),
+                                    at<float>(ws, L.w8_as), has_shared ? a.act_s : nullptr, T,
+                                    Is, at<int8_t>(ws, L.w8_aqs), at<float>(ws, L.w8_ass), st));
   pc->end(4);
   a.w0 = w->w_down;
   a.s0 = (const uint16_t *)w->s_down;
@@ -371,7 +392,7 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
                const void *resid, void *y, int T, void *ws, hipStream_t st,
                ProfCall *pc, const NormIn *norm = nullptr) {
   if (s->precision == AINFER_PRECISION_W4A8)
-    return do_forward_w4a8(s, w, x, resid, y, T, ws, st, pc);
+    return do_forward_w4a8(s, w, x, resid, y, T, ws, st, pc, norm);
   const Layout L = layout_of(*s, T);
   const int E = s->n_experts, k = s->top_k, H = s->hidden;
   const int has_shared = s->shared_inter > 0;
@@ -590,8 +611,8 @@ int do_block(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const void 
   ProfCall pc(st);
   pc.start();
   DecodeGeom dg;
-  if (T <= DECODE_NORM_MAX_T && s->precision == AINFER_PRECISION_W4A16 &&
-      decode_geometry(*s, &dg)) {
+  if (T <= DECODE_NORM_MAX_T && s->n_experts <= 1024 &&
+      (s->precision == AINFER_PRECISION_W4A8 || decode_geometry(*s, &dg))) {
     // decode at up to 4 tokens: the routing kernel normalizes x itself (one
     // launch fewer per block: c4 T=1 about 2470 -> 2235 us per 60-block
     // step); the values are those k_rmsnorm writes

@@ -206,8 +206,14 @@ hipError_t launch_w4a8_expert(int mode, int scale_dtype, const W4A8Args &a, int 
 hipError_t launch_combine_f32(const float *o, const int32_t *inv, const float *w,
                               const float *sg, int has_shared, const void *resid, void *y, int T,
                               int k, int H, const int32_t *err, hipStream_t s);
+// mfma_order: x is bf16 in MFMA order (the routing kernel's copy); q and sq
+// are those of the plain row
 hipError_t launch_act_quant_i8(const void *x, int x_dtype, int T, int K, int8_t *q, float *sq,
-                               hipStream_t s);
+                               hipStream_t s, bool mfma_order = false);
+// two fp32 quantizations in one launch (x2 may be null)
+hipError_t launch_act_quant_f32_pair(const float *x, int T, int K, int8_t *q, float *sq,
+                                     const float *x2, int T2, int K2, int8_t *q2, float *sq2,
+                                     hipStream_t s);
 hipError_t launch_int4_gemv_i8(const uint8_t *P, const void *S, int scale_dtype, const int8_t *xq,
                                const float *sq, int M, int K, int T, float *y, hipStream_t s);
 // 0 when the shape has no decode geometry (the staged path is used then)

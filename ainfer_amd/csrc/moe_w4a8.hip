@@ -27,14 +27,33 @@ namespace {
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
-// one wave per (token, group of 128): two elements per lane
-template <typename XT>
+// one wave per (token, group of 128): two elements per lane.  PERM: x is
+// bf16 in MFMA order (inside each 32-element block, position 8j + e holds
+// element 4e + j); the group max does not depend on the order and every code
+// is written to its element's own position, so q and sq are those of the
+// plain row.
+// A second row set (x2, T2, K2 -> q2, sq2) takes the items past T * K / 128,
+// so two quantizations share a launch.
+template <typename XT, bool PERM = false>
 __global__ __launch_bounds__(256) void k_act_quant_i8(const XT *__restrict__ x, int T, int K,
                                                       int8_t *__restrict__ q,
-                                                      float *__restrict__ sq) {
+                                                      float *__restrict__ sq,
+                                                      const XT *__restrict__ x2 = nullptr,
+                                                      int T2 = 0, int K2 = 128,
+                                                      int8_t *__restrict__ q2 = nullptr,
+                                                      float *__restrict__ sq2 = nullptr) {
+  int item = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (item >= T * (K / 128)) {
+    item -= T * (K / 128);
+    if (item >= T2 * (K2 / 128)) return;
+    x = x2;
+    T = T2;
+    K = K2;
+    q = q2;
+    sq = sq2;
+  }
   const int G = K / 128;
-  const int item = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-  if (item >= T * G) return;
   const int t = item / G, g = item % G;
   const size_t base = (size_t)t * K + (size_t)g * 128 + 2 * lane;
   float v[2];
@@ -64,7 +83,18 @@ __global__ __launch_bounds__(256) void k_act_quant_i8(const XT *__restrict__ x, 
     qi = qi < -127 ? -127 : (qi > 127 ? 127 : qi);
     out[i] = (int8_t)qi;
   }
-  *(uint16_t *)(q + base) = (uint16_t)((uint8_t)out[0] | ((uint16_t)(uint8_t)out[1] << 8));
+  if constexpr (PERM) {
+    // positions 2 lane + i of the group: block p / 32, element 4 e + j of it
+    // for p % 32 = 8 j + e
+    const size_t gb = (size_t)t * K + (size_t)g * 128;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int p = 2 * lane + i, pb = p & 31;
+      q[gb + (p & ~31) + 4 * (pb & 7) + (pb >> 3)] = out[i];
+    }
+  } else {
+    *(uint16_t *)(q + base) = (uint16_t)((uint8_t)out[0] | ((uint16_t)(uint8_t)out[1] << 8));
+  }
   if (lane == 0) sq[(size_t)t * G + g] = s;
 }
 
@@ -452,13 +482,28 @@ __global__ __launch_bounds__(256) void k_combine_f32(const float *__restrict__ o
 }  // namespace
 
 hipError_t launch_act_quant_i8(const void *x, int x_dtype, int T, int K, int8_t *q, float *sq,
-                               hipStream_t s) {
+                               hipStream_t s, bool mfma_order) {
   const int items = T * (K / 128);
   const unsigned grid = (items + 3) / 4;
+  if (mfma_order) {
+    if (x_dtype != AINFER_ACT_BF16) return hipErrorInvalidValue;
+    k_act_quant_i8<uint16_t, true><<<grid, 256, 0, s>>>((const uint16_t *)x, T, K, q, sq);
+    return hipGetLastError();
+  }
   if (x_dtype == AINFER_ACT_F32)
     k_act_quant_i8<float><<<grid, 256, 0, s>>>((const float *)x, T, K, q, sq);
   else
     k_act_quant_i8<uint16_t><<<grid, 256, 0, s>>>((const uint16_t *)x, T, K, q, sq);
+  return hipGetLastError();
+}
+
+hipError_t launch_act_quant_f32_pair(const float *x, int T, int K, int8_t *q, float *sq,
+                                     const float *x2, int T2, int K2, int8_t *q2, float *sq2,
+                                     hipStream_t s) {
+  const int items = T * (K / 128) + (x2 ? T2 * (K2 / 128) : 0);
+  if (items == 0) return hipSuccess;
+  k_act_quant_i8<float><<<(items + 3) / 4, 256, 0, s>>>(x, T, K, q, sq, x2, x2 ? T2 : 0,
+                                                        x2 ? K2 : 128, q2, sq2);
   return hipGetLastError();
 }
 
