@@ -298,10 +298,10 @@ def test_block_forward_and_stack(torch, oracle):
 @pytest.mark.parametrize("mode", ["plain", "one_plus"])
 def test_block_forward_fused_norm(torch, oracle, mode):
     """At T <= 4 the routing kernel applies the block's RMSNorm itself (one
-    code path for T = 1..4).  At T = 3 and 4 every later stage is the one
+    code path for T = 1..4).  At T = 3 to 16 every later stage is the one
     T = 17 runs (4-token tiles, per-token arithmetic), and T = 17 normalizes
     with the separate RMSNorm kernel: each token's output must be equal bit
-    for bit.  T = 1 and 2 run the fused expert kernel, whose down items split
+    for bit (T = 5 and 8: both normalize with the separate kernel).  T = 1 and 2 run the fused expert kernel, whose down items split
     K differently, so there the check is the oracle's block within tolerance
     (as at every T)."""
     from ainfer_amd import _lib as L
@@ -323,7 +323,7 @@ def test_block_forward_fused_norm(torch, oracle, mode):
     ref17 = torch.empty_like(x)
     layer.block_forward(x, ref17, ws, norm_w=nw, norm_mode=nm)
     hl = host_copy(oracle, layer)
-    for T in (1, 2, 3, 4, 16):
+    for T in (1, 2, 3, 4, 5, 8, 16):
         print(f"[case] fused norm {mode} T={T}", flush=True)
         out = torch.empty_like(x[:T])
         layer.block_forward(x[:T].contiguous(), out, ws, norm_w=nw, norm_mode=nm)
