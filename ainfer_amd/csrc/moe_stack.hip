@@ -431,33 +431,22 @@ __global__ __launch_bounds__(STK_NW * 64, STK_WAVES_PER_EU) void k_decode_stack(
       if (threadIdx.x < 64) arrive(c_lg, rel_lg, tag, a.nrw, threadIdx.x);
     }
     STRACE(l, 3);
-    // ---- 1b. the shared expert's items: independent of the routing, on
-    // workgroups after the routing ones, as soon as x is normalized --------
+    // ---- 1b. the shared expert's gate/up items: independent of the
+    // routing, on workgroups after the routing ones, as soon as x is
+    // normalized (its down items lead the main list's down section) --------
     const int nsh = a.has_shared ? 1 : 0;  // one shared tile: T <= DEC_MT
+    const int4 tsh = make_int4(E, 0, T, 0);
     if (nsh) {
-      const int4 tsh = make_int4(E, 0, T, 0);
-      const int n_sh = sg + sd;
-      for (int q = (wg - a.nrw + G) % G; q < n_sh; q += G) {
+      for (int q = (wg - a.nrw + G) % G; q < sg; q += G) {
         lane = tid_opaque() & 63;
         __syncthreads();
-        if (q < sg) {
-          const ExpertArgs gu = item_args(a, ly, lb, s_ptok, 0);
-          const int32_t *fx = a.fx;
-          expert_lds_item<SD, 4, DEC_RG_GATE_UP, DEC_MT, 0, true, false>(
-              gu, tsh, q, lds, [&]() { wg_wait_flags(fx, 1, tag, a); });
-          if (threadIdx.x < 64) {
-            wait_stores();
-            if (lane == 0) st_dev(a.fsgu + q, (int32_t)tag);
-          }
-        } else {
-          const int32_t *fg = a.fsgu;
-          const ExpertArgs dn = item_args(a, ly, lb, s_ptok, 1);
-          expert_lds_item<SD, KBW_DN, DEC_RG_DOWN, DEC_MT, 1, true, false>(
-              dn, tsh, q - sg, lds, [&]() { wg_wait_flags(fg, sg, tag, a); });
-          if (threadIdx.x < 64) {
-            wait_stores();
-            if (lane == 0) st_dev(a.fsdn + (q - sg), (int32_t)tag);
-          }
+        const ExpertArgs gu = item_args(a, ly, lb, s_ptok, 0);
+        const int32_t *fx = a.fx;
+        expert_lds_item<SD, 4, DEC_RG_GATE_UP, DEC_MT, 0, true, false>(
+            gu, tsh, q, lds, [&]() { wg_wait_flags(fx, 1, tag, a); });
+        if (threadIdx.x < 64) {
+          wait_stores();
+          if (lane == 0) st_dev(a.fsgu + q, (int32_t)tag);
         }
       }
     }
@@ -521,15 +510,20 @@ __global__ __launch_bounds__(STK_NW * 64, STK_WAVES_PER_EU) void k_decode_stack(
     // 4. the combine units, dealt from workgroup 0 again: their count does
     // not depend on the routing, so each runs exactly once even if
     // workgroups disagreed on the tiles (a timed-out wait) ------------------
-    const int n_rt = n_tiles - nsh;  // the routed tiles (the shared one ran above)
-    const int n_gu = n_rt * sg, n_dn = n_rt * sd, n_cb = T * sd;
-    const int n_items = n_gu + n_dn;
-    const int my_items = n_items > wg ? (n_items - wg + G - 1) / G : 0;
+    // items: the routed gate/up items, the shared expert's down items, the
+    // routed down items.  Dealt round-robin from workgroup nrw + sg on, so the
+    // routing workgroups and those that ran the shared gate/up items (both
+    // start this phase late) come last and take fewer items.
+    const int n_rt = n_tiles - nsh;  // the routed tiles
+    const int n_gu = n_rt * sg, n_sdn = nsh * sd, n_dn = n_rt * sd, n_cb = T * sd;
+    const int n_items = n_gu + n_sdn + n_dn;
+    const int wr = (wg - (a.nrw + nsh * sg) % G + G) % G;  // this workgroup's turn
+    const int my_items = n_items > wr ? (n_items - wr + G - 1) / G : 0;
     const int my_cb = n_cb > wg ? (n_cb - wg + G - 1) / G : 0;
     for (int i = 0; i < my_items + my_cb; ++i) {
       STRACE(l, 6 + (i < 5 ? i : 5));
       // q: item index, or n_items + combine unit index
-      const int q = i < my_items ? wg + i * G : n_items + wg + (i - my_items) * G;
+      const int q = i < my_items ? wr + i * G : n_items + wg + (i - my_items) * G;
       lane = tid_opaque() & 63;
       __syncthreads();  // the previous item's LDS (read by its wave 0) is free
       if (q < n_gu) {
@@ -541,8 +535,18 @@ __global__ __launch_bounds__(STK_NW * 64, STK_WAVES_PER_EU) void k_decode_stack(
           wait_stores();
           if (lane == 0) st_dev(a.fgu + tile * sg + slab, (int32_t)tag);
         }
+      } else if (q < n_gu + n_sdn) {
+        const int slab = q - n_gu;
+        const int32_t *fg = a.fsgu;
+        const ExpertArgs dn = item_args(a, ly, lb, s_ptok, 1);
+        expert_lds_item<SD, KBW_DN, DEC_RG_DOWN, DEC_MT, 1, true, false>(
+            dn, tsh, slab, lds, [&]() { wg_wait_flags(fg, sg, tag, a); });
+        if (threadIdx.x < 64) {
+          wait_stores();
+          if (lane == 0) st_dev(a.fsdn + slab, (int32_t)tag);
+        }
       } else if (q < n_items) {
-        const int tile = (q - n_gu) / sd, slab = (q - n_gu) % sd;
+        const int tile = (q - n_gu - n_sdn) / sd, slab = (q - n_gu - n_sdn) % sd;
         const int32_t *fg = a.fgu + tile * sg;
         const ExpertArgs dn = item_args(a, ly, lb, s_ptok, 1);
         expert_lds_item<SD, KBW_DN, DEC_RG_DOWN, DEC_MT, 1, true, false>(
