@@ -354,7 +354,6 @@ __global__ __launch_bounds__(1024, DEC_WAVES_PER_SIMD) void k_experts_decode(Exp
   const int lane = threadIdx.x & 63;
   const int sg = a.gu.n_slabs, sd = a.dn.n_slabs;
   const int n_gu = a.max_tiles * sg;
-  const int n_tiles = *a.gu.n_tiles;
   {
     const int item = blockIdx.x + (SPLIT ? n_gu : 0);
     // ---- item -> (kind, tile, slab): all gate/up items (tile-major,
@@ -362,6 +361,8 @@ __global__ __launch_bounds__(1024, DEC_WAVES_PER_SIMD) void k_experts_decode(Exp
     const int is_gu = item < n_gu;
     const int r = is_gu ? item : item - n_gu, ns = is_gu ? sg : sd;
     const int tile = r / ns, slab = r % ns;
+    int n_tiles;
+    const int4 tt = sload_tile(is_gu ? a.gu.tiles : a.dn.tiles, a.gu.n_tiles, tile, n_tiles);
     if (tile >= n_tiles) return;
     DTRACE_AT(1, item, 0);
 #ifdef AINFER_DECODE_TRACE
@@ -371,8 +372,7 @@ __global__ __launch_bounds__(1024, DEC_WAVES_PER_SIMD) void k_experts_decode(Exp
     __syncthreads();
     if (!SPLIT && is_gu) {
       // x (MFMA order) comes from the routing kernel: plain, cacheable loads
-      expert_lds_item<SD, KBW_GU, RG_GU, DEC_MT, 0, true, false>(a.gu, a.gu.tiles[tile],
-                                                                          slab, lds);
+      expert_lds_item<SD, KBW_GU, RG_GU, DEC_MT, 0, true, false>(a.gu, tt, slab, lds);
       if (threadIdx.x >= 64) return;
       // wave 0: its act stores, then the arrival
       DTRACE_AT(1, item, 2);
@@ -381,7 +381,7 @@ __global__ __launch_bounds__(1024, DEC_WAVES_PER_SIMD) void k_experts_decode(Exp
       DTRACE_AT(1, item, 3);
       return;
     }
-    const int4 td = sload_int4(a.dn.tiles + tile);
+    const int4 td = tt;
     // the down weights are requested before the wait for the tile's act rows
     const int32_t *gdone = &gu_done[tile * SY_STRIDE];
     int32_t *err = a.sync + SY_ERR;

@@ -186,8 +186,10 @@ template <int SD, int KBW, int RG, int MT, int MODE>
 __global__ __launch_bounds__(1024) void k_expert_lds(ExpertArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int tile_id = blockIdx.x / a.n_slabs, slab = blockIdx.x % a.n_slabs;
-  if (tile_id >= *a.n_tiles) return;
-  expert_lds_item<SD, KBW, RG, MT, MODE, false, false, true>(a, a.tiles[tile_id], slab, lds);
+  int n_tiles;
+  const int4 t = sload_tile(a.tiles, a.n_tiles, tile_id, n_tiles);
+  if (tile_id >= n_tiles) return;
+  expert_lds_item<SD, KBW, RG, MT, MODE, false, false, true>(a, t, slab, lds);
 }
 
 }  // namespace

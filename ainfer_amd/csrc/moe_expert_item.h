@@ -17,6 +17,24 @@ static __device__ unsigned long long g_dland[2][1 << 14][3];  // [MODE][workgrou
 #define ITRACE(I)
 #endif
 
+// A tile entry and the tile count in one scalar round trip: both loads are
+// in flight before the wait (a count read first, then the entry, costs two
+// trips while every workgroup of the launch reads the same lines).  `tile`
+// is below the launch's tile bound, so the entry is inside the tile list
+// whether or not the dispatch filled it; the caller checks it against n.
+__device__ __forceinline__ int4 sload_tile(const int4 *tiles, const int32_t *n_tiles, int tile,
+                                           int &n) {
+  typedef int i32x4 __attribute__((ext_vector_type(4)));
+  i32x4 v;
+  int c;
+  asm volatile("s_load_dword %1, %3, 0x0\n\ts_load_dwordx4 %0, %2, 0x0\n\ts_waitcnt lgkmcnt(0)"
+               : "=&s"(v), "=&s"(c)
+               : "s"(tiles + tile), "s"(n_tiles)
+               : "memory");
+  n = c;
+  return make_int4(v[0], v[1], v[2], v[3]);
+}
+
 __device__ __forceinline__ u32x4 ldg_stream(const void *p) {
   return __builtin_nontemporal_load((const u32x4 *)p);
 }
