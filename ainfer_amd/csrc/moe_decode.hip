@@ -368,8 +368,9 @@ __global__ __launch_bounds__(1024, DEC_WAVES_PER_SIMD) void k_experts_decode(Exp
 #ifdef AINFER_DECODE_TRACE
     if (threadIdx.x == 0) g_dtrace[1][item][4] = is_gu;
 #endif
-    // the previous item's partials (read by wave 0) are no longer needed
-    __syncthreads();
+    // one item per workgroup, and no barrier before its loads: each wave
+    // issues its weight loads as soon as it is launched (the waves of a
+    // workgroup start up to about 1.5 us apart at the launch's start)
     if (!SPLIT && is_gu) {
       // x (MFMA order) comes from the routing kernel: plain, cacheable loads
       expert_lds_item<SD, KBW_GU, RG_GU, DEC_MT, 0, true, false>(a.gu, tt, slab, lds);
