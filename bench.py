@@ -471,7 +471,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the expert-parallel sharding plan is described in DESIGN.md)", file=sys.stderr)
+              "(expert parallelism is a design only)", file=sys.stderr)
         sys.exit(2)
 
     import torch
