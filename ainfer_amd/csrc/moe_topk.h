@@ -82,8 +82,9 @@ __device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a >
 //  1. tau = the k-th largest of the 16 quad maxima (each quad of lanes
 //     covers 4 * NV experts).  The k quads whose maxima are >= tau hold k
 //     distinct experts >= tau, so every expert of the top-k is >= tau.
-//  2. Experts >= tau are compacted into `cand` (LDS, 64 entries per wave);
-//     for random logits there are about k + 5 of them.
+//  2. Experts >= tau are compacted into `cand` (LDS, 64 entries per wave)
+//     at offsets from a wave prefix sum of the per-lane counts; for random
+//     logits there are about k + 5 of them.
 //  3. Each candidate's rank is the number of candidates above it; rank
 //     r < k is pick r.
 // More than 64 candidates (many equal logits), an absent tau or k > 16 take
@@ -114,14 +115,23 @@ __device__ __forceinline__ void wave_topk_fast(const uint32_t (&key)[NV], int E,
   const uint64_t tau = tb ? readlane_u64(lm, __builtin_ctzll(tb)) : 0ull;
   int nc = 0;
   if (tau != 0ull) {
+    // each lane's candidates at its offset from a wave prefix sum of the
+    // per-lane counts (one scan instead of NV ballot rounds; the rank below
+    // does not depend on the list's order)
+    bool p[NV];
+    int cnt = 0;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
-      const bool p = c[i] >= tau;
-      const uint64_t b = __ballot(p);
-      const int below = __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32),
-                                                  __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0));
-      if (p && nc + below < 64) cand[nc + below] = c[i];
-      nc += __popcll(b);
+      p[i] = c[i] >= tau;
+      cnt += p[i] ? 1 : 0;
+    }
+    const int incl = wave_scan_incl(cnt);
+    nc = __builtin_amdgcn_readlane(incl, 63);
+    int pos = incl - cnt;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      if (p[i] && pos < 64) cand[pos] = c[i];
+      pos += p[i] ? 1 : 0;
     }
   }
   if (tau == 0ull || nc > 64) {
@@ -132,13 +142,23 @@ __device__ __forceinline__ void wave_topk_fast(const uint32_t (&key)[NV], int E,
   __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
   const uint64_t mine = lane < nc ? cand[lane] : 0ull;
   int rk = 0;
-  // four broadcast reads in flight per step; entries past nc are ignored
-  for (int j0 = 0; j0 < nc; j0 += 4) {
-    uint64_t v[4];
+  if (nc <= 16) {
+    // the usual case (about k + 5 candidates): every broadcast read in
+    // flight at once; entries past nc are ignored
+    uint64_t v[16];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) v[q] = cand[j0 + q];
+    for (int j = 0; j < 16; ++j) v[j] = cand[j];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) rk += (j0 + q < nc && v[q] > mine) ? 1 : 0;
+    for (int j = 0; j < 16; ++j) rk += (j < nc && v[j] > mine) ? 1 : 0;
+  } else {
+    // four broadcast reads in flight per step
+    for (int j0 = 0; j0 < nc; j0 += 4) {
+      uint64_t v[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[q] = cand[j0 + q];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) rk += (j0 + q < nc && v[q] > mine) ? 1 : 0;
+    }
   }
   if (lane < nc && rk < k) sel[rk] = mine;
   __builtin_amdgcn_wave_barrier();
