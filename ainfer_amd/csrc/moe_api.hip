@@ -293,9 +293,9 @@ int down_kbw(const ainfer_moe_shape &s) { return down_kbw_of(s); }
 // the W4A16 path, then x quantized, the grouped gate/up GEMVs with SiLU, act
 // quantized, the grouped down GEMVs and the fp32 combine (moe_w4a8.hip).
 // Decode sizes take the W4A16 decode routing kernel (canonical logits,
-// top-k, weights, gate, the MFMA-order copy of x, the dispatch in tiles of
-// DEC_MT tokens, and with norm the block's RMSNorm) and quantize x from its
-// MFMA-order copy; larger T the staged router, 16-token tiles and the plain x.
+// top-k, weights, gate, the MFMA-order copy of x with its W4A8 codes, the
+// dispatch in tiles of DEC_MT tokens, and with norm the block's RMSNorm);
+// larger T the staged router, 16-token tiles and x quantized on its own.
 int do_forward_w4a8(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const void *x,
                     const void *resid, void *y, int T, void *ws, hipStream_t st, ProfCall *pc,
                     const NormIn *norm = nullptr) {
@@ -315,7 +315,8 @@ int do_forward_w4a8(const ainfer_moe_shape *s, const ainfer_moe_weights *w, cons
                                 at<float>(ws, L.logits), at<float>(ws, L.sg_logit),
                                 at<int32_t>(ws, L.idx), at<float>(ws, L.w), at<float>(ws, L.sg),
                                 at<uint16_t>(ws, L.xperm), T, H, E, k, has_shared, &dr, sync,
-                                (uint32_t *)(sync + L.slots), norm, st));
+                                (uint32_t *)(sync + L.slots), norm, st, at<int8_t>(ws, L.w8_xq),
+                                at<float>(ws, L.w8_xs)));
     pc->end(3);
   } else if (T <= EXACT_ROUTER_MAX_T)
     HIP_TRY(launch_router_exact(x, w->router_w, w->router_bias, w->shared_gate_w,
@@ -355,10 +356,7 @@ int do_forward_w4a8(const ainfer_moe_shape *s, const ainfer_moe_weights *w, cons
   a.I = I;
   a.Is = Is;
   const int mtb = max_tiles_bound(*s, T, d.mt);
-  if (decode)
-    HIP_TRY(launch_act_quant_i8(at<uint16_t>(ws, L.xperm), AINFER_ACT_BF16, T, H,
-                                at<int8_t>(ws, L.w8_xq), at<float>(ws, L.w8_xs), st, true));
-  else
+  if (!decode)  // the decode routing kernel wrote the codes with its x copy
     HIP_TRY(launch_act_quant_i8(x, AINFER_ACT_BF16, T, H, at<int8_t>(ws, L.w8_xq),
                                 at<float>(ws, L.w8_xs), st));
   a.w0 = w->w_gate;

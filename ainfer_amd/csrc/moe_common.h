@@ -373,10 +373,15 @@ __device__ __forceinline__ uint32_t norm_pair(uint32_t xp, uint32_t wp, float in
   return bf16x2_bits(v0 * w0, v1 * w1);
 }
 
+// q8 / sq8 (optional): the row's W4A8 codes and group scales as well, the
+// arithmetic of k_act_quant_i8 (ScalesMax + Quantize, kernels.cpp:551-579)
+// on the values written (the 4 lanes holding a 128-wide group share its max)
 __device__ __forceinline__ void write_xperm(const uint16_t *__restrict__ xrow,
                                             uint16_t *__restrict__ xperm,
                                             float *__restrict__ xsum, int t, int H, int lane,
-                                            const NormIn *norm = nullptr, float inv = 1.0f) {
+                                            const NormIn *norm = nullptr, float inv = 1.0f,
+                                            int8_t *__restrict__ q8 = nullptr,
+                                            float *__restrict__ sq8 = nullptr) {
   {
     uint16_t *xo = xperm + (size_t)t * H;
     for (int b = lane; b < (H >> 5); b += 64) {
@@ -419,6 +424,38 @@ __device__ __forceinline__ void write_xperm(const uint16_t *__restrict__ xrow,
         bs += __shfl_xor(bs, 1, 64);
         bs += __shfl_xor(bs, 2, 64);
         if ((b & 3) == 0) xsum[(size_t)t * (H >> 7) + (b >> 2)] = bs;
+      }
+      if (q8) {
+        float m = 0.0f;  // the reference's running max from 0 (exact: any order)
+#pragma unroll
+        for (int i2 = 0; i2 < 16; ++i2) {
+          const float a0 = fabsf(__uint_as_float(in[i2] << 16));
+          const float a1 = fabsf(__uint_as_float(in[i2] & 0xFFFF0000u));
+          m = a0 > m ? a0 : m;
+          m = a1 > m ? a1 : m;
+        }
+        const float m1 = __shfl_xor(m, 1, 64);
+        m = m1 > m ? m1 : m;
+        const float m2 = __shfl_xor(m, 2, 64);
+        m = m2 > m ? m2 : m;
+        float sc = m / 127.0f;
+        sc = sc == 0.0f ? 1.0f : sc;
+        uint32_t pk[8];
+#pragma unroll
+        for (int i2 = 0; i2 < 8; ++i2) pk[i2] = 0u;
+#pragma unroll
+        for (int i2 = 0; i2 < 32; ++i2) {
+          const uint32_t w = in[i2 >> 1];
+          const float v = __uint_as_float((i2 & 1) ? (w & 0xFFFF0000u) : (w << 16));
+          const float r = v / sc;
+          int qi = (int)(r >= 0.0f ? r + 0.5f : r - 0.5f);
+          qi = qi < -127 ? -127 : (qi > 127 ? 127 : qi);
+          pk[i2 >> 2] |= (uint32_t)(uint8_t)qi << (8 * (i2 & 3));
+        }
+        u32x4 *qd = (u32x4 *)(q8 + (size_t)t * H + b * 32);
+        qd[0] = u32x4{pk[0], pk[1], pk[2], pk[3]};
+        qd[1] = u32x4{pk[4], pk[5], pk[6], pk[7]};
+        if ((b & 3) == 0) sq8[(size_t)t * (H >> 7) + (b >> 2)] = sc;
       }
     }
   }

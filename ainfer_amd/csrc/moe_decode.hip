@@ -116,6 +116,8 @@ struct RouteDecodeArgs {
   int32_t *idx;
   float *w, *sg;
   uint16_t *xperm;
+  int8_t *w8q;      // optional: W4A8 codes and group scales of the (normalized) x
+  float *w8sq;
   DispatchOut ds;
   int32_t *sync;
   uint32_t *slots;  // [DECODE_MAX_T][E + 1] ~bits of the logits (sync region)
@@ -262,7 +264,8 @@ __global__ __launch_bounds__(W * 64) void k_route_decode(RouteDecodeArgs a) {
     // the selection's path (the selection polls as soon as it starts).
     if (t < T && a.xperm) {
       const float inv = NORM ? row_rms_inv(a.x + (size_t)t * H, H, a.norm.eps, lane) : 1.0f;
-      write_xperm(a.x + (size_t)t * H, a.xperm, nullptr, t, H, lane, NORM ? &a.norm : nullptr, inv);
+      write_xperm(a.x + (size_t)t * H, a.xperm, nullptr, t, H, lane, NORM ? &a.norm : nullptr, inv,
+                  a.w8q, a.w8sq);
     }
     return;
   }
@@ -486,7 +489,7 @@ hipError_t launch_route_decode(const void *x, const void *rw, const float *bias,
                                float *logits, float *sgl, int32_t *idx, float *w, float *sg,
                                void *xperm, int T, int H, int E, int k, int has_shared,
                                const DispatchOut *ds, int32_t *sync, uint32_t *slots,
-                               const NormIn *norm, hipStream_t s) {
+                               const NormIn *norm, hipStream_t s, int8_t *w8q, float *w8sq) {
   if (T <= 0) return hipSuccess;
   if (T > DECODE_MAX_T || T > RD_WAVES || E > 1024) return hipErrorInvalidValue;
   RouteDecodeArgs a;
@@ -501,6 +504,9 @@ hipError_t launch_route_decode(const void *x, const void *rw, const float *bias,
   a.w = w;
   a.sg = sg;
   a.xperm = (uint16_t *)xperm;
+  a.w8q = w8q;
+  a.w8sq = w8sq;
+  if (w8q && !xperm) return hipErrorInvalidValue;  // the codes come with the MFMA-order copy
   if (ds) a.ds = *ds;
   a.sync = sync;
   a.slots = slots;

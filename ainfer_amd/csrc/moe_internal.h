@@ -206,10 +206,8 @@ hipError_t launch_w4a8_expert(int mode, int scale_dtype, const W4A8Args &a, int 
 hipError_t launch_combine_f32(const float *o, const int32_t *inv, const float *w,
                               const float *sg, int has_shared, const void *resid, void *y, int T,
                               int k, int H, const int32_t *err, hipStream_t s);
-// mfma_order: x is bf16 in MFMA order (the routing kernel's copy); q and sq
-// are those of the plain row
 hipError_t launch_act_quant_i8(const void *x, int x_dtype, int T, int K, int8_t *q, float *sq,
-                               hipStream_t s, bool mfma_order = false);
+                               hipStream_t s);
 // two fp32 quantizations in one launch (x2 may be null)
 hipError_t launch_act_quant_f32_pair(const float *x, int T, int K, int8_t *q, float *sq,
                                      const float *x2, int T2, int K2, int8_t *q2, float *sq2,
@@ -224,7 +222,8 @@ hipError_t launch_route_decode(const void *x, const void *rw, const float *bias,
                                float *logits, float *sgl, int32_t *idx, float *w, float *sg,
                                void *xperm, int T, int H, int E, int k, int has_shared,
                                const DispatchOut *ds, int32_t *sync, uint32_t *slots,
-                               const NormIn *norm, hipStream_t s);
+                               const NormIn *norm, hipStream_t s, int8_t *w8q = nullptr,
+                               float *w8sq = nullptr);
 // gate/up + SiLU, down and the combine (y = sum_j w_j o_j + g_s o_s (+ resid));
 // split: gate/up in a launch of its own first (measured faster at T = 1,
 // where the down items of a fused launch wait behind the gate/up items for

@@ -27,14 +27,10 @@ namespace {
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
-// one wave per (token, group of 128): two elements per lane.  PERM: x is
-// bf16 in MFMA order (inside each 32-element block, position 8j + e holds
-// element 4e + j); the group max does not depend on the order and every code
-// is written to its element's own position, so q and sq are those of the
-// plain row.
+// one wave per (token, group of 128): two elements per lane.
 // A second row set (x2, T2, K2 -> q2, sq2) takes the items past T * K / 128,
 // so two quantizations share a launch.
-template <typename XT, bool PERM = false>
+template <typename XT>
 __global__ __launch_bounds__(256) void k_act_quant_i8(const XT *__restrict__ x, int T, int K,
                                                       int8_t *__restrict__ q,
                                                       float *__restrict__ sq,
@@ -83,18 +79,7 @@ __global__ __launch_bounds__(256) void k_act_quant_i8(const XT *__restrict__ x, 
     qi = qi < -127 ? -127 : (qi > 127 ? 127 : qi);
     out[i] = (int8_t)qi;
   }
-  if constexpr (PERM) {
-    // positions 2 lane + i of the group: block p / 32, element 4 e + j of it
-    // for p % 32 = 8 j + e
-    const size_t gb = (size_t)t * K + (size_t)g * 128;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int p = 2 * lane + i, pb = p & 31;
-      q[gb + (p & ~31) + 4 * (pb & 7) + (pb >> 3)] = out[i];
-    }
-  } else {
-    *(uint16_t *)(q + base) = (uint16_t)((uint8_t)out[0] | ((uint16_t)(uint8_t)out[1] << 8));
-  }
+  *(uint16_t *)(q + base) = (uint16_t)((uint8_t)out[0] | ((uint16_t)(uint8_t)out[1] << 8));
   if (lane == 0) sq[(size_t)t * G + g] = s;
 }
 
@@ -482,14 +467,9 @@ __global__ __launch_bounds__(256) void k_combine_f32(const float *__restrict__ o
 }  // namespace
 
 hipError_t launch_act_quant_i8(const void *x, int x_dtype, int T, int K, int8_t *q, float *sq,
-                               hipStream_t s, bool mfma_order) {
+                               hipStream_t s) {
   const int items = T * (K / 128);
   const unsigned grid = (items + 3) / 4;
-  if (mfma_order) {
-    if (x_dtype != AINFER_ACT_BF16) return hipErrorInvalidValue;
-    k_act_quant_i8<uint16_t, true><<<grid, 256, 0, s>>>((const uint16_t *)x, T, K, q, sq);
-    return hipGetLastError();
-  }
   if (x_dtype == AINFER_ACT_F32)
     k_act_quant_i8<float><<<grid, 256, 0, s>>>((const float *)x, T, K, q, sq);
   else
