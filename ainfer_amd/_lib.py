@@ -28,7 +28,7 @@ EXPORTS = (
     "ainfer_moe_forward", "ainfer_moe_block_forward", "ainfer_moe_block_forward_noalloc",
     "ainfer_moe_stack_workspace_bytes", "ainfer_moe_stack_table_bytes", "ainfer_moe_stack_prepare", "ainfer_moe_stack_forward",
     "ainfer_moe_route",
-    "ainfer_moe_dispatch", "ainfer_moe_rmsnorm", "ainfer_moe_fill",
+    "ainfer_moe_dispatch", "ainfer_moe_experts", "ainfer_moe_combine", "ainfer_moe_rmsnorm", "ainfer_moe_fill",
     "ainfer_moe_act_quant_i8", "ainfer_moe_int4_gemv_i8",
     "ainfer_moe_profile_enable", "ainfer_moe_profile_read", "ainfer_moe_profile_kernel", "ainfer_moe_debug_spin_limit",
     "ainfer_binfer_open", "ainfer_binfer_close", "ainfer_binfer_error", "ainfer_binfer_moe_info",
@@ -85,6 +85,8 @@ def lib():
         L.ainfer_moe_stack_forward.argtypes = [sp, P, I32, I32, F, P, P, I32, P, SZ, P]
         L.ainfer_moe_route.argtypes = [sp, wp, P, I32, P, P, P, P, P, SZ, P]
         L.ainfer_moe_dispatch.argtypes = [sp, P, I32, P, P, P, P, P, SZ, P]
+        L.ainfer_moe_experts.argtypes = [sp, wp, P, P, I32, P, P, SZ, P]
+        L.ainfer_moe_combine.argtypes = [sp, P, P, P, P, P, I32, P]
         L.ainfer_moe_rmsnorm.argtypes = [P, P, I32, F, P, I32, I32, P]
         L.ainfer_moe_fill.argtypes = [I32, C.c_uint64, F, SZ, P, P]
         L.ainfer_moe_act_quant_i8.argtypes = [P, I32, I32, I32, P, P, P]

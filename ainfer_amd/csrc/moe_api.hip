@@ -215,6 +215,11 @@ int check_weights(const ainfer_moe_shape *s, const ainfer_moe_weights *w) {
   do {                                             \
     if ((expr) != hipSuccess) return AINFER_ERR_HIP; \
   } while (0)
+#define HIP_TRY_RC(expr)          \
+  do {                            \
+    const int rc_ = (expr);       \
+    if (rc_ != AINFER_OK) return rc_; \
+  } while (0)
 
 DispatchOut dispatch_out(const ainfer_moe_shape *s, const Layout &L, void *ws, int T) {
   DispatchOut d;
@@ -386,6 +391,125 @@ int do_forward_w4a8(const ainfer_moe_shape *s, const ainfer_moe_weights *w, cons
   return AINFER_OK;
 }
 
+// The expert stage on the dispatch d in the workspace, x in MFMA order
+// written (and its group sums at T >= GEMM_MIN_T): the grouped GEMM there
+// (with the small experts' 16-token tiles), else the streaming items over
+// tiles of DEC_MT tokens.  Leaves o in the workspace: dispatch-position rows,
+// the shared expert's at rows T * k + t.
+int run_experts(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const Layout &L,
+                void *ws, DispatchOut &d, int T, bool gemm, hipStream_t st, ProfCall *pc) {
+  const int E = s->n_experts, k = s->top_k, H = s->hidden;
+  if (gemm) {
+    GemmArgs g;
+    memset(&g, 0, sizeof g);
+    g.ptok = d.ptok;
+    g.tiles = d.tiles;
+    g.n_tiles = d.n_tiles;
+    g.T = T;
+    g.k = k;
+    g.E = E;
+    g.H = H;
+    g.I = s->inter;
+    g.Is = s->shared_inter;
+    g.xsum = at<float>(ws, L.xsum);
+    g.asum = at<float>(ws, L.asum);
+    g.asum_s = at<float>(ws, L.asum_s);
+    const int gtiles = max_tiles_bound(*s, T, GEMM_MT);
+    g.w0 = w->w_gate;
+    g.w1 = w->w_up;
+    g.s0 = (const uint16_t *)w->s_gate;
+    g.s1 = (const uint16_t *)w->s_up;
+    g.ws0 = w->ws_gate;
+    g.ws1 = w->ws_up;
+    g.ss0 = (const uint16_t *)w->ss_gate;
+    g.ss1 = (const uint16_t *)w->ss_up;
+    g.a_routed = at<uint16_t>(ws, L.xperm);
+    g.act = at<uint16_t>(ws, L.act);
+    g.act_s = at<uint16_t>(ws, L.act_s);
+    HIP_TRY(launch_expert_gemm(0, s->scale_dtype, g, gtiles, st));
+    ExpertArgs sgu, sdn;
+    int small_bound = 0;
+    if (d.small_max > 0) {
+      DispatchOut d2 = d;
+      d2.tiles = d.tiles2;
+      d2.n_tiles = d.n_tiles2;
+      sgu = expert_args(s, w, L, ws, d2, T, 0);
+      sdn = expert_args(s, w, L, ws, d2, T, 1);
+      // tiles2 holds at most E * ceil(small_max / SMALL_MT) tiles, and at
+      // most one partial tile per expert beyond T * k / SMALL_MT full ones
+      const long b1 = (long)E * ((GEMM_SMALL_MAX + SMALL_MT - 1) / SMALL_MT);
+      const long b2 = (long)T * k / SMALL_MT + E;
+      small_bound = (int)(b1 < b2 ? b1 : b2);
+      HIP_TRY(launch_expert_stream(0, s->scale_dtype, sgu, small_bound, SGU_KBW, SGU_RG, SMALL_MT,
+                                   st));
+    }
+    pc->end(4);
+    g.w0 = w->w_down;
+    g.s0 = (const uint16_t *)w->s_down;
+    g.ws0 = w->ws_down;
+    g.ss0 = (const uint16_t *)w->ss_down;
+    g.w1 = nullptr;
+    g.s1 = nullptr;
+    g.ws1 = nullptr;
+    g.ss1 = nullptr;
+    g.a_routed = at<uint16_t>(ws, L.act);
+    g.a_shared = at<uint16_t>(ws, L.act_s);
+    g.o = at<uint16_t>(ws, L.o);
+    HIP_TRY(launch_expert_gemm(1, s->scale_dtype, g, gtiles, st));
+    if (d.small_max > 0) {
+      HIP_TRY(launch_expert_stream(1, s->scale_dtype, sdn, small_bound, SDN_KBW, SDN_RG, SMALL_MT,
+                                   st));
+    }
+    pc->end(5);
+    return AINFER_OK;
+  }
+  ExpertArgs a;
+  memset(&a, 0, sizeof a);
+  a.ptok = d.ptok;
+  a.tiles = d.tiles;
+  a.n_tiles = d.n_tiles;
+  a.T = T;
+  a.k = k;
+  a.E = E;
+  a.H = H;
+  a.I = s->inter;
+  a.Is = s->shared_inter;
+  const int smt = DEC_MT;  // tiles of the dispatch above
+  const int max_tiles = max_tiles_bound(*s, T, smt);
+  // k-groups per wave and 16-row groups per wave, measured at T = 1, 4, 16
+  const int kbw = 4, kbw_down = down_kbw(*s);
+  // gate/up + SiLU-mul
+  a.w0 = w->w_gate;
+  a.w1 = w->w_up;
+  a.s0 = (const uint16_t *)w->s_gate;
+  a.s1 = (const uint16_t *)w->s_up;
+  a.ws0 = w->ws_gate;
+  a.ws1 = w->ws_up;
+  a.ss0 = (const uint16_t *)w->ss_gate;
+  a.ss1 = (const uint16_t *)w->ss_up;
+  a.a_routed = at<uint16_t>(ws, L.xperm);
+  a.a_shared = at<uint16_t>(ws, L.xperm);
+  a.act = at<uint16_t>(ws, L.act);
+  a.act_s = at<uint16_t>(ws, L.act_s);
+  HIP_TRY(launch_expert_stream(0, s->scale_dtype, a, max_tiles, kbw, RG_GATE_UP, smt, st));
+  pc->end(4);
+  // down + combine
+  a.w0 = w->w_down;
+  a.s0 = (const uint16_t *)w->s_down;
+  a.ws0 = w->ws_down;
+  a.ss0 = (const uint16_t *)w->ss_down;
+  a.w1 = nullptr;
+  a.s1 = nullptr;
+  a.ws1 = nullptr;
+  a.ss1 = nullptr;
+  a.a_routed = at<uint16_t>(ws, L.act);
+  a.a_shared = at<uint16_t>(ws, L.act_s);
+  a.o = at<uint16_t>(ws, L.o);
+  HIP_TRY(launch_expert_stream(1, s->scale_dtype, a, max_tiles, kbw_down, RG_DOWN, smt, st));
+  pc->end(5);
+  return AINFER_OK;
+}
+
 int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const void *x,
                const void *resid, void *y, int T, void *ws, hipStream_t st,
                ProfCall *pc, const NormIn *norm = nullptr) {
@@ -468,121 +592,9 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
     HIP_TRY(launch_dispatch(at<int32_t>(ws, L.idx), T, k, E, mt, has_shared,
                             at<int32_t>(ws, L.chunk_counts), at<int32_t>(ws, L.rank), d, st));
   pc->end(3);
-  if (gemm) {
-    GemmArgs g;
-    memset(&g, 0, sizeof g);
-    g.ptok = d.ptok;
-    g.tiles = d.tiles;
-    g.n_tiles = d.n_tiles;
-    g.T = T;
-    g.k = k;
-    g.E = E;
-    g.H = H;
-    g.I = s->inter;
-    g.Is = s->shared_inter;
-    g.xsum = at<float>(ws, L.xsum);
-    g.asum = at<float>(ws, L.asum);
-    g.asum_s = at<float>(ws, L.asum_s);
-    const int gtiles = max_tiles_bound(*s, T, GEMM_MT);
-    g.w0 = w->w_gate;
-    g.w1 = w->w_up;
-    g.s0 = (const uint16_t *)w->s_gate;
-    g.s1 = (const uint16_t *)w->s_up;
-    g.ws0 = w->ws_gate;
-    g.ws1 = w->ws_up;
-    g.ss0 = (const uint16_t *)w->ss_gate;
-    g.ss1 = (const uint16_t *)w->ss_up;
-    g.a_routed = at<uint16_t>(ws, L.xperm);
-    g.act = at<uint16_t>(ws, L.act);
-    g.act_s = at<uint16_t>(ws, L.act_s);
-    HIP_TRY(launch_expert_gemm(0, s->scale_dtype, g, gtiles, st));
-    ExpertArgs sgu, sdn;
-    int small_bound = 0;
-    if (d.small_max > 0) {
-      DispatchOut d2 = d;
-      d2.tiles = d.tiles2;
-      d2.n_tiles = d.n_tiles2;
-      sgu = expert_args(s, w, L, ws, d2, T, 0);
-      sdn = expert_args(s, w, L, ws, d2, T, 1);
-      // tiles2 holds at most E * ceil(small_max / SMALL_MT) tiles, and at
-      // most one partial tile per expert beyond T * k / SMALL_MT full ones
-      const long b1 = (long)E * ((GEMM_SMALL_MAX + SMALL_MT - 1) / SMALL_MT);
-      const long b2 = (long)T * k / SMALL_MT + E;
-      small_bound = (int)(b1 < b2 ? b1 : b2);
-      HIP_TRY(launch_expert_stream(0, s->scale_dtype, sgu, small_bound, SGU_KBW, SGU_RG, SMALL_MT,
-                                   st));
-    }
-    pc->end(4);
-    g.w0 = w->w_down;
-    g.s0 = (const uint16_t *)w->s_down;
-    g.ws0 = w->ws_down;
-    g.ss0 = (const uint16_t *)w->ss_down;
-    g.w1 = nullptr;
-    g.s1 = nullptr;
-    g.ws1 = nullptr;
-    g.ss1 = nullptr;
-    g.a_routed = at<uint16_t>(ws, L.act);
-    g.a_shared = at<uint16_t>(ws, L.act_s);
-    g.o = at<uint16_t>(ws, L.o);
-    HIP_TRY(launch_expert_gemm(1, s->scale_dtype, g, gtiles, st));
-    if (d.small_max > 0) {
-      HIP_TRY(launch_expert_stream(1, s->scale_dtype, sdn, small_bound, SDN_KBW, SDN_RG, SMALL_MT,
-                                   st));
-    }
-    pc->end(5);
-    HIP_TRY(launch_combine(at<uint16_t>(ws, L.o), d.inv, at<float>(ws, L.w), at<float>(ws, L.sg),
-                           has_shared, resid, y, T, k, H,
-                           at<int32_t>(ws, L.sync) + SY_ERR, st));
-    pc->end(6);
-    return AINFER_OK;
-  }
-  ExpertArgs a;
-  memset(&a, 0, sizeof a);
-  a.ptok = d.ptok;
-  a.tiles = d.tiles;
-  a.n_tiles = d.n_tiles;
-  a.T = T;
-  a.k = k;
-  a.E = E;
-  a.H = H;
-  a.I = s->inter;
-  a.Is = s->shared_inter;
-  const int smt = DEC_MT;  // tiles of the dispatch above
-  const int max_tiles = max_tiles_bound(*s, T, smt);
-  // k-groups per wave and 16-row groups per wave, measured at T = 1, 4, 16
-  const int kbw = 4, kbw_down = down_kbw(*s);
-  // gate/up + SiLU-mul
-  a.w0 = w->w_gate;
-  a.w1 = w->w_up;
-  a.s0 = (const uint16_t *)w->s_gate;
-  a.s1 = (const uint16_t *)w->s_up;
-  a.ws0 = w->ws_gate;
-  a.ws1 = w->ws_up;
-  a.ss0 = (const uint16_t *)w->ss_gate;
-  a.ss1 = (const uint16_t *)w->ss_up;
-  a.a_routed = at<uint16_t>(ws, L.xperm);
-  a.a_shared = at<uint16_t>(ws, L.xperm);
-  a.act = at<uint16_t>(ws, L.act);
-  a.act_s = at<uint16_t>(ws, L.act_s);
-  HIP_TRY(launch_expert_stream(0, s->scale_dtype, a, max_tiles, kbw, RG_GATE_UP, smt, st));
-  pc->end(4);
-  // down + combine
-  a.w0 = w->w_down;
-  a.s0 = (const uint16_t *)w->s_down;
-  a.ws0 = w->ws_down;
-  a.ss0 = (const uint16_t *)w->ss_down;
-  a.w1 = nullptr;
-  a.s1 = nullptr;
-  a.ws1 = nullptr;
-  a.ss1 = nullptr;
-  a.a_routed = at<uint16_t>(ws, L.act);
-  a.a_shared = at<uint16_t>(ws, L.act_s);
-  a.o = at<uint16_t>(ws, L.o);
-  HIP_TRY(launch_expert_stream(1, s->scale_dtype, a, max_tiles, kbw_down, RG_DOWN, smt, st));
-  pc->end(5);
+  HIP_TRY_RC(run_experts(s, w, L, ws, d, T, gemm, st, pc));
   HIP_TRY(launch_combine(at<uint16_t>(ws, L.o), d.inv, at<float>(ws, L.w), at<float>(ws, L.sg),
-                         has_shared, resid, y, T, k, H,
-                           at<int32_t>(ws, L.sync) + SY_ERR, st));
+                         has_shared, resid, y, T, k, H, at<int32_t>(ws, L.sync) + SY_ERR, st));
   pc->end(6);
   return AINFER_OK;
 }
@@ -907,6 +919,53 @@ int ainfer_moe_route(const ainfer_moe_shape *s, const ainfer_moe_weights *w, con
                        topk_idx + (size_t)t0 * k, topk_w + (size_t)t0 * k, shared_gate + t0,
                        logits ? logits + (size_t)t0 * E : nullptr, ws, (hipStream_t)stream)))
       return rc;
+  return AINFER_OK;
+}
+
+int ainfer_moe_experts(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const void *x,
+                       const int32_t *topk_idx, int32_t T, void *o, void *ws, size_t ws_bytes,
+                       void *stream) {
+  int rc = ainfer_moe_validate(s);
+  if (rc) return rc;
+  if (s->precision != AINFER_PRECISION_W4A16) return AINFER_ERR_ARG;
+  if (T < 0 || T > AINFER_MOE_CHUNK_TOKENS) return AINFER_ERR_TOKENS;
+  if ((rc = check_weights(s, w))) return rc;
+  if (T == 0) return AINFER_OK;
+  if (!x || !topk_idx || !o) return AINFER_ERR_NULL;
+  if ((uintptr_t)x % 16 || (uintptr_t)o % 16) return AINFER_ERR_ARG;
+  if ((rc = check_ws(s, T, ws, ws_bytes))) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  const Layout L = layout_of(*s, T);
+  const int H = s->hidden, k = s->top_k, has_shared = s->shared_inter > 0;
+  const bool gemm = T >= GEMM_MIN_T;
+  DispatchOut d = dispatch_out(s, L, ws, T);
+  d.mt = gemm ? GEMM_MT : DEC_MT;
+  if (gemm) d.small_max = GEMM_SMALL_MAX;
+  ProfCall pc(st);
+  pc.start();
+  HIP_TRY(launch_xperm(x, at<uint16_t>(ws, L.xperm), gemm ? at<float>(ws, L.xsum) : nullptr, T,
+                       H, st));
+  HIP_TRY(launch_dispatch(topk_idx, T, k, s->n_experts, d.mt, has_shared,
+                          at<int32_t>(ws, L.chunk_counts), at<int32_t>(ws, L.rank), d, st));
+  pc.end(3);
+  HIP_TRY_RC(run_experts(s, w, L, ws, d, T, gemm, st, &pc));
+  HIP_TRY(launch_gather_rows(at<uint16_t>(ws, L.o), d.inv, o, T, k, H, has_shared, st));
+  return AINFER_OK;
+}
+
+int ainfer_moe_combine(const ainfer_moe_shape *s, const void *o, const float *topk_w,
+                       const float *shared_gate, const void *resid, void *y, int32_t T,
+                       void *stream) {
+  int rc = ainfer_moe_validate(s);
+  if (rc) return rc;
+  if (T < 0 || T > AINFER_MOE_MAX_TOKENS) return AINFER_ERR_TOKENS;
+  if (T == 0) return AINFER_OK;
+  const int has_shared = s->shared_inter > 0;
+  if (!o || !topk_w || !y || (has_shared && !shared_gate)) return AINFER_ERR_NULL;
+  if ((uintptr_t)o % 16 || (uintptr_t)y % 16 || (resid && (uintptr_t)resid % 16))
+    return AINFER_ERR_ARG;
+  HIP_TRY(launch_combine((const uint16_t *)o, nullptr, topk_w, shared_gate, has_shared, resid, y,
+                         T, s->top_k, s->hidden, nullptr, (hipStream_t)stream));
   return AINFER_OK;
 }
 

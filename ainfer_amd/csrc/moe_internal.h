@@ -107,6 +107,12 @@ constexpr int EXACT_ROUTER_MAX_T = 16;
 hipError_t launch_dispatch(const int32_t *idx, int T, int k, int E, int mt, int has_shared,
                            int32_t *chunk_counts, int32_t *rank, const DispatchOut &ds,
                            hipStream_t s);
+// x in MFMA order (+ its per-128 group sums when xsum is non-null)
+hipError_t launch_xperm(const void *x, void *xperm, float *xsum, int T, int H, hipStream_t s);
+// expert output rows from dispatch-position order to slot order (H % 8 == 0)
+hipError_t launch_gather_rows(const void *src, const int32_t *inv, void *dst, int T, int k,
+                              int H, int has_shared, hipStream_t s);
+// inv null: o's routed rows are in slot order (row t * k + j)
 hipError_t launch_combine(const uint16_t *o, const int32_t *inv, const float *w, const float *sg,
                           int has_shared, const void *resid, void *y, int T, int k, int H,
                           const int32_t *err, hipStream_t s);

@@ -470,7 +470,7 @@ __global__ __launch_bounds__(256) void k_combine(const uint16_t *__restrict__ o,
 #pragma unroll
   for (int j = 0; j < 32; ++j)
     if (j < k) {
-      pos[j] = inv[(size_t)t * k + j];
+      pos[j] = inv ? inv[(size_t)t * k + j] : t * k + j;  // null: rows in slot order
       wj[j] = w[(size_t)t * k + j];
     }
   float acc[CPT];
@@ -517,6 +517,42 @@ __global__ __launch_bounds__(256) void k_combine(const uint16_t *__restrict__ o,
     for (int q = 0; q < CPT / 2; ++q) out[q] = 0x7FC07FC0u;
   }
   *(vec_t *)(y + (size_t)t * H + h0) = out;
+}
+
+// x in MFMA order and (xsum non-null) its per-128 group sums: one wave per
+// token, the copy the routers write beside their logits
+__global__ __launch_bounds__(256) void k_xperm(const uint16_t *__restrict__ x,
+                                               uint16_t *__restrict__ xperm,
+                                               float *__restrict__ xsum, int T, int H) {
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (t < T) write_xperm(x + (size_t)t * H, xperm, xsum, t, H, lane);
+}
+
+hipError_t launch_xperm(const void *x, void *xperm, float *xsum, int T, int H, hipStream_t s) {
+  if (T == 0) return hipSuccess;
+  k_xperm<<<(T + 3) / 4, 256, 0, s>>>((const uint16_t *)x, (uint16_t *)xperm, xsum, T, H);
+  return hipGetLastError();
+}
+
+// dst row t * k + j = src row inv[t * k + j] (dispatch position -> slot
+// order); rows T * k + t (the shared expert's) copied as they are
+__global__ __launch_bounds__(256) void k_gather_rows(const uint16_t *__restrict__ src,
+                                                     const int32_t *__restrict__ inv,
+                                                     uint16_t *__restrict__ dst, int T, int k,
+                                                     int H) {
+  const int r = blockIdx.x;
+  const size_t from = r < T * k ? (size_t)inv[r] : (size_t)r;
+  const u32x4 *a = (const u32x4 *)(src + from * H);
+  u32x4 *b = (u32x4 *)(dst + (size_t)r * H);
+  for (int i = threadIdx.x; i < H / 8; i += blockDim.x) b[i] = a[i];
+}
+
+hipError_t launch_gather_rows(const void *src, const int32_t *inv, void *dst, int T, int k,
+                              int H, int has_shared, hipStream_t s) {
+  const int rows = T * k + (has_shared ? T : 0);
+  if (rows == 0) return hipSuccess;
+  k_gather_rows<<<rows, 256, 0, s>>>((const uint16_t *)src, inv, (uint16_t *)dst, T, k, H);
+  return hipGetLastError();
 }
 
 hipError_t launch_combine(const uint16_t *o, const int32_t *inv, const float *w, const float *sg,

@@ -127,6 +127,22 @@ class MoeLayer:
                                          ws.numel(), _stream(stream)))
         return idx, w, sg, lg
 
+    def experts(self, x, idx, ws, stream=None):
+        """Expert rows in slot order: [T * k + T][H] bf16 (row t * k + j =
+        expert idx[t][j] on token t, row T * k + t = the shared expert)."""
+        T, k, H = x.shape[0], self.cfg.top_k, self.cfg.hidden
+        o = torch.empty(T * k + T, H, dtype=torch.bfloat16, device=self.device)
+        L.check(L.lib().ainfer_moe_experts(C.byref(self.shape), C.byref(self.weights), _ptr(x),
+                                           _ptr(idx), T, _ptr(o), _ptr(ws), ws.numel(),
+                                           _stream(stream)))
+        return o
+
+    def combine(self, o, w, sg, y, resid=None, stream=None):
+        T = y.shape[0]
+        L.check(L.lib().ainfer_moe_combine(C.byref(self.shape), _ptr(o), _ptr(w), _ptr(sg),
+                                           _ptr(resid), _ptr(y), T, _stream(stream)))
+        return y
+
     def dispatch(self, idx, ws, stream=None):
         T, E, k = idx.shape[0], self.cfg.n_experts, self.cfg.top_k
         dev = self.device

@@ -261,6 +261,27 @@ int ainfer_moe_dispatch(const ainfer_moe_shape *shape,
                         int32_t *offsets, int32_t *perm, int32_t *inv_perm,
                         void *workspace, size_t workspace_bytes, void *stream);
 
+/* Expert stage alone (W4A16, T <= AINFER_MOE_CHUNK_TOKENS), for routing the
+ * caller computed (ainfer_moe_route or its own): o[T*k + T][H] bf16, 16-byte
+ * aligned; row t*k + j is expert topk_idx[t][j] applied to token t (gate/up,
+ * SiLU-mul, down), row T*k + t the shared expert on token t (unused without
+ * one).  The kernels and arithmetic of ainfer_moe_forward's expert stage at
+ * the same T (for T <= 2 forward fuses the stages and splits K differently;
+ * there the rows agree within the layer tolerance).  No reference counterpart
+ * (the reference is dense); the per-expert MLP is decode_l0.cpp:663-674's. */
+int ainfer_moe_experts(const ainfer_moe_shape *shape,
+                       const ainfer_moe_weights *weights, const void *x,
+                       const int32_t *topk_idx, int32_t T, void *o,
+                       void *workspace, size_t workspace_bytes, void *stream);
+
+/* Combine: y[t] = bf16(sum_j topk_w[t][j] * o[t*k + j] + shared_gate[t] *
+ * o[T*k + t] (+ resid[t])), fp32 fma in slot order, as ainfer_moe_forward;
+ * o as ainfer_moe_experts writes it, resid NULL or [T][H] bf16 (the residual
+ * add of ResAddF, kernels.cpp:646-652).  16-byte aligned rows. */
+int ainfer_moe_combine(const ainfer_moe_shape *shape, const void *o,
+                       const float *topk_w, const float *shared_gate,
+                       const void *resid, void *y, int32_t T, void *stream);
+
 /* RMSNorm over rows: y[T][H] bf16 = x * 1/sqrt(mean(x^2) + eps) * w
  * (norm_mode PLAIN) or * (1 + w) (ONE_PLUS); w bf16 [H] or NULL (unit).
  * Sum of squares in fp64, as RMSNormW (kernels.cpp:73-116). */

@@ -84,6 +84,34 @@ def test_forward_rejects_bad_arguments_without_gpu(L):
     assert L.lib().ainfer_moe_strerror(L.ERR_WORKSPACE).startswith(b"workspace")
 
 
+def test_stage_entries_reject_bad_arguments_without_gpu(L):
+    lib = L.lib()
+    s = shape(L)
+    fake = C.c_void_p(0x1000)
+    w = L.Weights(*([fake] * len(L.Weights._fields_)))
+    # experts: one chunk at most, W4A16 only, 16-byte aligned x and o, a real workspace
+    assert lib.ainfer_moe_experts(C.byref(s), C.byref(w), fake, fake, 4097, fake, fake, 1 << 40,
+                                  None) == L.ERR_TOKENS
+    assert lib.ainfer_moe_experts(C.byref(s), C.byref(w), None, fake, 1, fake, fake, 1 << 40,
+                                  None) == L.ERR_NULL
+    assert lib.ainfer_moe_experts(C.byref(s), C.byref(w), fake, fake, 1, C.c_void_p(0x1008), fake,
+                                  1 << 40, None) == L.ERR_ARG
+    assert lib.ainfer_moe_experts(C.byref(s), C.byref(w), fake, fake, 1, fake, fake, 16,
+                                  None) == L.ERR_WORKSPACE
+    s8 = shape(L)
+    s8.precision = L.PRECISION_W4A8
+    assert lib.ainfer_moe_experts(C.byref(s8), C.byref(w), fake, fake, 1, fake, fake, 1 << 40,
+                                  None) == L.ERR_ARG
+    assert lib.ainfer_moe_experts(C.byref(s), C.byref(w), None, None, 0, None, None, 0, None) == L.OK
+    # combine: the shared gate is required with a shared expert; aligned rows
+    assert lib.ainfer_moe_combine(C.byref(s), fake, fake, None, None, fake, 1, None) == L.ERR_NULL
+    assert lib.ainfer_moe_combine(C.byref(s), fake, fake, fake, C.c_void_p(0x1004), fake, 1,
+                                  None) == L.ERR_ARG
+    assert lib.ainfer_moe_combine(C.byref(s), fake, fake, fake, None, fake, -1, None) == L.ERR_TOKENS
+    assert lib.ainfer_moe_combine(C.byref(shape(L, top_k=0)), fake, fake, fake, None, fake, 1,
+                                  None) == L.ERR_SHAPE
+
+
 def test_missing_library_fails_loudly(L, monkeypatch, tmp_path):
     monkeypatch.setattr(L, "LIB_PATH", tmp_path / "nope.so")
     monkeypatch.setattr(L, "_lib", None)

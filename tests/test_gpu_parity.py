@@ -507,3 +507,41 @@ def test_block_forward_heavy_tailed_residual(torch, oracle):
         want = hl.block_forward(to_np(x), T, norm_w=to_np(nw), mode=L.NORM_PLAIN)
         check_close(to_np(out), oracle.bf16_to_f32(want), f"heavy block T={T}")
     assert layer.workspace_check(ws) == 0
+
+
+@pytest.mark.parametrize("name,T", [("c1", 1), ("c1", 4), ("c1", 16), ("c1", 100), ("c1", 300),
+                                    ("c3", 64)])
+def test_stage_entries_compose_to_forward(torch, oracle, name, T):
+    """ainfer_moe_route -> ainfer_moe_experts -> ainfer_moe_combine: within
+    the layer tolerance of the oracle at every T, bit-identical to
+    ainfer_moe_forward where forward runs the same expert kernels (T >= 3;
+    at T <= 2 it fuses the stages), and with the residual bit-identical to
+    block_forward where that normalizes with the separate kernel (T > 4)."""
+    from ainfer_amd.moe import make_input, rmsnorm
+    print(f"[case] stage entries {name} T={T}", flush=True)
+    layer = get_layer(torch, name)
+    x = make_input(layer.cfg, T, tag=600 + T)
+    ws = layer.workspace(T)
+    idx, w, sg, _ = layer.route(x, ws)
+    o = layer.experts(x, idx, ws)
+    y2 = torch.empty(T, layer.cfg.hidden, dtype=torch.bfloat16, device="cuda")
+    layer.combine(o, w, sg, y2)
+    y = torch.empty_like(y2)
+    layer.forward(x, y, ws)
+    torch.cuda.synchronize()
+    ref = host_copy(oracle, layer).forward(to_np(x), T)
+    check_close(to_np(y2), ref, f"stages {name} T={T}")
+    if T >= 3:
+        assert torch.equal(y2.view(torch.int16), y.view(torch.int16)), "stages differ from forward"
+    if T > 4:
+        r = x * 3
+        h = torch.empty_like(r)
+        rmsnorm(r, h)
+        idx, w, sg, _ = layer.route(h, ws)
+        o = layer.experts(h, idx, ws)
+        y3 = torch.empty_like(r)
+        layer.combine(o, w, sg, y3, resid=r)
+        yb = torch.empty_like(r)
+        layer.block_forward(r, yb, ws)
+        torch.cuda.synchronize()
+        assert torch.equal(y3.view(torch.int16), yb.view(torch.int16)), "stages differ from block"
