@@ -255,14 +255,18 @@ int ainfer_moe_route(const ainfer_moe_shape *shape,
 
 /* Dispatch (T <= AINFER_MOE_CHUNK_TOKENS): counts[E], offsets[E+1] (exclusive scan of counts),
  * perm[T*k] (position p holds t*k + j, expert-contiguous, token ascending
- * within an expert) and inv_perm[T*k] (inverse of perm). */
+ * within an expert) and inv_perm[T*k] (inverse of perm).  Each row of
+ * topk_idx must hold k distinct expert ids in [0, E), as ainfer_moe_route
+ * writes them; the contents are not checked (other values are undefined
+ * behaviour, including out-of-bounds device accesses). */
 int ainfer_moe_dispatch(const ainfer_moe_shape *shape,
                         const int32_t *topk_idx, int32_t T, int32_t *counts,
                         int32_t *offsets, int32_t *perm, int32_t *inv_perm,
                         void *workspace, size_t workspace_bytes, void *stream);
 
 /* Expert stage alone (W4A16, T <= AINFER_MOE_CHUNK_TOKENS), for routing the
- * caller computed (ainfer_moe_route or its own): o[T*k + T][H] bf16, 16-byte
+ * caller computed (ainfer_moe_route or its own; topk_idx as for
+ * ainfer_moe_dispatch: k distinct ids in [0, E) per row, not checked): o[T*k + T][H] bf16, 16-byte
  * aligned; row t*k + j is expert topk_idx[t][j] applied to token t (gate/up,
  * SiLU-mul, down), row T*k + t the shared expert on token t (unused without
  * one).  The kernels and arithmetic of ainfer_moe_forward's expert stage at
