@@ -358,7 +358,8 @@ def run_c4(steps, tokens=(1, 8), warmup=3, keep_layer0=False, stack=True):
 
 def measured_peaks():
     """What this box sustains, beside the spec peaks: a 1 GiB device copy
-    (read + write bytes) and a bf16 8192^3 GEMM through the vendor BLAS."""
+    (read + write bytes), a bf16 8192^3 GEMM through the vendor BLAS, and the
+    MFMA rate of a loop with a given VALU load (ainfer_moe_mfma_probe)."""
     import torch
     n = 1 << 30
     src = torch.ones(n, dtype=torch.uint8, device="cuda")
@@ -389,9 +390,24 @@ def measured_peaks():
     tfs = 2 * m ** 3 * 10 / (t0.elapsed_time(t1) * 1e-3) / 1e12
     del a, b, c
     torch.cuda.empty_cache()
+    # the bf16 MFMA rate with 0-4 fp32 VALU instructions issued per MFMA, 1
+    # and 2 waves per SIMD: the ceiling of an MFMA main loop that spends that
+    # much VALU work (the prefill GEMM's dequantisation and scale step)
+    import ctypes as C
+    from ainfer_amd import _lib
+    mf = {}
+    for wps in (1, 2):
+        for nv in range(5):
+            r = C.c_float()
+            rc = _lib.lib().ainfer_moe_mfma_probe(nv, wps, 4000, C.c_void_p(torch.cuda.current_stream().cuda_stream),
+                                                  C.byref(r))
+            if rc != _lib.OK:
+                raise RuntimeError(f"ainfer_moe_mfma_probe failed: {rc}")
+            mf[f"w{wps}_v{nv}"] = round(r.value, 1)
     return {"hbm_copy_gbs": round(copy_gbs, 1), "hbm_copy_frac_of_spec": round(copy_gbs / HBM_PEAK_GBS, 4),
             "bf16_gemm_8192_tflops": round(tfs, 1),
-            "bf16_gemm_frac_of_spec": round(tfs / MFMA_BF16_PEAK_TFS, 4)}
+            "bf16_gemm_frac_of_spec": round(tfs / MFMA_BF16_PEAK_TFS, 4),
+            "mfma_probe_tflops_waves_per_simd_valu_per_mfma": mf}
 
 
 def host_cpu():

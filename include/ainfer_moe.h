@@ -410,6 +410,15 @@ int ainfer_moe_profile_read(float *stage_us, int32_t n_stages, int32_t *n_calls)
  * measurement aid for roofline figures. */
 int ainfer_moe_profile_kernel(float *gate_up_us, int32_t *n_launches);
 
+/* The MFMA ceiling of a main loop: every wave of one block per CU
+ * (waves_per_simd in 1..4 per SIMD) issues iters x 16 independent
+ * v_mfma_f32_16x16x32_bf16 with valu_per_mfma (0..4) independent fp32 FMAs
+ * after each; *tflops receives the bf16 MFMA rate of the second of two
+ * launches on `stream` (host-synchronous).  No counterpart in the reference:
+ * a measurement aid for the prefill GEMM's roofline. */
+int ainfer_moe_mfma_probe(int32_t valu_per_mfma, int32_t waves_per_simd, int32_t iters,
+                          void *stream, float *tflops);
+
 #ifdef __cplusplus
 }
 #endif

@@ -112,6 +112,15 @@ def test_stage_entries_reject_bad_arguments_without_gpu(L):
                                   None) == L.ERR_SHAPE
 
 
+
+def test_mfma_probe_rejects_bad_arguments_without_gpu(L):
+    r = C.c_float()
+    lib = L.lib()
+    for args in ((5, 1, 10), (-1, 1, 10), (0, 0, 10), (0, 5, 10), (0, 1, 0), (0, 1, 1 << 21)):
+        assert lib.ainfer_moe_mfma_probe(*args, None, C.byref(r)) == L.ERR_ARG, args
+    assert lib.ainfer_moe_mfma_probe(0, 1, 10, None, None) == L.ERR_ARG
+
+
 def test_missing_library_fails_loudly(L, monkeypatch, tmp_path):
     monkeypatch.setattr(L, "LIB_PATH", tmp_path / "nope.so")
     monkeypatch.setattr(L, "_lib", None)
