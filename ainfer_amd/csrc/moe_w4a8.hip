@@ -243,7 +243,7 @@ __global__ __launch_bounds__(GV_WAVES * 64) void k_int4_gemv_i8(
 #define GV1_RW 2  // rows per wave (2: 10.0 us at 17408 x 5120; 1: 12.1, 4: 10.9, 8: 13.0)
 #endif
 #ifndef GV1_WAVES
-#define GV1_WAVES 4  // waves per block
+#define GV1_WAVES 4  // waves per block (4: 10.0-10.3 us at 17408 x 5120; 2: 10.0, 8: 10.6, 16: 12.9)
 #endif
 
 // Rows [m0, m0 + GV1_RW) of NMAT matrices P[j] / S[j] (M rows, K columns)
