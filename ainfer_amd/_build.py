@@ -13,7 +13,7 @@ LIB = PKG / "libainfer_moe.so"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 SOURCES = ["moe_api.hip", "moe_route.hip", "moe_router.hip", "moe_expert.hip", "moe_gemm.hip",
-           "moe_decode.hip", "moe_w4a8.hip", "moe_stack.hip", "moe_binfer.cpp"]
+           "moe_decode.hip", "moe_w4a8.hip", "moe_stack.hip", "moe_probe.hip", "moe_binfer.cpp"]
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

@@ -31,7 +31,7 @@ EXPORTS = (
     "ainfer_moe_dispatch", "ainfer_moe_experts", "ainfer_moe_combine", "ainfer_moe_rmsnorm", "ainfer_moe_fill",
     "ainfer_moe_act_quant_i8", "ainfer_moe_int4_gemv_i8",
     "ainfer_moe_profile_enable", "ainfer_moe_profile_read", "ainfer_moe_profile_kernel", "ainfer_moe_debug_spin_limit",
-    "ainfer_moe_mfma_probe",
+    "ainfer_moe_mfma_probe", "ainfer_moe_read_probe",
     "ainfer_binfer_open", "ainfer_binfer_close", "ainfer_binfer_error", "ainfer_binfer_moe_info",
     "ainfer_binfer_moe_layer_bytes", "ainfer_binfer_load_moe_layer",
 )
@@ -95,6 +95,7 @@ def lib():
         L.ainfer_moe_profile_enable.argtypes = [I32]
         L.ainfer_moe_profile_kernel.argtypes = [C.POINTER(C.c_float), C.POINTER(I32)]
         L.ainfer_moe_mfma_probe.argtypes = [I32, I32, I32, P, C.POINTER(C.c_float)]
+        L.ainfer_moe_read_probe.argtypes = [P, C.c_uint64, I32, I32, I32, P, C.POINTER(C.c_float)]
         L.ainfer_binfer_open.argtypes = [C.c_char_p, C.POINTER(P), C.c_char_p, SZ]
         L.ainfer_binfer_close.restype = None
         L.ainfer_binfer_close.argtypes = [P]

@@ -140,9 +140,12 @@ struct Entry {
   uint32_t group = 0;
   uint64_t sc_off = 0, sc_bytes = 0, d_off = 0, d_bytes = 0;
   uint32_t crc = 0;
+  // Element count, or UINT64_MAX when the product of the dims overflows 64 bits
+  // (every caller then rejects the shape as implausible).
   uint64_t numel() const {
     uint64_t n = 1;
-    for (int i = 0; i < ndim; ++i) n *= shape[i];
+    for (int i = 0; i < ndim; ++i)
+      if (__builtin_mul_overflow(n, shape[i], &n)) return UINT64_MAX;
     return n;
   }
 };
@@ -239,7 +242,9 @@ int validate(ainfer_binfer *b) {
     if (c != scrc[id]) return fail(b, "section " + std::to_string(id) + " CRC mismatch");
     if (id == 2) b->arch.assign(body.begin(), body.end());
   }
-  if (sbytes[5] != n * DIR_ENTRY)
+  // n is checked against the section size before it is multiplied, so a crafted count
+  // cannot wrap n * 192 onto the section's byte count.
+  if (n > sbytes[5] / DIR_ENTRY || sbytes[5] != n * DIR_ENTRY)
     return fail(b, "dir size mismatch: tensor_count " + std::to_string(n) + " x 192 != " +
                        std::to_string(sbytes[5]));
   std::vector<uint8_t> dir(sbytes[5]);
@@ -457,7 +462,13 @@ int ainfer_binfer_open(const char *path, ainfer_binfer **out, char *err, size_t 
   } else {
     fseeko(b->f, 0, SEEK_END);
     b->size = (uint64_t)ftello(b->f);
-    rc = validate(b);
+    // The validator reports a bad file through its return code; an exception from it
+    // (an allocation a damaged file would size) must not cross the C ABI.
+    try {
+      rc = validate(b);
+    } catch (...) {
+      rc = fail(b, "file rejected: a directory or section size the validator cannot hold");
+    }
   }
   if (rc != AINFER_OK) {
     if (err && err_len) snprintf(err, err_len, "%s", b->err.c_str());

@@ -275,6 +275,10 @@ def run_c4(steps, tokens=(1, 8), warmup=3, keep_layer0=False, stack=True):
         t1.record()
         torch.cuda.synchronize()
         us = t0.elapsed_time(t1) * 1e3 / steps
+        # a bounded device wait that ran out leaves NaN rows: such a step is not a result
+        if not bool(torch.isfinite(y).all()):
+            raise RuntimeError(f"c4 T={T}: the 60-block residual is not finite")
+        L.check(layers[0].workspace_check(ws))
         # profiled pass: mean device time per stage and block
         L.profile_enable(True)
         for s in range(steps):
@@ -312,6 +316,8 @@ def run_c4(steps, tokens=(1, 8), warmup=3, keep_layer0=False, stack=True):
             t1.record()
             torch.cuda.synchronize()
             stack_us = round(t0.elapsed_time(t1) * 1e3 / steps, 1)
+            if not bool(torch.isfinite(y).all()):
+                raise RuntimeError(f"c4 T={T}: the one-launch stack's residual is not finite")
             del stk, sws
         w8_us = None
         if T == 1:
@@ -356,6 +362,21 @@ def run_c4(steps, tokens=(1, 8), warmup=3, keep_layer0=False, stack=True):
     return out, keep
 
 
+def add_read_roof_fracs(details, read_gbs):
+    """Beside every decode line's fraction of the 8 TB/s spec, its fraction of
+    the read roof this box sustained in the same run (hbm_read_gbs)."""
+    for d in (details.get("c4_stack60") or {}).values():
+        d["hbm_frac_of_read_roof"] = round(d["hbm_gbs"] / read_gbs, 4)
+    for d in (details.get("decode_c1") or {}).values():
+        d["layer_hbm_frac_of_read_roof"] = round(d["layer_hbm_gbs"] / read_gbs, 4)
+    c3 = details.get("c3_T64")
+    if c3:
+        c3["layer_hbm_frac_of_read_roof"] = round(c3["layer_hbm_frac"] * HBM_PEAK_GBS / read_gbs, 4)
+    g = details.get("gemv_w4a8")
+    if g:
+        g["gemv_hbm_frac_of_read_roof"] = round(g["gemv_hbm_frac"] * HBM_PEAK_GBS / read_gbs, 4)
+
+
 def measured_peaks():
     """What this box sustains, beside the spec peaks: a 1 GiB device copy
     (read + write bytes), a bf16 8192^3 GEMM through the vendor BLAS, and the
@@ -376,6 +397,26 @@ def measured_peaks():
     torch.cuda.synchronize()
     copy_gbs = 2 * n * 10 / (t0.elapsed_time(t1) * 1e-3) / 1e9
     del src, dst
+    # read-only roof: the decode path streams weights and writes almost
+    # nothing; random bytes over 4 GiB (far beyond the 256 MB MALL), best of a
+    # sweep over loads in flight per lane and blocks per CU
+    import ctypes as C
+    from ainfer_amd import _lib
+    nr = 4 << 30
+    rbuf = torch.randint(0, 256, (nr,), dtype=torch.uint8, device="cuda")
+    torch.cuda.synchronize()
+    read = {}
+    for unroll in (4, 8, 16):
+        for bpc in (2, 4, 8):
+            r = C.c_float()
+            rc = _lib.lib().ainfer_moe_read_probe(C.c_void_p(rbuf.data_ptr()), nr, unroll, bpc, 5,
+                                                  C.c_void_p(torch.cuda.current_stream().cuda_stream),
+                                                  C.byref(r))
+            if rc != _lib.OK:
+                raise RuntimeError(f"ainfer_moe_read_probe failed: {rc}")
+            read[f"u{unroll}_b{bpc}"] = round(r.value, 1)
+    del rbuf
+    torch.cuda.empty_cache()
     m = 8192
     a = torch.randn(m, m, device="cuda", dtype=torch.bfloat16)
     b = torch.randn(m, m, device="cuda", dtype=torch.bfloat16)
@@ -393,8 +434,6 @@ def measured_peaks():
     # the bf16 MFMA rate with 0-4 fp32 VALU instructions issued per MFMA, 1
     # and 2 waves per SIMD: the ceiling of an MFMA main loop that spends that
     # much VALU work (the prefill GEMM's dequantisation and scale step)
-    import ctypes as C
-    from ainfer_amd import _lib
     mf = {}
     for wps in (1, 2):
         for nv in range(5):
@@ -404,7 +443,10 @@ def measured_peaks():
             if rc != _lib.OK:
                 raise RuntimeError(f"ainfer_moe_mfma_probe failed: {rc}")
             mf[f"w{wps}_v{nv}"] = round(r.value, 1)
+    read_gbs = max(read.values())
     return {"hbm_copy_gbs": round(copy_gbs, 1), "hbm_copy_frac_of_spec": round(copy_gbs / HBM_PEAK_GBS, 4),
+            "hbm_read_gbs": read_gbs, "hbm_read_frac_of_spec": round(read_gbs / HBM_PEAK_GBS, 4),
+            "hbm_read_sweep_gbs_unroll_blocks_per_cu": read,
             "bf16_gemm_8192_tflops": round(tfs, 1),
             "bf16_gemm_frac_of_spec": round(tfs / MFMA_BF16_PEAK_TFS, 4),
             "mfma_probe_tflops_waves_per_simd_valu_per_mfma": mf}
@@ -590,6 +632,8 @@ def main():
         "c3_T64": c3,
         "measured_peaks": peaks,
     }
+    if peaks:
+        add_read_roof_fracs(details, peaks["hbm_read_gbs"])
     if c4 is None:
         print(json.dumps(details), flush=True)
         return
@@ -622,6 +666,8 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(dom["gbs"], 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4),
+                     "frac_of_read_roof": (round(dom["gbs"] / peaks["hbm_read_gbs"], 4)
+                                           if peaks else None),
                      "traffic": measured_traffic(dom["file"], f"c4_T{Th}"),
                      "kernel": dom["kernel"],
                      "alg_bytes_per_launch": round(dom["alg_bytes"]),

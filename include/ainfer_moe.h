@@ -419,6 +419,19 @@ int ainfer_moe_profile_kernel(float *gate_up_us, int32_t *n_launches);
 int ainfer_moe_mfma_probe(int32_t valu_per_mfma, int32_t waves_per_simd, int32_t iters,
                           void *stream, float *tflops);
 
+/* The sustainable HBM read rate: iters launches of a read-only kernel that
+ * walks `bytes` of `buf` (16-byte aligned, a multiple of 16; fill it with
+ * random bytes, not a uniform value) with `unroll`
+ * (1, 2, 4, 8 or 16) independent 16-byte loads in flight per lane, on
+ * blocks_per_cu x CUs blocks of 256 threads; *gbs receives bytes x iters over
+ * the elapsed time on `stream` (host-synchronous).  The buffer is a probe
+ * buffer: its first 16 bytes receive a lane's fold in the (2^-128 per lane)
+ * case that the fold is all ones.  No counterpart in the
+ * reference's operator surface: the read roof its own tuning measured before
+ * any kernel (tasks.md:240-250), for decode's "fraction of measured". */
+int ainfer_moe_read_probe(const void *buf, uint64_t bytes, int32_t unroll, int32_t blocks_per_cu,
+                          int32_t iters, void *stream, float *gbs);
+
 #ifdef __cplusplus
 }
 #endif

@@ -135,6 +135,13 @@ CASES = {
         "not 64-byte aligned"),
     "sha_mismatch": (dict(fix_sha=False), None, "trailing sha256"),
     "dir_size": (dict(mutate=lambda b: struct.pack_into("<Q", b, 16, 4)), None, "dir size"),
+    # 3 + 2**58 entries: the count times 192 wraps to the real 576-byte directory
+    "dir_count_overflow": (dict(mutate=lambda b: struct.pack_into("<Q", b, 16, 3 + (1 << 58))),
+                           None, "dir size"),
+    # three dims of 2**32: the element count overflows 64 bits (it would wrap to 0)
+    "numel_overflow": (dict(mutate_entry=lambda i, e: (e.__setitem__(64, 3), struct.pack_into(
+        "<QQQ", e, 72, 1 << 32, 1 << 32, 1 << 32)) if i == 1 else None), None,
+        "b.weight: implausible shape"),
 }
 
 
