@@ -8,6 +8,8 @@ checks are live.  The reference's own negative-test file (two tensors,
 tools/binfer.py:502-560) is rebuilt here and must be accepted as well."""
 import ctypes as C
 import struct
+import json
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -200,3 +202,29 @@ def test_load_checks_layer_shape(L, tmp_path, c0_layers):
     assert LL.lib().ainfer_binfer_load_moe_layer(bf.h, 5, C.c_void_p(256), 1 << 30, C.byref(w),
                                                  C.byref(nw), None) == LL.ERR_ARG
     bf.close()
+
+
+GOLDEN = Path(__file__).resolve().parent / "golden" / "binfer"
+
+
+def test_reference_validator_verdicts(L):
+    """Files the reference's own negatives command emitted, and files this
+    writer made, with the reference validator's verdict on each
+    (tests/golden/make_binfer_fixtures.py): ainfer_binfer_open accepts
+    exactly what the reference accepts.  The one difference is deliberate:
+    layout_id 32 (expert-stacked tensors) is this format's extension, which
+    the v1 reference rejects as an unsupported layout."""
+    verdicts = json.loads((GOLDEN / "verdicts.json").read_text())
+    assert len(verdicts) == 8
+    for name, v in sorted(verdicts.items()):
+        rc, err = _open(L, GOLDEN / name)
+        if name == "ours_layout32.binfer":
+            assert v["rc"] == 1 and v["errors"] == ["unsupported layout_id"]
+            assert rc == L.OK, (name, err)
+            continue
+        assert (rc == L.OK) == (v["rc"] == 0), (name, rc, err, v)
+        if v["rc"] != 0:
+            assert rc == L.ERR_FORMAT
+            # same first failure where the reference reports a single one
+            if len(v["errors"]) == 1:
+                assert v["errors"][0] in err, (name, err, v["errors"])

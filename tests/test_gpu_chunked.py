@@ -35,7 +35,9 @@ def test_workspace_stops_growing_at_one_chunk(torch):
         assert lib.ainfer_moe_workspace_bytes(sh, T) == chunk, T
 
 
-@pytest.mark.parametrize("T", [8192, 9000, 16384])
+# 4097 and 4100 end on a 1- and 4-token chunk, which runs the decode path
+# (shared sync words, folded RMSNorm) on a workspace a 4096-token chunk just used
+@pytest.mark.parametrize("T", [4097, 4100, 8192, 9000, 16384])
 def test_chunked_prefill_parity(torch, oracle, T):
     from ainfer_amd.moe import make_input
     print(f"[case] chunked prefill c2 T={T}", flush=True)
@@ -74,13 +76,14 @@ def test_chunked_prefill_parity(torch, oracle, T):
         assert torch.equal(yc.view(torch.int16), y[c0:c0 + n].view(torch.int16)), (T, c0)
 
 
-def test_chunked_block_forward_in_place(torch):
+@pytest.mark.parametrize("T", [4097, 4100, 8200])
+def test_chunked_block_forward_in_place(torch, T):
     """block_forward (RMSNorm + layer + residual) chunks the same way, also
     with resid_out == resid_in."""
     from ainfer_amd.moe import make_input
+    print(f"[case] chunked block_forward c2 T={T}", flush=True)
     layer = get_layer(torch, "c2")
     cfg = layer.cfg
-    T = 8200
     r0 = make_input(cfg, T, tag=9300) * 3
     ws = layer.workspace(T)
     out = torch.empty_like(r0)

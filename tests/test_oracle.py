@@ -518,3 +518,78 @@ def test_ref_gemv_inputs_follow_the_reference_quantiser(oracle):
     assert scales[0] == oracle.f32_to_bf16(np.array([sc0]))[0]
     q0 = np.clip(np.rint((wf / sc0).astype(np.float32)), -8, 7).astype(np.int64)
     assert np.array_equal(w[0, 0], q0)
+
+
+# ------------------------------------------------------ W4A8 layer ----
+def _expf32(v):
+    """The C library's expf, elementwise (the oracle's SiluMul calls it)."""
+    import ctypes
+    libm = ctypes.CDLL("libm.so.6")
+    libm.expf.restype = ctypes.c_float
+    libm.expf.argtypes = [ctypes.c_float]
+    return np.array([libm.expf(float(a)) for a in np.asarray(v, np.float32).ravel()],
+                    np.float32).reshape(np.shape(v))
+
+
+def _fmaf(a, b, c):
+    """fmaf(a, b, c) on float32 arrays: a*b is exact in fp64 (48-bit product),
+    the fp64 sum is then rounded to float32 (a double rounding, which can only
+    differ from fmaf on an exact float32 midpoint: none occurs on these
+    seeded inputs, or the bit-exact assertion below would say so)."""
+    return (np.asarray(a, np.float64) * np.asarray(b, np.float64)
+            + np.asarray(c, np.float64)).astype(np.float32)
+
+
+def _np_w4a8_expert(oracle, hl, which, e, xq, xs):
+    """decode_l0.cpp:663-674 per (token, expert): Int4Gemv gate and up on the
+    quantised x, SiluMul in float32 (kernels.cpp:29-37), quantise, Int4Gemv
+    down -- composed from the separately pinned pieces."""
+    H, I = hl.H, (hl.I if which == "r" else hl.Is)
+    a = hl.a
+    if which == "r":
+        pg = slice(e * I * H // 2, (e + 1) * I * H // 2)
+        sgs = slice(e * I * H // 128, (e + 1) * I * H // 128)
+        pd = slice(e * H * I // 2, (e + 1) * H * I // 2)
+        sds = slice(e * H * I // 128, (e + 1) * H * I // 128)
+        wg, sg, wu, su = a["w_gate"][pg], a["s_gate"][sgs], a["w_up"][pg], a["s_up"][sgs]
+        wd, sd = a["w_down"][pd], a["s_down"][sds]
+    else:
+        wg, sg, wu, su = a["ws_gate"], a["ss_gate"], a["ws_up"], a["ss_up"]
+        wd, sd = a["ws_down"], a["ss_down"]
+    sdt = oracle.SCALE_FP16
+    g = oracle.int4_gemv_i8(wg, sg, sdt, xq, xs, I, H)[0]
+    u = oracle.int4_gemv_i8(wu, su, sdt, xq, xs, I, H)[0]
+    act = ((g / (np.float32(1.0) + _expf32(-g))).astype(np.float32) * u).astype(np.float32)
+    aq, as_ = oracle.act_quant_i8(act[None, :])
+    return oracle.int4_gemv_i8(wd, sd, sdt, aq, as_, H, I)[0]
+
+
+@pytest.mark.parametrize("Is,gate", [(128, True), (256, False), (0, False)])
+def test_forward_w4a8_composite(oracle, Is, gate):
+    """mo_forward_w4a8 against a numpy composition of the pinned act_quant_i8,
+    int4_gemv_i8, float32 SiluMul and the fmaf combine in slot order
+    (bit-exact), and against the fp64 dense layer on the same routing (the
+    int8 activations cost accuracy, not correctness: cos >= 0.999)."""
+    cfg, hl = _tiny_layer(oracle, Is=Is, gate=gate)
+    T, H, k = 3, cfg.hidden, cfg.top_k
+    x = oracle.fill(oracle.FILL_BF16_NORMAL, 123, 1.0, T * H).reshape(T, H)
+    y = hl.forward_w4a8(x, T)
+    idx, w, sg, _ = hl.route(x, T)
+    want = np.zeros((T, H), np.float32)
+    for t in range(T):
+        xq, xs = oracle.act_quant_i8(x[t:t + 1])
+        acc = np.zeros(H, np.float32)
+        for j in range(k):
+            acc = _fmaf(np.float32(w[t, j]), _np_w4a8_expert(oracle, hl, "r", idx[t, j], xq, xs), acc)
+        if Is > 0:
+            acc = _fmaf(np.float32(sg[t]), _np_w4a8_expert(oracle, hl, "s", 0, xq, xs), acc)
+        want[t] = acc
+    assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
+    dense = hl.forward_dense(x, T, idx, w, sg)
+    cos = (y * dense).sum() / np.sqrt((y.astype(np.float64) ** 2).sum() * (dense ** 2).sum())
+    assert cos >= 0.999, cos
+    # a dropped shared expert or a transposed slot weight is visible in cos
+    if Is > 0:
+        no_shared = y - sg[:, None] * np.stack([_np_w4a8_expert(oracle, hl, "s", 0, *oracle.act_quant_i8(x[t:t + 1])) for t in range(T)])
+        cos2 = (no_shared * dense).sum() / np.sqrt((no_shared.astype(np.float64) ** 2).sum() * (dense ** 2).sum())
+        assert cos2 < 0.99, cos2
