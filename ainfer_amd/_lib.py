@@ -27,6 +27,7 @@ EXPORTS = (
     "ainfer_moe_workspace_init", "ainfer_moe_workspace_check",
     "ainfer_moe_forward", "ainfer_moe_block_forward", "ainfer_moe_block_forward_noalloc",
     "ainfer_moe_stack_workspace_bytes", "ainfer_moe_stack_table_bytes", "ainfer_moe_stack_prepare", "ainfer_moe_stack_forward",
+    "ainfer_moe_stack_forward_persistent",
     "ainfer_moe_route",
     "ainfer_moe_dispatch", "ainfer_moe_experts", "ainfer_moe_combine", "ainfer_moe_rmsnorm", "ainfer_moe_fill",
     "ainfer_moe_act_quant_i8", "ainfer_moe_int4_gemv_i8",
@@ -84,6 +85,7 @@ def lib():
         L.ainfer_moe_stack_table_bytes.argtypes = [I32]
         L.ainfer_moe_stack_prepare.argtypes = [sp, wp, C.POINTER(C.c_void_p), I32, P, SZ, P]
         L.ainfer_moe_stack_forward.argtypes = [sp, P, I32, I32, F, P, P, I32, P, SZ, P]
+        L.ainfer_moe_stack_forward_persistent.argtypes = [sp, P, I32, I32, F, P, P, I32, P, SZ, P]
         L.ainfer_moe_route.argtypes = [sp, wp, P, I32, P, P, P, P, P, SZ, P]
         L.ainfer_moe_dispatch.argtypes = [sp, P, I32, P, P, P, P, P, SZ, P]
         L.ainfer_moe_experts.argtypes = [sp, wp, P, P, I32, P, P, SZ, P]

@@ -3,6 +3,7 @@
 // down -> combine.  Host code; every device buffer comes from the caller.
 #include <string.h>
 
+#include <map>
 #include <mutex>
 #include <vector>
 
@@ -512,7 +513,20 @@ int run_experts(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const La
 
 int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const void *x,
                const void *resid, void *y, int T, void *ws, hipStream_t st,
-               ProfCall *pc, const NormIn *norm = nullptr) {
+               ProfCall *pc, const NormIn *norm = nullptr, const NormIn *next = nullptr,
+               void *h_next = nullptr) {
+  // the final combine, or (next non-null, W4A16, resid non-null) the combine
+  // followed by the next block's RMSNorm of the rows it writes, into h_next
+  auto combine = [&](const DispatchOut &d, const Layout &L) -> hipError_t {
+    if (next && resid)
+      return launch_combine_norm(at<uint16_t>(ws, L.o), d.inv, at<float>(ws, L.w),
+                                 at<float>(ws, L.sg), s->shared_inter > 0, resid, y, T,
+                                 s->top_k, s->hidden, at<int32_t>(ws, L.sync) + SY_ERR, *next,
+                                 h_next, st);
+    return launch_combine(at<uint16_t>(ws, L.o), d.inv, at<float>(ws, L.w), at<float>(ws, L.sg),
+                          s->shared_inter > 0, resid, y, T, s->top_k, s->hidden,
+                          at<int32_t>(ws, L.sync) + SY_ERR, st);
+  };
   if (s->precision == AINFER_PRECISION_W4A8)
     return do_forward_w4a8(s, w, x, resid, y, T, ws, st, pc, norm);
   const Layout L = layout_of(*s, T);
@@ -562,9 +576,7 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
       pc->end(4);
       HIP_TRY(launch_expert_stream(1, s->scale_dtype, dn, mtb, down_kbw(*s), DEC_RG_DOWN, DEC_MT, st));
       pc->end(5);
-      HIP_TRY(launch_combine(at<uint16_t>(ws, L.o), d.inv, at<float>(ws, L.w), at<float>(ws, L.sg),
-                             has_shared, resid, y, T, k, H,
-                           at<int32_t>(ws, L.sync) + SY_ERR, st));
+      HIP_TRY(combine(d, L));
       pc->end(6);
       return AINFER_OK;
     }
@@ -593,8 +605,7 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
                             at<int32_t>(ws, L.chunk_counts), at<int32_t>(ws, L.rank), d, st));
   pc->end(3);
   HIP_TRY_RC(run_experts(s, w, L, ws, d, T, gemm, st, pc));
-  HIP_TRY(launch_combine(at<uint16_t>(ws, L.o), d.inv, at<float>(ws, L.w), at<float>(ws, L.sg),
-                         has_shared, resid, y, T, k, H, at<int32_t>(ws, L.sync) + SY_ERR, st));
+  HIP_TRY(combine(d, L));
   pc->end(6);
   return AINFER_OK;
 }
@@ -644,6 +655,10 @@ int do_block(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const void 
 // the array's name to a kernel or a copy (on the host it is only a stand-in
 // symbol); it uses the per-device address hipGetSymbolAddress returns.
 __device__ __align__(256) unsigned char scratch[AINFER_MOE_NOALLOC_SCRATCH_BYTES];
+
+// host copies of the tables ainfer_moe_stack_prepare wrote, by device address
+std::mutex g_tables_mu;
+std::map<const void *, std::vector<StackLayer>> g_tables;
 
 constexpr int NOALLOC_MAX_DEVICES = 64;
 std::mutex g_scratch_mu;
@@ -859,26 +874,34 @@ int ainfer_moe_stack_prepare(const ainfer_moe_shape *s, const ainfer_moe_weights
   hipStream_t st = (hipStream_t)stream;
   HIP_TRY(hipMemcpyAsync(table, h.data(), h.size() * sizeof(StackLayer), hipMemcpyHostToDevice,
                          st));
-  HIP_TRY(hipStreamSynchronize(st));  // h is released on return
+  HIP_TRY(hipStreamSynchronize(st));
+  // the host keeps its own copy for the replayed form, which launches the
+  // layers' kernels from the host
+  std::lock_guard<std::mutex> lock(g_tables_mu);
+  g_tables[table] = std::move(h);
   return AINFER_OK;
 }
 
 size_t ainfer_moe_stack_workspace_bytes(const ainfer_moe_shape *s, int32_t max_tokens,
                                         int32_t n_layers) {
   if (ainfer_moe_validate(s) != AINFER_OK) return 0;
-  if (max_tokens < 1 || max_tokens > DECODE_NORM_MAX_T || n_layers < 1) return 0;
+  if (max_tokens < 1 || max_tokens > AINFER_MOE_MAX_TOKENS || n_layers < 1) return 0;
+  size_t need = layout_of(*s, chunk_of(max_tokens)).total;  // the replayed form
   StackGeom g;
-  if (!stack_geometry(*s, max_tokens, &g)) return 0;
-  return layout_of(*s, 1).total + (size_t)n_layers * stack_layer_bytes(*s, max_tokens, nullptr);
+  if (max_tokens <= DECODE_NORM_MAX_T && stack_geometry(*s, max_tokens, &g)) {
+    const size_t p = layout_of(*s, 1).total + (size_t)n_layers * stack_layer_bytes(*s, max_tokens, nullptr);
+    if (p > need) need = p;  // the persistent form's per-layer regions
+  }
+  return need;
 }
 
-int ainfer_moe_stack_forward(const ainfer_moe_shape *s, const void *table, int32_t n_layers,
-                             int32_t norm_mode, float eps, const void *resid_in,
-                             void *resid_out, int32_t T, void *ws, size_t ws_bytes,
-                             void *stream) {
+namespace {
+int check_stack_args(const ainfer_moe_shape *s, const void *table, int32_t n_layers,
+                     int32_t norm_mode, float eps, const void *resid_in, const void *resid_out,
+                     int32_t T, int max_t) {
   int rc = ainfer_moe_validate(s);
   if (rc) return rc;
-  if (T < 0 || T > DECODE_NORM_MAX_T) return AINFER_ERR_TOKENS;
+  if (T < 0 || T > max_t) return AINFER_ERR_TOKENS;
   if (n_layers < 0) return AINFER_ERR_ARG;
   if (norm_mode != AINFER_NORM_PLAIN && norm_mode != AINFER_NORM_ONE_PLUS) return AINFER_ERR_ARG;
   if (!(eps >= 0.0f)) return AINFER_ERR_ARG;
@@ -886,6 +909,81 @@ int ainfer_moe_stack_forward(const ainfer_moe_shape *s, const void *table, int32
   if (!table || !resid_in || !resid_out) return AINFER_ERR_NULL;
   if (((uintptr_t)table) & 15 || ((uintptr_t)resid_in) & 15 || ((uintptr_t)resid_out) & 15)
     return AINFER_ERR_ARG;
+  return AINFER_OK;
+}
+
+// The replayed stack on one chunk of at most CHUNK tokens.  Where the block's
+// routing kernel normalizes x itself (decode, T <= 4) and in W4A8, the layers
+// are the per-block entry's calls as they are.  Elsewhere the first layer's
+// RMSNorm is a launch of its own and every later one is computed by the
+// previous layer's combine, from the rows it writes (launch_combine_norm),
+// into the workspace's h; the values are those the block entry computes.
+int do_stack(const ainfer_moe_shape *s, const std::vector<StackLayer> &ly, int n_layers,
+             int norm_mode, float eps, const void *resid_in, void *resid_out, int T, void *ws,
+             hipStream_t st) {
+  DecodeGeom dg;
+  const bool folded = T <= DECODE_NORM_MAX_T && s->n_experts <= 1024 &&
+                      (s->precision == AINFER_PRECISION_W4A8 || decode_geometry(*s, &dg));
+  if (folded || s->precision == AINFER_PRECISION_W4A8) {
+    for (int l = 0; l < n_layers; ++l) {
+      int rc = do_block(s, &ly[l].w, ly[l].norm_w, norm_mode, eps, l ? resid_out : resid_in,
+                        resid_out, T, ws, st);
+      if (rc) return rc;
+    }
+    return AINFER_OK;
+  }
+  const Layout L = layout_of(*s, T);
+  void *h = at<void>(ws, L.h);
+  for (int l = 0; l < n_layers; ++l) {
+    ProfCall pc(st);
+    pc.start();
+    if (l == 0)
+      HIP_TRY(launch_rmsnorm(resid_in, ly[0].norm_w, norm_mode, eps, h, T, s->hidden, st));
+    pc.end(0);
+    NormIn nx;
+    nx.w = l + 1 < n_layers ? (const uint16_t *)ly[l + 1].norm_w : nullptr;
+    nx.mode = norm_mode;
+    nx.eps = eps;
+    nx.on = 1;
+    int rc = do_forward(s, &ly[l].w, h, l ? resid_out : resid_in, resid_out, T, ws, st, &pc,
+                        nullptr, l + 1 < n_layers ? &nx : nullptr, h);
+    if (rc) return rc;
+  }
+  return AINFER_OK;
+}
+}  // namespace
+
+int ainfer_moe_stack_forward(const ainfer_moe_shape *s, const void *table, int32_t n_layers,
+                             int32_t norm_mode, float eps, const void *resid_in,
+                             void *resid_out, int32_t T, void *ws, size_t ws_bytes,
+                             void *stream) {
+  int rc = check_stack_args(s, table, n_layers, norm_mode, eps, resid_in, resid_out, T,
+                            AINFER_MOE_MAX_TOKENS);
+  if (rc || T == 0 || n_layers == 0) return rc;
+  if ((rc = check_ws(s, chunk_of(T), ws, ws_bytes))) return rc;
+  std::vector<StackLayer> ly;
+  {
+    std::lock_guard<std::mutex> lock(g_tables_mu);
+    auto it = g_tables.find(table);
+    if (it == g_tables.end() || (int)it->second.size() < n_layers) return AINFER_ERR_ARG;
+    ly.assign(it->second.begin(), it->second.begin() + n_layers);
+  }
+  // tokens are independent through the whole stack: each chunk runs all layers
+  const size_t row = (size_t)s->hidden * 2;
+  for (int t0 = 0; t0 < T; t0 += CHUNK)
+    if ((rc = do_stack(s, ly, n_layers, norm_mode, eps, (const char *)resid_in + t0 * row,
+                       (char *)resid_out + t0 * row, chunk_of(T - t0), ws, (hipStream_t)stream)))
+      return rc;
+  return AINFER_OK;
+}
+
+int ainfer_moe_stack_forward_persistent(const ainfer_moe_shape *s, const void *table,
+                                        int32_t n_layers, int32_t norm_mode, float eps,
+                                        const void *resid_in, void *resid_out, int32_t T,
+                                        void *ws, size_t ws_bytes, void *stream) {
+  int rc = check_stack_args(s, table, n_layers, norm_mode, eps, resid_in, resid_out, T,
+                            DECODE_NORM_MAX_T);
+  if (rc || T == 0 || n_layers == 0) return rc;
   StackGeom g;
   if (!stack_geometry(*s, T, &g)) return AINFER_ERR_SHAPE;
   if (!ws) return AINFER_ERR_NULL;

@@ -116,6 +116,14 @@ hipError_t launch_gather_rows(const void *src, const int32_t *inv, void *dst, in
 hipError_t launch_combine(const uint16_t *o, const int32_t *inv, const float *w, const float *sg,
                           int has_shared, const void *resid, void *y, int T, int k, int H,
                           const int32_t *err, hipStream_t s);
+// The same combine (resid non-null, H % 8 == 0, H <= 4096, 16-byte aligned
+// rows) followed by the next block's RMSNorm of each written row:
+// h[t] = RMSNorm(y[t]) with `next` (weight, mode, eps), bit-identical to
+// launch_rmsnorm on y.  One 256-thread block per token.
+hipError_t launch_combine_norm(const uint16_t *o, const int32_t *inv, const float *w,
+                               const float *sg, int has_shared, const void *resid, void *y,
+                               int T, int k, int H, const int32_t *err, const NormIn &next,
+                               void *h, hipStream_t s);
 // polls a bounded device wait makes before it gives up (sets the workspace's
 // error word); ainfer_moe_debug_spin_limit changes it for tests
 extern int g_spin_max;

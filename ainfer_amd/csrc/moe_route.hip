@@ -10,6 +10,8 @@
 // order atomics land in.
 #include <string.h>
 
+#include <type_traits>
+
 #include "moe_common.h"
 #include "moe_internal.h"
 
@@ -522,6 +524,144 @@ __global__ __launch_bounds__(256) void k_combine(const uint16_t *__restrict__ o,
     for (int q = 0; q < CPT / 2; ++q) out[q] = 0x7FC07FC0u;
   }
   *(vec_t *)(y + (size_t)t * H + h0) = out;
+}
+
+// Combine with the residual, then the next block's RMSNorm of the row just
+// written, so a stack of blocks needs no RMSNorm launch between them (the
+// residual add fused into the norm, as tools/norm/norm.cpp:30-61 does with
+// FUSED = true).  One block of NT = H / 8 threads (rounded up to whole waves)
+// per token: thread l holds chunk l of the row from the combine to the norm,
+// with every slot's load of it in flight at once.  Each output element is
+// k_combine's arithmetic (slot order fmaf, shared expert, residual, bf16); h
+// is k_rmsnorm's on those bf16 values (the fp64 mean is order-free whenever
+// rms_mean_f accepts it, else the row is re-summed sequentially from an LDS
+// copy).
+template <int NT>
+__global__ __launch_bounds__(NT) void k_combine_norm(
+    const uint16_t *__restrict__ o, const int32_t *__restrict__ inv, const float *__restrict__ w,
+    const float *__restrict__ sg, int has_shared, const uint16_t *resid, uint16_t *y, int T,
+    int k, int H, const int32_t *__restrict__ err, const uint16_t *__restrict__ nw, int mode,
+    float eps, uint16_t *__restrict__ h) {
+  constexpr int NWV = NT / 64;
+  __shared__ double ps[NWV];
+  __shared__ int pe[NWV];
+  __shared__ __attribute__((aligned(16))) uint16_t srow[NT * 8];
+  const int t = blockIdx.x, lid = threadIdx.x, lane = lid & 63, wv = lid >> 6;
+  const int nch = H >> 3;
+  const bool live = lid < nch;
+  const int c = min(lid, nch - 1);
+  const bool bad = err && *err;
+  int pos[32];
+  float wj[32];
+#pragma unroll
+  for (int j = 0; j < 32; ++j)
+    if (j < k) {
+      pos[j] = inv ? inv[(size_t)t * k + j] : t * k + j;
+      wj[j] = w[(size_t)t * k + j];
+    }
+  // loads of up to 16 slots in flight, then their fmas in slot order
+  constexpr int B = 16;
+  float acc[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) acc[q] = 0.0f;
+  auto fma_row = [&](float g, const u32x4 &rv) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      acc[2 * q] = __builtin_fmaf(g, __uint_as_float(rv[q] << 16), acc[2 * q]);
+      acc[2 * q + 1] = __builtin_fmaf(g, __uint_as_float(rv[q] & 0xFFFF0000u), acc[2 * q + 1]);
+    }
+  };
+  const u32x4 nv = nw ? *(const u32x4 *)(nw + 8 * c) : u32x4{0u, 0u, 0u, 0u};
+  const u32x4 rr = *(const u32x4 *)(resid + (size_t)t * H + 8 * c);
+  const u32x4 sv = has_shared ? __builtin_nontemporal_load((const u32x4 *)(o + ((size_t)T * k + t) * H + 8 * c))
+                              : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int j0 = 0; j0 < 32; j0 += B) {
+    if (j0 >= k) break;
+    u32x4 r[B];
+#pragma unroll
+    for (int j = 0; j < B; ++j)
+      if (j0 + j < k) r[j] = __builtin_nontemporal_load((const u32x4 *)(o + (size_t)pos[j0 + j] * H + 8 * c));
+#pragma unroll
+    for (int j = 0; j < B; ++j)
+      if (j0 + j < k) fma_row(wj[j0 + j], r[j]);
+  }
+  if (has_shared) fma_row(sg[t], sv);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    acc[2 * q] += __uint_as_float(rr[q] << 16);
+    acc[2 * q + 1] += __uint_as_float(rr[q] & 0xFFFF0000u);
+  }
+  u32x4 yv;
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    yv[q] = bad ? 0x7FC07FC0u
+                : (uint32_t)f32_to_bf16(acc[2 * q]) | ((uint32_t)f32_to_bf16(acc[2 * q + 1]) << 16);
+  // y may alias resid: each chunk is read and then written by one thread only
+  if (live) *(u32x4 *)(y + (size_t)t * H + 8 * c) = yv;
+  double p4[4] = {0.0, 0.0, 0.0, 0.0};
+  u16x2_t ek = {0x7F80, 0x7F80};
+  if (live) sumsq_chunk(yv, p4, ek);
+  const double wtot = wave_sum_f64((p4[0] + p4[1]) + (p4[2] + p4[3]));
+  const int wemin = (int)wave_min_u32((uint32_t)ek_emin(ek));
+  if (lane == 0) {
+    ps[wv] = wtot;
+    pe[wv] = wemin;
+  }
+  __syncthreads();
+  double tot = ps[0];
+  int emin = pe[0];
+#pragma unroll
+  for (int i = 1; i < NWV; ++i) {
+    tot += ps[i];
+    emin = min(emin, pe[i]);
+  }
+  float mean;
+  if (!rms_mean_f(tot, emin, H, mean)) {  // block-uniform; see rms_mean_f
+    if (live) *(u32x4 *)(srow + 8 * c) = yv;
+    __syncthreads();
+    if (lid == 0) ps[0] = row_sumsq_seq(srow, H);
+    __syncthreads();
+    mean = (float)(ps[0] / H);
+  }
+  const float rinv = 1.0f / sqrtf(mean + eps);
+  NormIn n;
+  n.w = nw;
+  n.mode = mode;
+  n.eps = eps;
+  n.on = 1;
+  if (live) {
+    u32x4 ov;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) ov[q] = norm_pair(yv[q], nv[q], rinv, n);
+    *(u32x4 *)(h + (size_t)t * H + 8 * c) = ov;
+  }
+}
+
+hipError_t launch_combine_norm(const uint16_t *o, const int32_t *inv, const float *w,
+                               const float *sg, int has_shared, const void *resid, void *y,
+                               int T, int k, int H, const int32_t *err, const NormIn &next,
+                               void *h, hipStream_t s) {
+  if (T == 0) return hipSuccess;
+  if (!resid || H % 8 || H > 4096 || k > 32 || ((uintptr_t)resid & 15) || ((uintptr_t)y & 15) ||
+      ((uintptr_t)h & 15) || ((uintptr_t)next.w & 15))
+    return hipErrorInvalidValue;
+  const uint16_t *r = (const uint16_t *)resid, *nw = next.w;
+  const int nch = H / 8;
+  auto go = [&](auto nt_c) {
+    constexpr int NT = decltype(nt_c)::value;
+    k_combine_norm<NT><<<T, NT, 0, s>>>(o, inv, w, sg, has_shared, r, (uint16_t *)y, T, k, H, err,
+                                        nw, next.mode, next.eps, (uint16_t *)h);
+  };
+  if (nch <= 64)
+    go(std::integral_constant<int, 64>());
+  else if (nch <= 128)
+    go(std::integral_constant<int, 128>());
+  else if (nch <= 256)
+    go(std::integral_constant<int, 256>());
+  else
+    go(std::integral_constant<int, 512>());
+  return hipGetLastError();
 }
 
 // x in MFMA order and (xsum non-null) its per-128 group sums: one wave per

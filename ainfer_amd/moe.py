@@ -193,9 +193,12 @@ def with_precision(layer, precision):
 
 
 class MoeStack:
-    """L decoder-block MLP halves run as one persistent launch
-    (ainfer_moe_stack_forward, T <= 4): the layers' weights and per-layer
-    RMSNorm weights go into a device table once (ainfer_moe_stack_prepare)."""
+    """L decoder-block MLP halves as one call (ainfer_moe_stack_forward: the
+    layers' kernels replayed, each layer's combine computing the next layer's
+    RMSNorm; any T), or as one persistent launch
+    (ainfer_moe_stack_forward_persistent, T <= 4).  The layers' weights and
+    per-layer RMSNorm weights go into a device table once
+    (ainfer_moe_stack_prepare)."""
 
     def __init__(self, layers, norm_ws=None, device="cuda"):
         assert layers, "a stack needs at least one layer"
@@ -225,9 +228,12 @@ class MoeStack:
         L.check(lib.ainfer_moe_workspace_init(C.byref(self.shape), _ptr(ws), n, _stream(None)))
         return ws
 
-    def forward(self, resid_in, resid_out, ws, norm_mode=L.NORM_PLAIN, eps=1e-6, stream=None):
+    def forward(self, resid_in, resid_out, ws, norm_mode=L.NORM_PLAIN, eps=1e-6, stream=None,
+                persistent=False):
         T = resid_in.shape[0]
-        return L.check(L.lib().ainfer_moe_stack_forward(
+        fn = (L.lib().ainfer_moe_stack_forward_persistent if persistent
+              else L.lib().ainfer_moe_stack_forward)
+        return L.check(fn(
             C.byref(self.shape), _ptr(self.table), len(self.layers), norm_mode, eps,
             _ptr(resid_in), _ptr(resid_out), T, _ptr(ws), ws.numel(), _stream(stream)))
 

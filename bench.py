@@ -226,11 +226,14 @@ def run_c3(steps, warmup=5):
 
 
 def run_c4(steps, tokens=(1, 8), warmup=3, keep_layer0=False, stack=True):
-    """60 blocks of config 3 (RMSNorm -> MoE -> residual,
-    ainfer_moe_block_forward), one decode step = all 60 blocks in sequence on
-    a bf16 residual stream; 200 GB of weights resident.  A second pass over
-    the same steps reads per-stage device times (HIP events on the launch
-    stream, mean per block)."""
+    """60 blocks of config 3 (RMSNorm -> MoE -> residual),
+    one decode step = all 60 blocks in sequence on a bf16 residual stream,
+    200 GB of weights resident.  The step is one ainfer_moe_stack_forward
+    call (the layers' kernels replayed; from T = 5 on each layer's combine
+    computes the next layer's RMSNorm).  Beside it: the same step as 60
+    chained ainfer_moe_block_forward calls, and (T <= 4) as the one-launch
+    persistent kernel.  A second pass over the stack's steps reads per-stage
+    device times (HIP events on the launch stream, mean per block)."""
     import torch
     from ainfer_amd import _lib as L
     from ainfer_amd.moe import MoeLayer, MoeStack, make_input, rmsnorm
@@ -239,11 +242,27 @@ def run_c4(steps, tokens=(1, 8), warmup=3, keep_layer0=False, stack=True):
     log(f"[bench] c4: allocating {cfg.layers} layers "
         f"({cfg.layers * cfg.layer_weight_bytes() / 1e9:.1f} GB)")
     layers = [MoeLayer(cfg, layer=i) for i in range(cfg.layers)]
+    stk = MoeStack(layers)
     torch.cuda.synchronize()
     out = {}
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+
+    def timed(step):
+        for s in range(warmup):
+            step(s)
+        torch.cuda.synchronize()
+        t0.record()
+        for s in range(steps):
+            step(s)
+        t1.record()
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1) * 1e3 / steps
+
     for T in tokens:
         log(f"[bench] c4 T={T}")
         ws = layers[0].workspace(T)
+        sws = stk.workspace(T)
         r0 = make_input(cfg, T, tag=4000 + T) * 4
         # distinct routed experts per layer along the actual residual stream
         U = 0.0
@@ -261,24 +280,22 @@ def run_c4(steps, tokens=(1, 8), warmup=3, keep_layer0=False, stack=True):
         y = torch.empty_like(r0)
 
         def step(s):
-            layers[0].block_forward(xs[s % len(xs)], y, ws)
-            for L_ in layers[1:]:
-                L_.block_forward(y, y, ws)
-        for s in range(warmup):
-            step(s)
-        torch.cuda.synchronize()
-        t0 = torch.cuda.Event(enable_timing=True)
-        t1 = torch.cuda.Event(enable_timing=True)
-        t0.record()
-        for s in range(steps):
-            step(s)
-        t1.record()
-        torch.cuda.synchronize()
-        us = t0.elapsed_time(t1) * 1e3 / steps
+            stk.forward(xs[s % len(xs)], y, sws)
+        us = timed(step)
         # a bounded device wait that ran out leaves NaN rows: such a step is not a result
         if not bool(torch.isfinite(y).all()):
             raise RuntimeError(f"c4 T={T}: the 60-block residual is not finite")
-        L.check(layers[0].workspace_check(ws))
+        L.check(layers[0].workspace_check(sws))
+        y_stack = y.clone()
+
+        def step_blocks(s):
+            layers[0].block_forward(xs[s % len(xs)], y, ws)
+            for L_ in layers[1:]:
+                L_.block_forward(y, y, ws)
+        blocks_us = timed(step_blocks)
+        # the last steps of both forms ran the same input: the same bits
+        if not torch.equal(y.view(torch.int16), y_stack.view(torch.int16)):
+            raise RuntimeError(f"c4 T={T}: stack and chained blocks differ")
         # profiled pass: mean device time per stage and block
         L.profile_enable(True)
         for s in range(steps):
@@ -301,46 +318,26 @@ def run_c4(steps, tokens=(1, 8), warmup=3, keep_layer0=False, stack=True):
                    "file": "k_experts_decode",
                    "alg_bytes": experts_bytes(cfg, Ul, T), "us": st["down"]}
         dom["gbs"] = dom["alg_bytes"] / (dom["us"] * 1e-6) / 1e9 if dom["us"] else 0.0
-        stack_us = None
-        use_stack = stack
-        if use_stack and T <= L.STACK_MAX_TOKENS:
-            # the same step as one persistent launch (ainfer_moe_stack_forward)
-            stk = MoeStack(layers)
-            sws = stk.workspace(T)
-            for s in range(warmup):
-                stk.forward(xs[s % len(xs)], y, sws)
-            torch.cuda.synchronize()
-            t0.record()
-            for s in range(steps):
-                stk.forward(xs[s % len(xs)], y, sws)
-            t1.record()
-            torch.cuda.synchronize()
-            stack_us = round(t0.elapsed_time(t1) * 1e3 / steps, 1)
+        pers_us = None
+        if stack and T <= L.STACK_MAX_TOKENS:
+            # the same step as one persistent launch (ainfer_moe_stack_forward_persistent)
+            def step_p(s):
+                stk.forward(xs[s % len(xs)], y, sws, persistent=True)
+            pers_us = round(timed(step_p), 1)
             if not bool(torch.isfinite(y).all()):
-                raise RuntimeError(f"c4 T={T}: the one-launch stack's residual is not finite")
-            del stk, sws
+                raise RuntimeError(f"c4 T={T}: the persistent stack's residual is not finite")
         w8_us = None
         if T == 1:
             # the same step in the reference's W4A8 numerics (row f3: int8
             # activations per group of 128, Int4Gemv products, fp32 SiluMul
             # and combine), on the same resident weights
             from ainfer_amd.moe import with_precision
-            w8 = [with_precision(L_, L.PRECISION_W4A8) for L_ in layers]
-            ws8 = w8[0].workspace(T)
+            w8 = MoeStack([with_precision(L_, L.PRECISION_W4A8) for L_ in layers])
+            ws8 = w8.workspace(T)
 
             def step8(s):
-                w8[0].block_forward(xs[s % len(xs)], y, ws8)
-                for L_ in w8[1:]:
-                    L_.block_forward(y, y, ws8)
-            for s in range(warmup):
-                step8(s)
-            torch.cuda.synchronize()
-            t0.record()
-            for s in range(steps):
-                step8(s)
-            t1.record()
-            torch.cuda.synchronize()
-            w8_us = round(t0.elapsed_time(t1) * 1e3 / steps, 1)
+                w8.forward(xs[s % len(xs)], y, ws8)
+            w8_us = round(timed(step8), 1)
             del w8, ws8
         out[str(T)] = {"us_per_step": round(us, 1), "us_per_token": round(us / T, 2),
                        "us_per_block": round(us / len(layers), 2),
@@ -350,14 +347,15 @@ def run_c4(steps, tokens=(1, 8), warmup=3, keep_layer0=False, stack=True):
                        "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                        "stage_us_per_block": {k: round(v, 3) for k, v in st.items() if v > 0},
                        "dominant": dom,
-                       "stack_launch_us_per_step": stack_us,
+                       "chained_blocks_us_per_step": round(blocks_us, 1),
+                       "stack_persistent_us_per_step": pers_us,
                        "w4a8_us_per_step": w8_us,
                        "w4a8_hbm_frac": (round(nbytes / (w8_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
                                          if w8_us else None)}
         log(f"[bench]   c4 T={T}: {json.dumps(out[str(T)])}")
-        del ws
+        del ws, sws
     keep = layers[0] if keep_layer0 else None
-    del layers
+    del layers, stk
     torch.cuda.empty_cache()
     return out, keep
 
@@ -522,7 +520,8 @@ def main():
                     help="skip config 4 (no headline line: prints the details only)")
     ap.add_argument("--no-peaks", action="store_true", help="skip the measured-peak probes")
     ap.add_argument("--no-stack", action="store_true",
-                    help="skip the one-launch stack timing of c4 (ainfer_moe_stack_forward)")
+                    help="skip the persistent one-launch timing of c4 "
+                         "(ainfer_moe_stack_forward_persistent)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="finally copy MIB MiB device-to-device 5 times (PMC calibration)")

@@ -185,22 +185,38 @@ int ainfer_moe_block_forward(const ainfer_moe_shape *shape,
                              void *workspace, size_t workspace_bytes,
                              void *stream);
 
-/* ---- decode stack: many blocks in one launch ----------------------------
+/* ---- decode stack: many blocks in one call ------------------------------
  * The reference records each layer's command list once at init and replays
  * the recorded lists every decode step (tools/decode/decode_l0.cpp:553-677,
  * the MLP part :663-674).  Here the init step writes a device table of the
- * layers' weights (ainfer_moe_stack_prepare) and one call runs all of them:
+ * layers' weights (ainfer_moe_stack_prepare, which also keeps a host copy)
+ * and one call runs all of them:
  *   for l in 0..n_layers-1:  r = bf16(r + MoE_l(RMSNorm_l(r)))
  * with r = resid_in at the start and resid_out at the end (resid_out may
  * alias resid_in).  Each layer's output is bit-identical to
  * ainfer_moe_block_forward on the same input, so the stack equals n_layers
- * chained block_forward calls.  T <= 4 tokens (AINFER_ERR_TOKENS above);
- * shapes without a stack geometry (K split of more than 8 waves) return
- * AINFER_ERR_SHAPE, and callers use block_forward.  The workspace
- * (ainfer_moe_stack_workspace_bytes: every layer's intermediates get a
- * region of their own, about 0.5 MB per layer at H4096/E512/k10/I1024,
- * T = 4) is initialised once with ainfer_moe_workspace_init; it also serves
- * the per-block entries at T = 1.  Calls on one workspace must not overlap. */
+ * chained block_forward calls.
+ *
+ * ainfer_moe_stack_forward replays the layers' kernels from the host, any T
+ * up to AINFER_MOE_MAX_TOKENS (chunks of AINFER_MOE_CHUNK_TOKENS each run
+ * every layer).  Where the block entry would launch an RMSNorm of its own
+ * (T > 4, W4A16), the previous layer's combine computes it from the rows it
+ * writes (the residual add fused into the next norm, tools/norm/norm.cpp:
+ * 30-61), so a layer is one launch shorter.  The table must come from
+ * ainfer_moe_stack_prepare in this process (else AINFER_ERR_ARG); workspace:
+ * ainfer_moe_stack_workspace_bytes(max_tokens), initialised once with
+ * ainfer_moe_workspace_init.
+ *
+ * ainfer_moe_stack_forward_persistent runs the same L blocks at T <= 4 as one
+ * persistent launch (AINFER_ERR_TOKENS above; shapes without a stack
+ * geometry, K split of more than 8 waves, return AINFER_ERR_SHAPE).  Its
+ * workgroups must all be resident at once: it needs the device to itself
+ * (a concurrent kernel turns its waits into bounded time-outs: NaN outputs
+ * and AINFER_ERR_SYNC from ainfer_moe_workspace_check).  It is slower than
+ * the replayed form on MI355X (c4, T = 1: about 2.6 against 2.0 ms per 60
+ * layers); callers that cannot launch from the host per layer are its use.
+ * Its workspace holds every layer's intermediates (about 0.5 MB per layer at
+ * H4096/E512/k10/I1024, T = 4).  Calls on one workspace must not overlap. */
 size_t ainfer_moe_stack_workspace_bytes(const ainfer_moe_shape *shape,
                                         int32_t max_tokens, int32_t n_layers);
 size_t ainfer_moe_stack_table_bytes(int32_t n_layers);
@@ -217,6 +233,11 @@ int ainfer_moe_stack_forward(const ainfer_moe_shape *shape, const void *table,
                              int32_t n_layers, int32_t norm_mode, float eps,
                              const void *resid_in, void *resid_out, int32_t T,
                              void *workspace, size_t workspace_bytes, void *stream);
+int ainfer_moe_stack_forward_persistent(const ainfer_moe_shape *shape, const void *table,
+                                        int32_t n_layers, int32_t norm_mode, float eps,
+                                        const void *resid_in, void *resid_out, int32_t T,
+                                        void *workspace, size_t workspace_bytes,
+                                        void *stream);
 
 /* Bytes of the static device scratch behind ainfer_moe_block_forward_noalloc
  * (one copy per GPU the library runs on, held until the process ends). */

@@ -1,12 +1,16 @@
-"""The persistent decode stack (ainfer_moe_stack_forward: L blocks in one
-launch) against L chained ainfer_moe_block_forward calls, which the other GPU
-tests pin to the oracle: the outputs must be bit-identical.  Config 4's shape
+"""The decode stack in both forms -- ainfer_moe_stack_forward (the layers'
+kernels replayed, each layer's combine computing the next layer's RMSNorm)
+and ainfer_moe_stack_forward_persistent (L blocks in one launch, T <= 4) --
+against L chained ainfer_moe_block_forward calls, which the other GPU tests
+pin to the oracle: the outputs must be bit-identical.  Config 4's shape
 (H4096, E512, top-10, I1024 + shared) with four independent layers, T = 1..4
-(the fused and the three-launch expert paths of block_forward), both RMSNorm
-weight forms with per-layer weights, in place and out of place, repeated
-calls (the layer tags advance) and calls interleaved with block_forward on
-the same workspace; config 1's shape (H2048); the argument errors; and the
-bounded waits made to run out from the host (NaN outputs, no hang)."""
+(the fused and the three-launch expert paths of block_forward) in both forms
+and T = 5, 8, 16 and 64 replayed (the fused combine + next RMSNorm), both
+RMSNorm weight forms with per-layer weights, in place and out of place,
+repeated calls (the layer tags advance) and calls interleaved with
+block_forward on the same workspace; config 1's shape (H2048) up to the
+prefill path (T = 300) and a chunked call (T = 4100); the argument errors;
+and the bounded waits made to run out from the host (NaN outputs, no hang)."""
 import numpy as np
 import pytest
 
@@ -53,9 +57,13 @@ def c4_stack(torch):
     torch.cuda.empty_cache()
 
 
-@pytest.mark.parametrize("T", [1, 2, 3, 4])
+CASES_C4 = [(T, "replay") for T in (1, 2, 3, 4, 5, 8, 16, 64)] + \
+    [(T, "persistent") for T in (1, 2, 3, 4)]
+
+
+@pytest.mark.parametrize("T,form", CASES_C4)
 @pytest.mark.parametrize("mode", ["plain", "one_plus"])
-def test_stack_equals_chained_blocks_c4(torch, c4_stack, T, mode):
+def test_stack_equals_chained_blocks_c4(torch, c4_stack, T, form, mode):
     from ainfer_amd import _lib as L
     from ainfer_amd.moe import MoeStack, make_input
     cfg, layers, norm_ws = c4_stack
@@ -63,18 +71,19 @@ def test_stack_equals_chained_blocks_c4(torch, c4_stack, T, mode):
     stack = MoeStack(layers, norm_ws)
     ws = stack.workspace(T)
     wsb = layers[0].workspace(T)
+    pers = form == "persistent"
     for rep in range(2):
-        print(f"[case] stack c4 T={T} mode={mode} rep={rep}", flush=True)
+        print(f"[case] stack c4 T={T} {form} mode={mode} rep={rep}", flush=True)
         r0 = (make_input(cfg, T, tag=6100 + 10 * T + rep) * 4).contiguous()
         want = _chain(layers, r0, wsb, norm_ws, nm)
         out = torch.empty_like(r0)
-        stack.forward(r0, out, ws, norm_mode=nm)
+        stack.forward(r0, out, ws, norm_mode=nm, persistent=pers)
         torch.cuda.synchronize()
         assert not torch.isnan(out.float()).any(), (T, mode, rep)
         assert torch.equal(_bits(out), _bits(want)), (T, mode, rep)
         # in place
         r = r0.clone()
-        stack.forward(r, r, ws, norm_mode=nm)
+        stack.forward(r, r, ws, norm_mode=nm, persistent=pers)
         torch.cuda.synchronize()
         assert torch.equal(_bits(r), _bits(want)), (T, mode, rep, "in place")
     assert layers[0].workspace_check(ws) == L.OK
@@ -96,11 +105,11 @@ def test_stack_matches_oracle_per_block_c4(torch, oracle, c4_stack):
     cfg, layers, norm_ws = c4_stack
     hl = host_copy(oracle, layers[1])
     stack = MoeStack([layers[1]], [norm_ws[1]])
-    for T in (1, 3):
+    for T, pers in ((1, True), (3, True), (1, False), (8, False)):
         ws = stack.workspace(T)
         r0 = (make_input(cfg, T, tag=6300 + T) * 4).contiguous()
         out = torch.empty_like(r0)
-        stack.forward(r0, out, ws, norm_mode=L.NORM_ONE_PLUS)
+        stack.forward(r0, out, ws, norm_mode=L.NORM_ONE_PLUS, persistent=pers)
         torch.cuda.synchronize()
         want = hl.block_forward(to_np(r0), T, norm_w=to_np(norm_ws[1]), mode=L.NORM_ONE_PLUS)
         check_close(to_np(out), oracle.bf16_to_f32(want), f"stack vs oracle T={T}")
@@ -118,15 +127,18 @@ def test_stack_equals_chained_blocks_small(torch, name):
     layers = [MoeLayer(cfg, layer=i) for i in range(3)]
     norm_ws = [None] * 3
     stack = MoeStack(layers)
-    for T in (1, 2, 4):
-        print(f"[case] stack {name} T={T}", flush=True)
+    cases = [(T, p) for T in (1, 2, 4) for p in (True, False)] + [(8, False), (300, False)]
+    if name == "c1":
+        cases.append((4100, False))  # two chunks, the second of 4 tokens
+    for T, pers in cases:
+        print(f"[case] stack {name} T={T} persistent={pers}", flush=True)
         ws = stack.workspace(T)
         r0 = (make_input(cfg, T, tag=6200 + T) * 2).contiguous()
         want = _chain(layers, r0, layers[0].workspace(T), norm_ws, L.NORM_PLAIN)
         out = torch.empty_like(r0)
-        stack.forward(r0, out, ws)
+        stack.forward(r0, out, ws, persistent=pers)
         torch.cuda.synchronize()
-        assert torch.equal(_bits(out), _bits(want)), (name, T)
+        assert torch.equal(_bits(out), _bits(want)), (name, T, pers)
     del layers, stack
     torch.cuda.empty_cache()
 
@@ -141,16 +153,28 @@ def test_stack_argument_errors(torch, c4_stack):
     ws = stack.workspace(4)
     r = torch.zeros(5, cfg.hidden, dtype=torch.bfloat16, device="cuda")
     sh = C.byref(stack.shape)
-    fwd = lambda T, n=2, mode=L.NORM_PLAIN, tab=stack.table: lib.ainfer_moe_stack_forward(
-        sh, _ptr(tab), n, mode, 1e-6, _ptr(r), _ptr(r), T, _ptr(ws), ws.numel(), _stream(None))
-    assert fwd(5) == L.ERR_TOKENS
-    assert fwd(-1) == L.ERR_TOKENS
-    assert fwd(0) == L.OK and fwd(2, n=0) == L.OK
-    assert fwd(2, mode=7) == L.ERR_ARG
-    assert fwd(2, tab=None) == L.ERR_NULL
-    assert lib.ainfer_moe_stack_forward(sh, _ptr(stack.table), 2, 0, 1e-6, _ptr(r), _ptr(r), 4,
-                                        _ptr(ws), ws.numel() - 256, _stream(None)) == L.ERR_WORKSPACE
-    assert lib.ainfer_moe_stack_workspace_bytes(sh, 5, 2) == 0
+    for f in (lib.ainfer_moe_stack_forward_persistent, lib.ainfer_moe_stack_forward):
+        fwd = lambda T, n=2, mode=L.NORM_PLAIN, tab=stack.table: f(
+            sh, _ptr(tab), n, mode, 1e-6, _ptr(r), _ptr(r), T, _ptr(ws), ws.numel(), _stream(None))
+        assert fwd(-1) == L.ERR_TOKENS
+        assert fwd(0) == L.OK and fwd(2, n=0) == L.OK
+        assert fwd(2, mode=7) == L.ERR_ARG
+        assert fwd(2, tab=None) == L.ERR_NULL
+        need = (ws.numel() if f == lib.ainfer_moe_stack_forward_persistent
+                else lib.ainfer_moe_workspace_bytes(sh, 4))
+        assert f(sh, _ptr(stack.table), 2, 0, 1e-6, _ptr(r), _ptr(r), 4,
+                 _ptr(ws), need - 256, _stream(None)) == L.ERR_WORKSPACE
+    assert lib.ainfer_moe_stack_forward_persistent(
+        sh, _ptr(stack.table), 2, L.NORM_PLAIN, 1e-6, _ptr(r), _ptr(r), 5, _ptr(ws), ws.numel(),
+        _stream(None)) == L.ERR_TOKENS
+    # the replayed form needs the host copy ainfer_moe_stack_prepare keeps
+    other = torch.zeros_like(stack.table)
+    assert lib.ainfer_moe_stack_forward(sh, _ptr(other), 2, L.NORM_PLAIN, 1e-6, _ptr(r), _ptr(r),
+                                        2, _ptr(ws), ws.numel(), _stream(None)) == L.ERR_ARG
+    assert lib.ainfer_moe_stack_forward(sh, _ptr(stack.table), 3, L.NORM_PLAIN, 1e-6, _ptr(r),
+                                        _ptr(r), 2, _ptr(ws), ws.numel(), _stream(None)) == L.ERR_ARG
+    assert lib.ainfer_moe_stack_workspace_bytes(sh, 5, 2) >= lib.ainfer_moe_workspace_bytes(sh, 5)
+    assert lib.ainfer_moe_stack_workspace_bytes(sh, L.MAX_TOKENS + 1, 2) == 0
     assert lib.ainfer_moe_stack_workspace_bytes(sh, 1, 0) == 0
     arr = (L.Weights * 1)(layers[0].weights)
     assert lib.ainfer_moe_stack_prepare(sh, arr, None, 1, _ptr(stack.table), 16, None) == L.ERR_ARG
@@ -181,7 +205,7 @@ def test_stack_wait_timeout_is_visible(torch, oracle, c4_stack):
     try:
         L.check(L.lib().ainfer_moe_debug_spin_limit(0))
         print("[case] stack forced timeout", flush=True)
-        stack.forward(r0, out, ws)
+        stack.forward(r0, out, ws, persistent=True)
         torch.cuda.synchronize()
     finally:
         L.check(L.lib().ainfer_moe_debug_spin_limit(1 << 20))
@@ -190,6 +214,6 @@ def test_stack_wait_timeout_is_visible(torch, oracle, c4_stack):
     L.check(L.lib().ainfer_moe_workspace_init(C.byref(layers[0].shape), _ptr(ws), ws.numel(),
                                               _stream(None)))
     want = _chain(layers[:2], r0, layers[0].workspace(T), norm_ws[:2], L.NORM_PLAIN)
-    stack.forward(r0, out, ws)
+    stack.forward(r0, out, ws, persistent=True)
     torch.cuda.synchronize()
     assert torch.equal(_bits(out), _bits(want))

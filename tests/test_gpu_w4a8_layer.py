@@ -123,4 +123,23 @@ def test_w4a8_shape_rules(torch):
     n16 = L.lib().ainfer_moe_workspace_bytes(C.byref(base.shape), 16)
     n8 = L.lib().ainfer_moe_workspace_bytes(C.byref(layer.shape), 16)
     assert n8 > n16
-    assert L.lib().ainfer_moe_stack_workspace_bytes(C.byref(layer.shape), 1, 1) == 0
+    # the stack replays W4A8 blocks as the block entry runs them; the
+    # persistent one-launch form has W4A16 items only
+    assert L.lib().ainfer_moe_stack_workspace_bytes(C.byref(layer.shape), 1, 1) == \
+        L.lib().ainfer_moe_workspace_bytes(C.byref(layer.shape), 1)
+    from ainfer_amd.moe import make_input
+    w8 = [layer, with_precision(get_layer(torch, "c1"), L.PRECISION_W4A8)]
+    stack = MoeStack(w8)
+    for T in (1, 8):
+        ws = stack.workspace(T)
+        r0 = (make_input(base.cfg, T, tag=7700 + T) * 2).contiguous()
+        want = r0.clone()
+        for ly in w8:
+            ly.block_forward(want, want, w8[0].workspace(T))
+        out = torch.empty_like(r0)
+        stack.forward(r0, out, ws)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), want.view(torch.int16)), T
+        assert L.lib().ainfer_moe_stack_forward_persistent(
+            C.byref(layer.shape), _ptr(stack.table), 2, L.NORM_PLAIN, 1e-6, _ptr(r0), _ptr(out), T,
+            _ptr(ws), ws.numel(), _stream(None)) == (L.ERR_SHAPE if T == 1 else L.ERR_TOKENS)
