@@ -374,10 +374,9 @@ int do_forward_w4a8(const ainfer_moe_shape *s, const ainfer_moe_weights *w, cons
   a.ss0 = (const uint16_t *)w->ss_gate;
   a.ss1 = (const uint16_t *)w->ss_up;
   HIP_TRY(launch_w4a8_expert(0, s->scale_dtype, a, mtb, st));
-  HIP_TRY(launch_act_quant_f32_pair(a.act, T * k, I, at<int8_t>(ws, L.w8_aq),
-                                    at<float>(ws, L.w8_as), has_shared ? a.act_s : nullptr, T,
-                                    Is, at<int8_t>(ws, L.w8_aqs), at<float>(ws, L.w8_ass), st));
   pc->end(4);
+  // the down launch quantizes act itself (at T = 1 inside its blocks)
+  a.quant_in = 1;
   a.w0 = w->w_down;
   a.s0 = (const uint16_t *)w->s_down;
   a.ws0 = w->ws_down;

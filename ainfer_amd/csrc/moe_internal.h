@@ -214,6 +214,10 @@ struct W4A8Args {
   const int4 *tiles;
   const int32_t *n_tiles;
   int T, k, E, H, I, Is;
+  // MODE 1: act / act_s are the fp32 inputs; the launch quantizes them into
+  // aq / as (one token per tile: inside the GEMV kernel, each block into its
+  // LDS; else a quantization launch first)
+  int quant_in;
 };
 hipError_t launch_w4a8_expert(int mode, int scale_dtype, const W4A8Args &a, int max_tiles,
                               hipStream_t s);

@@ -251,11 +251,14 @@ __global__ __launch_bounds__(GV_WAVES * 64) void k_int4_gemv_i8(
 // m0 + r of matrix j (other lanes 0).  term: this wave's LDS, NMAT * GV1_RW
 // rows of NC * 16 floats.  Every weight load of every matrix is issued
 // before any is used.
-template <int SD, int NC, int NMAT>
+struct NoHook {
+  __device__ void operator()() const {}
+};
+template <int SD, int NC, int NMAT, typename Hook = NoHook>
 __device__ __forceinline__ float gemv1_rows(const uint8_t *const (&P)[NMAT],
                                             const uint16_t *const (&S)[NMAT], int m0, int M,
-                                            int K, const int8_t *__restrict__ xq,
-                                            const float *__restrict__ sq, float *term, int lane) {
+                                            int K, const int8_t *xq, const float *sq,
+                                            float *term, int lane, Hook hook = Hook()) {
   constexpr int R = NMAT * GV1_RW;
   const int C = K >> 5, G = K >> 7;  // 16-byte chunks and groups per row
   const size_t rowb = (size_t)K / 2;
@@ -267,6 +270,9 @@ __device__ __forceinline__ float gemv1_rows(const uint8_t *const (&P)[NMAT],
     for (int i = 0; i < NC; ++i)
       wv[r][i] = __builtin_nontemporal_load((const u32x4 *)(wp + (size_t)min(lane + 64 * i, C - 1) * 16));
   }
+  // with the weights in flight: whatever produces xq / sq (the block's
+  // quantization of its activation row into LDS)
+  hook();
   // activations of this lane's chunks (32 bytes each, the same for every
   // row), the group scales of its quad's groups, and the weight scales
   u32x4 xa[NC], xb[NC];
@@ -345,15 +351,71 @@ __global__ __launch_bounds__(GV1_WAVES * 64) void k_int4_gemv_i8_t1(
   if (lane < GV1_RW && m0 + lane < M) y[m0 + lane] = acc;
 }
 
+// One fp32 row x[0, K) quantized per group of 128 into LDS by a whole block
+// of GV1_WAVES waves, the arithmetic of k_act_quant_i8 (ScalesMax + Quantize,
+// tools/cmdlist/kernels.cpp:551-579): thread l takes elements 1024 j + 4 l +
+// [0, 4), so each half-wave covers one group and its max is a 32-lane
+// reduction (max is exact: the order does not matter).  K <= 4096.  The
+// loads (quant_row_load) are issued before the weight loads, so the
+// quantization (quant_row_lds) waits for them alone.
+struct QRow {
+  float4 v[4];
+};
+__device__ __forceinline__ QRow quant_row_load(const float *__restrict__ x, int K) {
+  static_assert(GV1_WAVES == 4, "a block of 256 threads covers 1024 elements per step");
+  QRow r;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = 1024 * j + 4 * (int)threadIdx.x;
+    r.v[j] = e < K ? *(const float4 *)(x + e) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  return r;
+}
+__device__ __forceinline__ void quant_row_lds(const QRow &r, int K, int8_t *q, float *sq) {
+  const int lid = threadIdx.x;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = 1024 * j + 4 * lid;
+    if (1024 * j >= K) break;
+    const float vv[4] = {r.v[j].x, r.v[j].y, r.v[j].z, r.v[j].w};
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float a = fabsf(vv[i]);
+      m = a > m ? a : m;
+    }
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1)
+      m = __uint_as_float(max(__float_as_uint(m), (uint32_t)__shfl_xor((int)__float_as_uint(m), o, 64)));
+    float sc = m / 127.0f;
+    sc = sc == 0.0f ? 1.0f : sc;
+    uint32_t packed = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float rr = vv[i] / sc;
+      int qi = (int)(rr >= 0.0f ? rr + 0.5f : rr - 0.5f);
+      qi = qi < -127 ? -127 : (qi > 127 ? 127 : qi);
+      packed |= (uint32_t)(uint8_t)(int8_t)qi << (8 * i);
+    }
+    if (e < K) {
+      *(uint32_t *)(q + e) = packed;
+      if ((lid & 31) == 0) sq[e >> 7] = sc;
+    }
+  }
+}
+
 // The layer's expert GEMVs at T = 1 (every dispatch tile holds one token):
 // grid (ceil(N / (GV1_WAVES * GV1_RW)), tiles), the rows of gemv1_rows.
 //   MODE 0: act[pos][n] = silu(gate . x) * (up . x), fp32 (SiluMul,
 //           tools/cmdlist/kernels.cpp:29-37);
 //   MODE 1: o[pos][h] = down . act.
-template <int SD, int MODE, int NC>
+template <int SD, int MODE, int NC, bool QIN = false>
 __global__ __launch_bounds__(GV1_WAVES * 64) void k_w4a8_expert_t1(W4A8Args a) {
   constexpr int NMAT = MODE == 0 ? 2 : 1;
   __shared__ float term[GV1_WAVES][NMAT * GV1_RW * NC * 16];
+  // QIN: the block's own int8 copy of its fp32 activation row
+  __shared__ __attribute__((aligned(16))) int8_t q_l[QIN ? 4096 : 16];
+  __shared__ float sq_l[QIN ? 32 : 1];
   if ((int)blockIdx.y >= *a.n_tiles) return;
   const int4 t = a.tiles[blockIdx.y];
   const int e = t.x, pos0 = t.y;
@@ -363,7 +425,9 @@ __global__ __launch_bounds__(GV1_WAVES * 64) void k_w4a8_expert_t1(W4A8Args a) {
   const int tx = tid_opaque();
   const int wave = __builtin_amdgcn_readfirstlane(tx >> 6), lane = tx & 63;
   const int m0 = (blockIdx.x * GV1_WAVES + wave) * GV1_RW;
-  if (m0 >= N) return;
+  // (QIN: every wave of the block takes part in the quantization; the host
+  // keeps N a multiple of the block's rows there)
+  if (!QIN && m0 >= N) return;
   const size_t rowb = (size_t)K / 2, G = K / 128;
   if constexpr (MODE == 0) {
     const int tok = shared ? pos0 : a.ptok[pos0];
@@ -380,9 +444,18 @@ __global__ __launch_bounds__(GV1_WAVES * 64) void k_w4a8_expert_t1(W4A8Args a) {
   } else {
     const uint8_t *const Pm[1] = {shared ? a.ws0 : a.w0 + (size_t)e * N * rowb};
     const uint16_t *const Sm[1] = {shared ? a.ss0 : a.s0 + (size_t)e * N * G};
-    const int8_t *aq = (shared ? a.aq_s : a.aq) + (size_t)pos0 * K;
-    const float *as = (shared ? a.as_s : a.as) + (size_t)pos0 * G;
-    const float v = gemv1_rows<SD, NC, 1>(Pm, Sm, m0, N, K, aq, as, term[wave], lane);
+    float v;
+    if constexpr (QIN) {
+      const QRow xr = quant_row_load((shared ? a.act_s : a.act) + (size_t)pos0 * K, K);
+      v = gemv1_rows<SD, NC, 1>(Pm, Sm, m0, N, K, q_l, sq_l, term[wave], lane, [&]() {
+        quant_row_lds(xr, K, q_l, sq_l);
+        __syncthreads();
+      });
+    } else {
+      const int8_t *aq = (shared ? a.aq_s : a.aq) + (size_t)pos0 * K;
+      const float *as = (shared ? a.as_s : a.as) + (size_t)pos0 * G;
+      v = gemv1_rows<SD, NC, 1>(Pm, Sm, m0, N, K, aq, as, term[wave], lane);
+    }
     if (lane < GV1_RW && m0 + lane < N)
       a.o[(size_t)((shared ? a.T * a.k : 0) + pos0) * N + m0 + lane] = v;
   }
@@ -497,10 +570,21 @@ hipError_t launch_w4a8_expert(int mode, int scale_dtype, const W4A8Args &a, int 
     // one token per tile: the wide one-token rows (gemv1_rows)
     const int nc = (K / 32 + 63) / 64;
     const dim3 g1((N + GV1_WAVES * GV1_RW - 1) / (GV1_WAVES * GV1_RW), max_tiles);
+    // the in-kernel quantization needs whole blocks of rows and K <= 4096
+    const bool qin = mode == 1 && a.quant_in && a.H % (GV1_WAVES * GV1_RW) == 0 && K <= 4096;
+    if (mode == 1 && a.quant_in && !qin) {
+      hipError_t e = launch_act_quant_f32_pair(a.act, a.T * a.k, a.I, const_cast<int8_t *>(a.aq),
+                                               const_cast<float *>(a.as), a.Is > 0 ? a.act_s : nullptr,
+                                               a.T, a.Is, const_cast<int8_t *>(a.aq_s),
+                                               const_cast<float *>(a.as_s), s);
+      if (e != hipSuccess) return e;
+    }
     auto go1 = [&](auto sd_c, auto nc_c) {
       constexpr int SDc = decltype(sd_c)::value, NCc = decltype(nc_c)::value;
       if (mode == 0)
         k_w4a8_expert_t1<SDc, 0, NCc><<<g1, GV1_WAVES * 64, 0, s>>>(a);
+      else if (qin)
+        k_w4a8_expert_t1<SDc, 1, NCc, true><<<g1, GV1_WAVES * 64, 0, s>>>(a);
       else
         k_w4a8_expert_t1<SDc, 1, NCc><<<g1, GV1_WAVES * 64, 0, s>>>(a);
     };
@@ -515,6 +599,13 @@ hipError_t launch_w4a8_expert(int mode, int scale_dtype, const W4A8Args &a, int 
     else
       go_nc(std::integral_constant<int, AINFER_SCALE_BF16>());
     return hipGetLastError();
+  }
+  if (mode == 1 && a.quant_in) {
+    hipError_t e = launch_act_quant_f32_pair(a.act, a.T * a.k, a.I, const_cast<int8_t *>(a.aq),
+                                             const_cast<float *>(a.as), a.Is > 0 ? a.act_s : nullptr,
+                                             a.T, a.Is, const_cast<int8_t *>(a.aq_s),
+                                             const_cast<float *>(a.as_s), s);
+    if (e != hipSuccess) return e;
   }
   const dim3 grid((N + 15) / 16, max_tiles);
   const size_t stg = (size_t)16 * (K / 128) * 6;  // staged scales

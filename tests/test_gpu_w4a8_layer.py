@@ -143,3 +143,25 @@ def test_w4a8_shape_rules(torch):
         assert L.lib().ainfer_moe_stack_forward_persistent(
             C.byref(layer.shape), _ptr(stack.table), 2, L.NORM_PLAIN, 1e-6, _ptr(r0), _ptr(out), T,
             _ptr(ws), ws.numel(), _stream(None)) == (L.ERR_SHAPE if T == 1 else L.ERR_TOKENS)
+
+
+@pytest.mark.parametrize("name", ["c1", "c3"])
+def test_w4a8_one_token_equals_batched_rows(torch, name):
+    """At T = 1 the down GEMV blocks quantize act into their LDS themselves;
+    at T = 2 a quantization launch does it.  Tokens are independent and both
+    GEMV forms sum the same terms in group order, so each token's row of a
+    T = 2 call is bit-identical to a T = 1 call on that token."""
+    from ainfer_amd import _lib as L
+    from ainfer_amd.moe import make_input, with_precision
+    base = get_layer(torch, name)
+    layer = with_precision(base, L.PRECISION_W4A8)
+    x = make_input(base.cfg, 2, tag=7800)
+    ws = layer.workspace(2)
+    y2 = torch.empty_like(x)
+    layer.forward(x, y2, ws)
+    for t in range(2):
+        print(f"[case] w4a8 {name} one token {t}", flush=True)
+        y1 = torch.empty_like(x[t:t + 1])
+        layer.forward(x[t:t + 1].contiguous(), y1, ws)
+        torch.cuda.synchronize()
+        assert torch.equal(y1.view(torch.int16), y2[t:t + 1].view(torch.int16)), (name, t)
