@@ -94,18 +94,44 @@ __global__ __launch_bounds__(1024) void k_expert(ExpertArgs a) {
   }
   u32x4 B0[RG][KBW], B1[RG][KBW];
   uint16_t S0[RG][KBW], S1[RG][KBW];
+  // Wide pattern (KBW = 4): a row's KBW * 64 bytes are LPR = 4 KBW lanes of
+  // one global->LDS DMA instruction (16 / KBW rows per instruction instead of
+  // 16 rows x 64 B), which streams from HBM faster; the lanes then read their
+  // MFMA fragments (row m, quarter q of group i) back from LDS.  16-byte
+  // chunk c of row r sits at chunk c ^ (r % LPR): the 16 rows one fragment
+  // read touches at one logical chunk land on distinct bank groups.
+  constexpr int LPR = 4 * KBW, RPI = 64 / LPR, MATS = MODE == 0 ? 2 : 1;
+  constexpr int WROWB = LPR * 16;  // staged bytes per row
+  uint8_t *bst = (uint8_t *)red + (size_t)2 * nw * RG * 256 * sizeof(float) +
+                 (size_t)wave * MATS * RG * 16 * WROWB;
+  if constexpr (KBW >= 4) {
+    const uint32_t bl = (uint32_t)(uintptr_t)bst;
+#pragma unroll
+    for (int mat = 0; mat < MATS; ++mat)
+#pragma unroll
+      for (int g = 0; g < RG; ++g)
+#pragma unroll
+        for (int j = 0; j < KBW; ++j) {
+          const int r = j * RPI + lane / LPR, pc = lane % LPR;
+          const int c = pc ^ (r % LPR);
+          const int n = act ? min(n0 + g * 16 + r, N - 1) : r;
+          const uint8_t *src = (mat ? w1 : w0) + (size_t)n * rowb + (size_t)kb0 * 64 + c * 16;
+          dma16(src, __builtin_amdgcn_readfirstlane(bl + (uint32_t)(((mat * RG + g) * 16 + j * RPI) * WROWB)));
+        }
+  }
 #pragma unroll
   for (int g = 0; g < RG; ++g) {
     const int n = act ? min(n0 + g * 16 + m, N - 1) : m;
     const size_t rb = (size_t)n * rowb + q * 16;
+    if constexpr (KBW < 4) {
 #pragma unroll
-    for (int i = 0; i < KBW; ++i) B0[g][i] = ldg_stream(w0 + rb + (size_t)(kb0 + i) * 64);
-    load_scales<KBW>(s0 + (size_t)n * KB + kb0, S0[g]);
-    if (MODE == 0) {
+      for (int i = 0; i < KBW; ++i) B0[g][i] = ldg_stream(w0 + rb + (size_t)(kb0 + i) * 64);
+      if (MODE == 0)
 #pragma unroll
-      for (int i = 0; i < KBW; ++i) B1[g][i] = ldg_stream(w1 + rb + (size_t)(kb0 + i) * 64);
-      load_scales<KBW>(s1 + (size_t)n * KB + kb0, S1[g]);
+        for (int i = 0; i < KBW; ++i) B1[g][i] = ldg_stream(w1 + rb + (size_t)(kb0 + i) * 64);
     }
+    load_scales<KBW>(s0 + (size_t)n * KB + kb0, S0[g]);
+    if (MODE == 0) load_scales<KBW>(s1 + (size_t)n * KB + kb0, S1[g]);
   }
   u32x4 A[KBW][4];
 #pragma unroll
@@ -114,6 +140,18 @@ __global__ __launch_bounds__(1024) void k_expert(ExpertArgs a) {
     for (int j = 0; j < 4; ++j)
       A[i][j] = buf_load16(arsrc, aoff + (uint32_t)(((kb0 + i) * 128 + q * 32 + j * 8) * 2));
 
+  if constexpr (KBW >= 4) {
+    // this wave's DMA (and every load above) has landed
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int g = 0; g < RG; ++g)
+#pragma unroll
+      for (int i = 0; i < KBW; ++i) {
+        const int pc = (i * 4 + q) ^ (m % LPR);
+        B0[g][i] = *(const u32x4 *)(bst + (size_t)(g * 16 + m) * WROWB + pc * 16);
+        if (MODE == 0) B1[g][i] = *(const u32x4 *)(bst + (size_t)((RG + g) * 16 + m) * WROWB + pc * 16);
+      }
+  }
   // ---- MFMA ---------------------------------------------------------------
   f32x4 tot0[RG], tot1[RG];
 #pragma unroll
@@ -284,6 +322,8 @@ hipError_t launch_expert_stream(int mode, int scale_dtype, ExpertArgs a, int max
   a.n_slabs = (Nmax + 16 * rg * a.WR - 1) / (16 * rg * a.WR);
   const int threads = a.WK * a.WR * 64;
   size_t lds = sizeof(float) * 2 * (size_t)a.WK * a.WR * rg * 256;
+  if (kbw >= 4)  // the wide B staging of k_expert: per wave (mats x RG x 16 rows x KBW * 64 B)
+    lds += (size_t)a.WK * a.WR * (mode == 0 ? 2 : 1) * rg * 16 * kbw * 64;
   if (mt == DEC_MT) {
     // A staging; the K-split partials reuse it when they fit (expert_lds_item, ALIAS)
     lds = (size_t)a.WK * a.WR * item_lds_per_wave(DEC_MT, kbw, rg, mode);
