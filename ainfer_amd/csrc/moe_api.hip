@@ -91,7 +91,7 @@ struct ProfCall {
 struct Layout {
   size_t w8_xq, w8_xs, w8_act, w8_acts, w8_aq, w8_as, w8_aqs, w8_ass, w8_o;
   size_t stack_flags, stack_cap, stack_end;
-  size_t sync, sync_words, slots, tiles2, n_tiles2, logits, sg_logit, idx, w, sg, xperm, chunk_counts, rank, counts, offsets, perm, inv,
+  size_t sync, sync_words, slots, tiles2, n_tiles2, logits, sg_logit, idx, w, sg, xperm, chunk_counts, chunk_masks, rank, counts, offsets, perm, inv,
       ptok, tiles, n_tiles, ticket, act, act_s, o, h, wnorm, xsum, asum, asum_s, total;
 };
 
@@ -139,6 +139,7 @@ Layout layout_of(const ainfer_moe_shape &s, int Tm) {
   L.sg = take(T * 4);
   L.xperm = take(T * H * 2);
   L.chunk_counts = take(nchunks * E * 4);
+  L.chunk_masks = take(nchunks * E * 8);  // right after the counts: zeroed as one range
   L.rank = take(T * k * 4);
   L.counts = take(E * 4);
   L.offsets = take((E + 1) * 4);
@@ -588,12 +589,17 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
                                 at<int32_t>(ws, L.idx), at<float>(ws, L.w), at<float>(ws, L.sg),
                                 at<uint16_t>(ws, L.xperm), T, H, E, k, has_shared,
                                 fused ? &d : nullptr, st));
-  else
+  // prefill (T >= GEMM_MIN_T, unfused dispatch): the selection builds the
+  // dispatch's per-chunk token masks itself, so the dispatch needs no counting launch
+  unsigned long long *cmask =
+      gemm && !fused ? at<unsigned long long>(ws, L.chunk_masks) : nullptr;
+  if (T > EXACT_ROUTER_MAX_T)
     HIP_TRY(launch_router_fast(x, w->router_w, w->router_bias, w->shared_gate_w,
                                at<float>(ws, L.logits), at<float>(ws, L.wnorm),
                                at<int32_t>(ws, L.idx), at<float>(ws, L.w), at<float>(ws, L.sg),
                                at<uint16_t>(ws, L.xperm), gemm ? at<float>(ws, L.xsum) : nullptr,
-                               T, H, E, k, has_shared, fused ? &d : nullptr, st));
+                               T, H, E, k, has_shared, fused ? &d : nullptr, st,
+                               cmask ? at<int32_t>(ws, L.chunk_counts) : nullptr, cmask));
   pc->end(2);
   // prefill: experts with at most SMALL_MT tokens skip the GEMM (a 128-token
   // tile costs about half a full one however few tokens it holds) for one
@@ -601,7 +607,8 @@ int do_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const voi
   if (gemm) d.small_max = GEMM_SMALL_MAX;
   if (!fused)
     HIP_TRY(launch_dispatch(at<int32_t>(ws, L.idx), T, k, E, mt, has_shared,
-                            at<int32_t>(ws, L.chunk_counts), at<int32_t>(ws, L.rank), d, st));
+                            at<int32_t>(ws, L.chunk_counts), at<int32_t>(ws, L.rank), d, st,
+                            cmask));
   pc->end(3);
   HIP_TRY_RC(run_experts(s, w, L, ws, d, T, gemm, st, pc));
   HIP_TRY(combine(d, L));

@@ -665,12 +665,16 @@ __global__ __launch_bounds__(256) void k_router_gemm(const uint16_t *__restrict_
                                                      const float *__restrict__ bias,
                                                      float *__restrict__ approx,
                                                      float *__restrict__ wnorm, int T, int H,
-                                                     int E, int n_mt, int n_nt) {
+                                                     int E, int n_mt, int n_nt,
+                                                     uint32_t *__restrict__ zbuf, int zwords) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int n_items = n_mt * n_nt;
   if ((int)blockIdx.x >= n_items) {
+    // ---- the dispatch counts and masks k_select fills next start at zero --
+    const int nb = (int)gridDim.x - n_items, b = (int)blockIdx.x - n_items;
+    for (int i = b * 256 + tid; i < zwords; i += nb * 256) zbuf[i] = 0u;
     // ---- row norms: wave w takes rows e0 + 4w .. e0 + 4w + 3 -------------
     const int e0 = ((int)blockIdx.x - n_items) * RG_NORM_ROWS + wave * 4;
     for (int r = 0; r < 4; ++r) {
@@ -817,7 +821,8 @@ hipError_t launch_geo(int mode, int scale_dtype, GemmArgs a, int max_tiles, hipS
 }  // namespace
 
 hipError_t launch_router_gemm(const void *x, const void *rw, const float *bias, float *approx,
-                              float *wnorm, int T, int H, int E, hipStream_t s) {
+                              float *wnorm, int T, int H, int E, uint32_t *zbuf, int zwords,
+                              hipStream_t s) {
   if (T <= 0) return hipSuccess;
   if (H % RG_BK) return hipErrorInvalidValue;
   const int n_mt = (T + RG_BM - 1) / RG_BM, n_nt = (E + RG_BN - 1) / RG_BN;
@@ -825,7 +830,8 @@ hipError_t launch_router_gemm(const void *x, const void *rw, const float *bias, 
   const long grid = (long)n_mt * n_nt + n_norm;
   if (grid > 0x7FFFFFFF) return hipErrorInvalidValue;
   k_router_gemm<<<(unsigned)grid, 256, RG_ST * RG_STAGE, s>>>(
-      (const uint16_t *)x, (const uint16_t *)rw, bias, approx, wnorm, T, H, E, n_mt, n_nt);
+      (const uint16_t *)x, (const uint16_t *)rw, bias, approx, wnorm, T, H, E, n_mt, n_nt,
+      zbuf, zbuf ? zwords : 0);
   return hipGetLastError();
 }
 

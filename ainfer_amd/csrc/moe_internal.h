@@ -45,8 +45,11 @@ struct GemmArgs {
   int n_nblk, aslots;         // set by the launcher
 };
 // Prefill router: approximate logits (+ bias) and router row norms, tiled bf16 MFMA GEMM.
+// zbuf: zwords 32-bit words zeroed by the kernel (the dispatch counts and
+// masks the following k_select fills), or null
 hipError_t launch_router_gemm(const void *x, const void *rw, const float *bias, float *approx,
-                              float *wnorm, int T, int H, int E, hipStream_t s);
+                              float *wnorm, int T, int H, int E, uint32_t *zbuf, int zwords,
+                              hipStream_t s);
 hipError_t launch_expert_gemm(int mode, int scale_dtype, GemmArgs a, int max_tiles,
                               hipStream_t s);
 // token-tile height of the prefill GEMM and the T above which it is used
@@ -95,7 +98,8 @@ bool router_supported(int H, int E);
 hipError_t launch_router_fast(const void *x, const void *rw, const float *bias, const void *gw,
                               float *approx, float *wnorm, int32_t *idx, float *w, float *sg,
                               void *xperm, float *xsum, int T, int H, int E, int k,
-                              int has_shared, const DispatchOut *fused, hipStream_t s);
+                              int has_shared, const DispatchOut *fused, hipStream_t s,
+                              int32_t *ccount = nullptr, unsigned long long *cmask = nullptr);
 // Small T: canonical logits of all experts on VALU (k_router_logits), then the
 // same selection without the refine.  logits [T][E], sg_logit [T] out.
 hipError_t launch_router_exact(const void *x, const void *rw, const float *bias, const void *gw,
@@ -104,9 +108,12 @@ hipError_t launch_router_exact(const void *x, const void *rw, const float *bias,
                                const DispatchOut *fused, hipStream_t s);
 // below this many tokens the router computes every logit in the canonical order
 constexpr int EXACT_ROUTER_MAX_T = 16;
+// cmask non-null: the per-(64-token chunk, expert) token masks (and, in
+// chunk_counts, the counts) the router's k_select already built
+// (T >= GEMM_MIN_T), so no counting launch
 hipError_t launch_dispatch(const int32_t *idx, int T, int k, int E, int mt, int has_shared,
                            int32_t *chunk_counts, int32_t *rank, const DispatchOut &ds,
-                           hipStream_t s);
+                           hipStream_t s, const unsigned long long *cmask = nullptr);
 // x in MFMA order (+ its per-128 group sums when xsum is non-null)
 hipError_t launch_xperm(const void *x, void *xperm, float *xsum, int T, int H, hipStream_t s);
 // expert output rows from dispatch-position order to slot order (H % 8 == 0)

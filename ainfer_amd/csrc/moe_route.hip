@@ -422,12 +422,15 @@ __global__ __launch_bounds__(NT) void k_dispatch_scan(int32_t *__restrict__ chun
 __global__ void k_dispatch_place(const int32_t *__restrict__ idx,
                                  const int32_t *__restrict__ rank,
                                  const int32_t *__restrict__ chunk_base, int T, int k, int E,
-                                 DispatchOut ds) {
+                                 DispatchOut ds,
+                                 const unsigned long long *__restrict__ cmask) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= T * k) return;
   const int t = i / k, c = t >> 6;
   const int e = idx[i];
-  const int pos = chunk_base[(size_t)c * E + e] + rank[i];
+  // rank of token t among its chunk's tokens of expert e
+  const int r = cmask ? __popcll(cmask[(size_t)c * E + e] & ((1ull << (t & 63)) - 1ull)) : rank[i];
+  const int pos = chunk_base[(size_t)c * E + e] + r;
   ds.perm[pos] = i;
   if (ds.inv) ds.inv[i] = pos;
   if (ds.ptok) ds.ptok[pos] = t;
@@ -435,10 +438,10 @@ __global__ void k_dispatch_place(const int32_t *__restrict__ idx,
 
 hipError_t launch_dispatch(const int32_t *idx, int T, int k, int E, int mt, int has_shared,
                            int32_t *chunk_counts, int32_t *rank, const DispatchOut &ds,
-                           hipStream_t s) {
+                           hipStream_t s, const unsigned long long *cmask) {
   const int nchunks = (T + 63) / 64;
   if (nchunks > DISPATCH_MAX_CHUNKS) return hipErrorInvalidValue;
-  if (T > 0) {
+  if (T > 0 && !cmask) {
     k_dispatch_count<<<nchunks, 64, sizeof(unsigned long long) * E, s>>>(idx, T, k, E,
                                                                          chunk_counts, rank);
   }
@@ -448,7 +451,7 @@ hipError_t launch_dispatch(const int32_t *idx, int T, int k, int E, int mt, int 
     k_dispatch_scan<1024><<<1, 1024, 0, s>>>(chunk_counts, nchunks, E, T, mt, has_shared, ds);
   if (T > 0) {
     int n = T * k;
-    k_dispatch_place<<<(n + 255) / 256, 256, 0, s>>>(idx, rank, chunk_counts, T, k, E, ds);
+    k_dispatch_place<<<(n + 255) / 256, 256, 0, s>>>(idx, rank, chunk_counts, T, k, E, ds, cmask);
   }
   return hipGetLastError();
 }

@@ -223,7 +223,8 @@ __global__ __launch_bounds__(256) void k_select(const float *__restrict__ approx
                                                 uint16_t *__restrict__ xperm,
                                                 float *__restrict__ xsum, int T, int E,
                                                 int k, int H, int has_shared, DispatchOut ds,
-                                                int fused) {
+                                                int fused, unsigned long long *cmask,
+                                                int32_t *ccount) {
   // candidate lists (fast path only)
   __shared__ int cl[SEL_WAVES][EXACT ? 1 : 1024];
   __shared__ float cv[SEL_WAVES][EXACT ? 1 : 1024];
@@ -383,6 +384,14 @@ __global__ __launch_bounds__(256) void k_select(const float *__restrict__ approx
       if (lane < k) {
         topk_idx[(size_t)t * k + lane] = seli;
         topk_w[(size_t)t * k + lane] = p / sum;
+        // the dispatch's count and token mask of (64-token chunk, expert):
+        // a sum and an OR over the chunk's picks, so the order of the
+        // atomics does not matter (the counts sit just before the masks)
+        if (cmask) {
+          const size_t ce = (size_t)(t >> 6) * E + seli;
+          atomicOr(cmask + ce, 1ull << (t & 63));
+          atomicAdd(ccount + ce, 1);
+        }
       }
       // ---- shared gate --------------------------------------------------
       float g = 1.0f;
@@ -514,10 +523,10 @@ hipError_t launch_select_nv(int ch, unsigned grid, const float *approx, const fl
                             const void *x, const void *rw, const float *bias, const void *gw,
                             int32_t *idx, float *w, float *sg, void *xperm, float *xsum, int T,
                             int E, int k, int H, int has_shared, const DispatchOut &ds, int fused,
-                            hipStream_t s) {
+                            unsigned long long *cmask, int32_t *ccount, hipStream_t s) {
 #define SEL_ARGS                                                                            \
   approx, sgl, wnorm, (const uint16_t *)x, (const uint16_t *)rw, bias, (const uint16_t *)gw, idx, \
-      w, sg, (uint16_t *)xperm, xsum, T, E, k, H, has_shared, ds, fused
+      w, sg, (uint16_t *)xperm, xsum, T, E, k, H, has_shared, ds, fused, cmask, ccount
   switch (ch) {
   case 1: k_select<NV, 1, EXACT, COOP><<<grid, 256, 0, s>>>(SEL_ARGS); break;
   case 2: k_select<NV, 2, EXACT, COOP><<<grid, 256, 0, s>>>(SEL_ARGS); break;
@@ -537,7 +546,8 @@ hipError_t launch_select(const float *approx, const float *sgl, const float *wno
                          const void *x, const void *rw, const float *bias, const void *gw,
                          int32_t *idx, float *w, float *sg, void *xperm, float *xsum, int T,
                          int H, int E, int k, int has_shared, const DispatchOut *fused,
-                         hipStream_t s) {
+                         hipStream_t s, unsigned long long *cmask = nullptr,
+                         int32_t *ccount = nullptr) {
   const int ch = (H / 8 + 63) / 64;  // chunks per lane
   const int chp = ch <= 1 ? 1 : (ch <= 2 ? 2 : (ch <= 4 ? 4 : 8));
   const int nv = (E + 63) / 64;
@@ -551,10 +561,10 @@ hipError_t launch_select(const float *approx, const float *sgl, const float *wno
 #define SEL_CALL(NVV)                                                                          \
   (coop ? launch_select_nv<NVV, EXACT, !EXACT>(chp, g, approx, sgl, wnorm, x, rw, bias, gw, idx, \
                                               w, sg, xperm, xsum, T, E, k, H, has_shared, ds, \
-                                              fz, s)                                          \
+                                              fz, cmask, ccount, s)                           \
         : launch_select_nv<NVV, EXACT, false>(chp, g, approx, sgl, wnorm, x, rw, bias, gw, idx, \
                                               w, sg, xperm, xsum, T, E, k, H, has_shared, ds, \
-                                              fz, s))
+                                              fz, cmask, ccount, s))
   if (nv <= 1) return SEL_CALL(1);
   if (nv <= 2) return SEL_CALL(2);
   if (nv <= 4) return SEL_CALL(4);
@@ -566,14 +576,19 @@ hipError_t launch_select(const float *approx, const float *sgl, const float *wno
 hipError_t launch_router_fast(const void *x, const void *rw, const float *bias, const void *gw,
                               float *approx, float *wnorm, int32_t *idx, float *w, float *sg,
                               void *xperm, float *xsum, int T, int H, int E, int k,
-                              int has_shared, const DispatchOut *fused, hipStream_t s) {
+                              int has_shared, const DispatchOut *fused, hipStream_t s,
+                              int32_t *ccount, unsigned long long *cmask) {
   if (T == 0) return hipSuccess;
   // ---- approximate logits + row norms ------------------------------------
   if (T >= GEMM_MIN_T) {
-    hipError_t err = launch_router_gemm(x, rw, bias, approx, wnorm, T, H, E, s);
+    // (and the chunk counts and masks zeroed: [ccount, cmask end), which
+    // k_select fills for the dispatch)
+    const size_t zb = cmask ? (size_t)((char *)(cmask + (size_t)((T + 63) / 64) * E) - (char *)ccount) : 0;
+    hipError_t err = launch_router_gemm(x, rw, bias, approx, wnorm, T, H, E, (uint32_t *)ccount,
+                                        (int)(zb / 4), s);
     if (err != hipSuccess) return err;
     return launch_select<false>(approx, nullptr, wnorm, x, rw, bias, gw, idx, w, sg, xperm,
-                                xsum, T, H, E, k, has_shared, fused, s);
+                                xsum, T, H, E, k, has_shared, fused, s, cmask, ccount);
   }
   // one 16-token tile per workgroup: more workgroups share the token reads
   // (c3 T=64: 55 -> 44 us against 64-token tiles; the router rows are
