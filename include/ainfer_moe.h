@@ -203,7 +203,9 @@ int ainfer_moe_block_forward(const ainfer_moe_shape *shape,
  * (T > 4, W4A16), the previous layer's combine computes it from the rows it
  * writes (the residual add fused into the next norm, tools/norm/norm.cpp:
  * 30-61), so a layer is one launch shorter.  The table must come from
- * ainfer_moe_stack_prepare in this process (else AINFER_ERR_ARG); workspace:
+ * ainfer_moe_stack_prepare in this process (else AINFER_ERR_ARG; the host
+ * copy, a few hundred bytes per layer, is kept until the process ends or the
+ * same table address is prepared again); workspace:
  * ainfer_moe_stack_workspace_bytes(max_tokens), initialised once with
  * ainfer_moe_workspace_init.
  *
