@@ -93,6 +93,20 @@ constexpr int RD_NB = 2;      // 8-element chunks per lane whose loads are issue
 #ifndef RD_NB1
 #define RD_NB1 8   // chunks in flight at T <= RD_TT1_MAX: a whole row up to H = 4096
 #endif
+// RD_TT1_MAX < T <= RD_W2: two tokens per wave in workgroups of RD_W2 waves
+// with RD_NB2 chunks in flight, so the 2048 units of c4 T=8 spread over all
+// CUs instead of half of them (16-wave workgroups, which T > RD_W2 needs for
+// its one selection wave per token).  c4 T=8 routing stage 13.8 -> 12.2 us
+// per block; one token per wave in 8-wave workgroups: 12.4 us.
+#ifndef RD_W2
+#define RD_W2 8
+#endif
+#ifndef RD_NB2
+#define RD_NB2 4
+#endif
+#ifndef RD_MID_TT
+#define RD_MID_TT 2
+#endif
 static_assert(RD_W1 >= RD_TT1_MAX, "the selection runs one wave per token");
 static_assert(DECODE_NORM_MAX_T <= RD_TT1_MAX, "the folded RMSNorm exists in the TT = 1 form only");
 constexpr int SPIN_MAX = 1 << 20;
@@ -519,18 +533,22 @@ hipError_t launch_route_decode(const void *x, const void *rw, const float *bias,
   a.has_shared = has_shared;
   a.spin = g_spin_max;
   const int nrows = E + (gw ? 1 : 0);
-  const int tt = T <= RD_TT1_MAX ? 1 : 2;
+  const bool mid = T > RD_TT1_MAX && T <= RD_W2;
+  const int tt = T <= RD_TT1_MAX ? 1 : mid ? RD_MID_TT : 2;
   const int units = (nrows + RD_R - 1) / RD_R * ((T + tt - 1) / tt);
-  const int wg = tt == 1 ? RD_W1 : RD_WAVES;
+  const int wg = T <= RD_TT1_MAX ? RD_W1 : mid ? RD_W2 : RD_WAVES;
   a.NR = (units + wg - 1) / wg;
   const unsigned grid = a.NR + 2;  // router units, the selection, the x copy
   const int nv = (E + 63) / 64;
   auto go = [&](auto nv_c) {
     constexpr int NVc = decltype(nv_c)::value;
-    if (tt == 1 && a.norm.on)
+    if (T <= RD_TT1_MAX && a.norm.on)
       k_route_decode<NVc, 1, RD_W1, RD_NB1, true><<<grid, RD_W1 * 64, 0, s>>>(a);
-    else if (tt == 1)
+    else if (T <= RD_TT1_MAX)
       k_route_decode<NVc, 1, RD_W1, RD_NB1, false><<<grid, RD_W1 * 64, 0, s>>>(a);
+    else if (mid)
+      k_route_decode<NVc, RD_MID_TT, RD_W2, RD_MID_TT == 1 ? RD_NB1 : RD_NB2, false>
+          <<<grid, RD_W2 * 64, 0, s>>>(a);
     else
       k_route_decode<NVc, 2, RD_WAVES, RD_NB, false><<<grid, RD_WAVES * 64, 0, s>>>(a);
   };

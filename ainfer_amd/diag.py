@@ -5,7 +5,8 @@
   AINFER_HIPFLAGS=-DAINFER_DECODE_TRACE python -m ainfer_amd._build /tmp/decode_trace.so
   python -m ainfer_amd.diag decode-phases /tmp/decode_trace.so
 
-decode-phases runs 8 blocks of config 4 at T = 1 (block_forward, three steps)
+decode-phases runs 8 blocks of config 4 at T = 1 (or the T given after the
+library path) through the replayed stack, three steps,
 and prints the last block's timeline in microseconds from the routing
 kernel's first workgroup (s_memrealtime stamps per workgroup, moe_decode.hip
 and moe_expert_item.h): the router waves' RMSNorm and dot, the selection's
@@ -54,23 +55,21 @@ def gemm_phases(lib_path, steps=3):
     return out
 
 
-def decode_phases(lib_path, n_layers=8):
+def decode_phases(lib_path, n_layers=8, T=1):
     import numpy as np
     from . import _lib as L
     L.LIB_PATH = Path(lib_path).resolve()
     import torch
-    from .moe import MoeLayer, make_input
+    from .moe import MoeLayer, MoeStack, make_input
     from .synthetic import CONFIGS
     cfg = CONFIGS["c4"]
     layers = [MoeLayer(cfg, layer=i) for i in range(n_layers)]
-    T = 1
-    ws = layers[0].workspace(T)
+    stack = MoeStack(layers)
+    ws = stack.workspace(T)
     x = make_input(cfg, T, tag=5000) * 4
     y = torch.empty_like(x)
     for _ in range(3):
-        layers[0].block_forward(x, y, ws)
-        for ly in layers[1:]:
-            ly.block_forward(y, y, ws)
+        stack.forward(x, y, ws)
     torch.cuda.synchronize()
     lib = L.lib()
     tr = np.zeros((2, 1 << 15, 5), dtype=np.uint64)
@@ -84,28 +83,31 @@ def decode_phases(lib_path, n_layers=8):
     us = lambda v: (v - t0) / 100.0
     rr = r[:nr - 2]
     sel = r[nr - 2]
-    print(f"router waves: RMSNorm done {us(np.median(rr[:, 2])):.2f} (max {us(rr[:, 2].max()):.2f}), "
+    print(f"T={T}: {nr - 2} router workgroups: start max {us(rr[:, 0].max()):.2f}, "
+          f"RMSNorm done {us(np.median(rr[:, 2])):.2f} (max {us(rr[:, 2].max()):.2f}), "
           f"dot done {us(np.median(rr[:, 3])):.2f}, logits stored {us(np.median(rr[:, 1])):.2f} "
           f"(max {us(rr[:, 1].max()):.2f})")
-    print(f"selection: slots seen {us(sel[4]):.2f}, top-k {us(sel[1]):.2f}, weights {us(sel[2]):.2f}, "
-          f"dispatch {us(sel[3]):.2f}")
-    g = ld[0].astype(np.int64)
-    g = g[g[:, 0] > 0]
-    if len(g):
-        print(f"gate/up items ({len(g)}): start {us(np.median(g[:, 0])):.2f}, weights landed "
-              f"{us(np.median(g[:, 1])):.2f} (max {us(g[:, 1].max()):.2f}), written max {us(g[:, 2].max()):.2f}")
+    print(f"selection: start {us(sel[0]):.2f}, slots seen {us(sel[4]):.2f}, top-k {us(sel[1]):.2f}, "
+          f"weights {us(sel[2]):.2f}, dispatch {us(sel[3]):.2f}")
+    # the stand-alone expert kernel (k_expert_lds): MODE 0 gate/up, 1 down
+    for m, name in ((0, "gate/up"), (1, "down")):
+        g = ld[m].astype(np.int64)
+        g = g[g[:, 0] > 0]
+        if len(g) and T > 1 or (m == 0 and len(g)):
+            print(f"{name} items ({len(g)}): start {us(g[:, 0].min()):.2f} - {us(np.median(g[:, 0])):.2f} "
+                  f"(median), weights landed {us(np.median(g[:, 1])):.2f} (max {us(g[:, 1].max()):.2f}), "
+                  f"written max {us(g[:, 2].max()):.2f}")
     d = tr[1].astype(np.int64)
     d = d[(d[:, 0] > 0) & (d[:, 4] == 0)]
-    if len(d):
+    if len(d) and T <= 2:
         print(f"down items ({len(d)}): start {us(np.median(d[:, 0])):.2f}, stores max {us(d[:, 2].max()):.2f}, "
               f"last arrival {us(d[:, 3].max()):.2f}")
-
 
 if __name__ == "__main__":
     if len(sys.argv) >= 3 and sys.argv[1] == "gemm-phases":
         gemm_phases(sys.argv[2])
     elif len(sys.argv) >= 3 and sys.argv[1] == "decode-phases":
-        decode_phases(sys.argv[2])
+        decode_phases(sys.argv[2], T=int(sys.argv[3]) if len(sys.argv) > 3 else 1)
     else:
         print(__doc__)
         sys.exit(2)

@@ -74,7 +74,9 @@ def test_fill_matches_oracle(torch, oracle):
         assert np.array_equal(got.a[n].view(a.dtype) if a.dtype != np.float32 else got.a[n], a), n
 
 
-ROUTE_CASES = [("c0", 1), ("c1", 1), ("c1", 4), ("c1", 16), ("c3", 64), ("c2", 4096)]
+# T = 5 and 8: two tokens per wave in 8-wave routing workgroups; 16: 16-wave workgroups
+ROUTE_CASES = [("c0", 1), ("c1", 1), ("c1", 4), ("c1", 5), ("c1", 8), ("c1", 16), ("c3", 8), ("c3", 64),
+               ("c2", 4096)]
 
 
 @pytest.mark.parametrize("name,T", ROUTE_CASES)
