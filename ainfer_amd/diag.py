@@ -102,6 +102,17 @@ def decode_phases(lib_path, n_layers=8, T=1):
     if len(d) and T <= 2:
         print(f"down items ({len(d)}): start {us(np.median(d[:, 0])):.2f}, stores max {us(d[:, 2].max()):.2f}, "
               f"last arrival {us(d[:, 3].max()):.2f}")
+        # the fused kernel's own item stamps (start, weights landed, partials written)
+        ldd = np.zeros((2, 1 << 14, 3), dtype=np.uint64)
+        if lib.ainfer_debug_land(ldd.ctypes.data_as(C.c_void_p)) == 0:
+            g = ldd[1].astype(np.int64)
+            g = g[(g[:, 0] > 0) & (g[:, 0] >= t0)]
+            if len(g):
+                p = lambda v, q: us(np.percentile(v, q))
+                print(f"down items, weights landed: 10/50/90% {p(g[:, 1], 10):.2f} / {p(g[:, 1], 50):.2f} / "
+                      f"{p(g[:, 1], 90):.2f}, max {us(g[:, 1].max()):.2f}; start 10/50/90% "
+                      f"{p(g[:, 0], 10):.2f} / {p(g[:, 0], 50):.2f} / {p(g[:, 0], 90):.2f}; "
+                      f"written max {us(g[:, 2].max()):.2f}")
 
 if __name__ == "__main__":
     if len(sys.argv) >= 3 and sys.argv[1] == "gemm-phases":
