@@ -1,4 +1,4 @@
-"""The layer entry points enqueue kernels only (no allocation, no host sync,
+"""The layer and stack entry points enqueue kernels only (no allocation, no host sync,
 no memset), so a HIP graph can capture them: the analogue of the
 reference's recorded command lists (tools/decode/decode_l0.cpp:553-677).
 Each replay is checked bit for bit against the eager call, with eager work
@@ -83,3 +83,47 @@ def test_block_forward_graph_replays_match_eager(torch):
         layer.block_forward(r0 * 2, torch.empty_like(r0), ws)
         torch.cuda.synchronize()
     del g
+
+
+@pytest.mark.parametrize("T", [1, 8])
+def test_stack_forward_graph_replays_match_eager(torch, T):
+    """The replayed 3-layer stack (at T = 8 with the next RMSNorm computed in
+    each combine) captured once and replayed: every replay equals the eager
+    call bit for bit."""
+    from ainfer_amd import _lib as L
+    from ainfer_amd.moe import MoeLayer, MoeStack, make_input
+    from ainfer_amd.synthetic import CONFIGS
+    print(f"[case] graph stack c1 x3 T={T}", flush=True)
+    cfg = CONFIGS["c1"]
+    layers = [MoeLayer(cfg, layer=i) for i in range(3)]
+    g0 = torch.Generator().manual_seed(5)
+    norm_ws = [(torch.randn(cfg.hidden, generator=g0) * 0.3 + 0.5).to(torch.bfloat16).cuda()
+               for _ in layers]
+    stack = MoeStack(layers, norm_ws)
+    ws = stack.workspace(T)
+    r0 = (make_input(cfg, T, tag=90 + T) * 2).contiguous()
+    other = (make_input(cfg, T, tag=95 + T) * 2).contiguous()
+    want = torch.empty_like(r0)
+    stack.forward(r0, want, ws, norm_mode=L.NORM_ONE_PLUS)
+    torch.cuda.synchronize()
+    out = torch.empty_like(r0)
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        stack.forward(r0, out, ws, norm_mode=L.NORM_ONE_PLUS, stream=s)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g, stream=s):
+        stack.forward(r0, out, ws, norm_mode=L.NORM_ONE_PLUS, stream=s)
+    scratch = torch.empty_like(r0)
+    for rep in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), want.view(torch.int16)), (T, rep)
+        stack.forward(other, scratch, ws, norm_mode=L.NORM_ONE_PLUS)  # eager work between replays
+        torch.cuda.synchronize()
+    assert layers[0].workspace_check(ws) == L.OK
+    del g, layers, stack
+    torch.cuda.empty_cache()
