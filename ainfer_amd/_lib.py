@@ -32,6 +32,7 @@ EXPORTS = (
     "ainfer_moe_dispatch", "ainfer_moe_experts", "ainfer_moe_combine", "ainfer_moe_rmsnorm", "ainfer_moe_fill",
     "ainfer_moe_act_quant_i8", "ainfer_moe_int4_gemv_i8",
     "ainfer_moe_profile_enable", "ainfer_moe_profile_read", "ainfer_moe_profile_kernel", "ainfer_moe_debug_spin_limit",
+    "ainfer_moe_set_strict",
     "ainfer_moe_mfma_probe", "ainfer_moe_read_probe",
     "ainfer_binfer_open", "ainfer_binfer_close", "ainfer_binfer_error", "ainfer_binfer_moe_info",
     "ainfer_binfer_moe_layer_bytes", "ainfer_binfer_load_moe_layer",
@@ -108,6 +109,7 @@ def lib():
         L.ainfer_binfer_moe_layer_bytes.argtypes = [P, I32]
         L.ainfer_binfer_load_moe_layer.argtypes = [P, I32, P, SZ, wp, C.POINTER(P), P]
         L.ainfer_moe_debug_spin_limit.argtypes = [I32]
+        L.ainfer_moe_set_strict.argtypes = [I32]
         L.ainfer_moe_profile_read.argtypes = [C.POINTER(C.c_float), I32, C.POINTER(I32)]
         for name in EXPORTS:
             if name != "ainfer_binfer_close":

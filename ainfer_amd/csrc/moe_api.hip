@@ -3,6 +3,7 @@
 // down -> combine.  Host code; every device buffer comes from the caller.
 #include <string.h>
 
+#include <atomic>
 #include <map>
 #include <mutex>
 #include <vector>
@@ -797,6 +798,33 @@ int ainfer_moe_workspace_check(const ainfer_moe_shape *s, const void *ws, size_t
   return AINFER_OK;
 }
 
+}  // extern "C"
+
+namespace {
+std::atomic<int> g_strict{0};
+
+// Strict mode: wait for the call's work and report a bounded wait that ran
+// out (the workspace's sticky error word).  rc: the call's own result so far.
+int strict_finish(int rc, const void *ws, void *stream) {
+  if (rc || !g_strict.load() || !ws) return rc;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  HIP_TRY(hipStreamIsCapturing((hipStream_t)stream, &cs));
+  if (cs != hipStreamCaptureStatusNone) return AINFER_OK;
+  HIP_TRY(hipStreamSynchronize((hipStream_t)stream));
+  int32_t err = 0;
+  // the sync region starts the workspace (layout_of: offset 0)
+  HIP_TRY(hipMemcpy(&err, (const int32_t *)ws + SY_ERR, sizeof err, hipMemcpyDeviceToHost));
+  return err ? AINFER_ERR_SYNC : AINFER_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int ainfer_moe_set_strict(int32_t on) {
+  g_strict.store(on ? 1 : 0);
+  return AINFER_OK;
+}
+
 int ainfer_moe_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const void *x,
                        void *y, int32_t T, void *ws, size_t ws_bytes, void *stream) {
   int rc = ainfer_moe_validate(s);
@@ -814,7 +842,7 @@ int ainfer_moe_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w, c
                          chunk_of(T - t0), ws, (hipStream_t)stream, &pc)))
       return rc;
   }
-  return AINFER_OK;
+  return strict_finish(AINFER_OK, ws, stream);
 }
 
 int ainfer_moe_block_forward(const ainfer_moe_shape *s, const ainfer_moe_weights *w,
@@ -829,7 +857,7 @@ int ainfer_moe_block_forward(const ainfer_moe_shape *s, const ainfer_moe_weights
     if ((rc = do_block(s, w, norm_w, norm_mode, eps, (const char *)resid_in + t0 * row,
                        (char *)resid_out + t0 * row, chunk_of(T - t0), ws, (hipStream_t)stream)))
       return rc;
-  return AINFER_OK;
+  return strict_finish(AINFER_OK, ws, stream);
 }
 
 int ainfer_moe_block_forward_noalloc(const ainfer_moe_shape *s, const ainfer_moe_weights *w,
@@ -853,7 +881,7 @@ int ainfer_moe_block_forward_noalloc(const ainfer_moe_shape *s, const ainfer_moe
     if ((rc = do_block(s, w, norm_w, norm_mode, eps, (const char *)resid_in + t0 * row,
                        (char *)resid_out + t0 * row, chunk_of(T - t0), ws, st)))
       return rc;
-  return AINFER_OK;
+  return strict_finish(AINFER_OK, ws, stream);
 }
 
 size_t ainfer_moe_stack_table_bytes(int32_t n_layers) {
@@ -980,7 +1008,7 @@ int ainfer_moe_stack_forward(const ainfer_moe_shape *s, const void *table, int32
     if ((rc = do_stack(s, ly, n_layers, norm_mode, eps, (const char *)resid_in + t0 * row,
                        (char *)resid_out + t0 * row, chunk_of(T - t0), ws, (hipStream_t)stream)))
       return rc;
-  return AINFER_OK;
+  return strict_finish(AINFER_OK, ws, stream);
 }
 
 int ainfer_moe_stack_forward_persistent(const ainfer_moe_shape *s, const void *table,
@@ -1004,7 +1032,7 @@ int ainfer_moe_stack_forward_persistent(const ainfer_moe_shape *s, const void *t
   w.err = at<int32_t>(ws, L.sync) + SY_ERR;
   HIP_TRY(launch_decode_stack(s->scale_dtype, *s, g, (const StackLayer *)table, n_layers,
                               resid_in, resid_out, T, norm_mode, eps, w, (hipStream_t)stream));
-  return AINFER_OK;
+  return strict_finish(AINFER_OK, ws, stream);
 }
 
 int ainfer_moe_route(const ainfer_moe_shape *s, const ainfer_moe_weights *w, const void *x,

@@ -396,6 +396,17 @@ int ainfer_moe_int4_gemv_i8(const uint8_t *packed, const void *scales,
  * kernel still exits normally.  Process-wide; no reference counterpart. */
 int ainfer_moe_debug_spin_limit(int32_t polls);
 
+/* Strict mode (process-wide, off by default; no reference counterpart): when
+ * on, ainfer_moe_forward, _block_forward, _block_forward_noalloc,
+ * _stack_forward and _stack_forward_persistent wait for the stream after
+ * enqueueing their work and return AINFER_ERR_SYNC when a bounded device-side
+ * wait of the call (or of an earlier call on the same workspace, whose error
+ * word is sticky until ainfer_moe_workspace_init) ran out, instead of
+ * AINFER_OK with NaN rows.  For validation runs and callers that read the
+ * result at once anyway; it costs a host round trip per call.  Under HIP
+ * graph capture the check is skipped (nothing can be waited for there). */
+int ainfer_moe_set_strict(int32_t on);
+
 /* ---- synthetic data (counter-based, bit-identical to the CPU oracle) --- */
 enum {
   AINFER_FILL_BYTES = 0,      /* uniform random bytes (packed int4 weights)  */
