@@ -26,7 +26,7 @@ def torch():
     return torch
 
 
-CASES = [("c0", 1), ("c0", 5), ("c1", 1), ("c1", 4), ("c1", 16), ("c1", 300), ("c2", 4096),
+CASES = [("c0", 1), ("c0", 5), ("c1", 1), ("c1", 4), ("c1", 8), ("c1", 16), ("c1", 300), ("c2", 4096),
          ("c3", 1), ("c3", 2)]
 
 
